@@ -1,0 +1,100 @@
+/*
+ * C-ABI of the MI355X (gfx950) quantized-weight matmul library
+ * (libvllm_mi355x.so): EXL3 trellis-coded linear layers and the
+ * Marlin-layout int4 fused MoE.
+ *
+ * Every entry point takes plain device pointers, sizes, dtype codes and a
+ * HIP stream (hipStream_t passed as void*; NULL = the default stream), runs
+ * asynchronously on that stream, never allocates, never synchronizes, and
+ * returns a status code.  On a nonzero status vllm_mi355x_last_error()
+ * returns the message (thread-local), worded as the reference's TORCH_CHECK
+ * messages are.  All buffers are caller-owned; only `out` and `workspace`
+ * arguments are written.
+ *
+ * Reference interfaces replaced (paths relative to the reference repo):
+ *   _exl3_C schema ..................... csrc/exl3/module.cpp:12-67
+ *   _ampere_marlin_C schema ............ csrc/ampere_marlin/decode_orig.cu:403-411
+ */
+#ifndef VLLM_MI355X_H
+#define VLLM_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VLLM_MI355X_ABI_VERSION 1
+
+/* Status codes. */
+#define VQ_OK 0
+#define VQ_INVALID_ARGUMENT 1 /* a check failed; see vllm_mi355x_last_error() */
+#define VQ_HIP_FAILURE 2      /* a launch failed */
+
+/* Element types of activations and outputs. */
+#define VQ_BF16 0
+#define VQ_FP16 1
+#define VQ_FP32 2
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* vllm_mi355x_last_error(void);
+/* VLLM_MI355X_ABI_VERSION of the loaded library. */
+int vllm_mi355x_abi_version(void);
+
+/* ---- EXL3 ---------------------------------------------------------------- */
+
+/*
+ * FP32 workspace elements exl3_linear_out needs for up to max_rows rows of
+ * a padded_in x padded_out matrix: max_rows * (padded_in + padded_out) plus
+ * min(max_rows, 8) * ceil(padded_in / 512) * padded_out for the K-split
+ * partial sums of the small-M kernel.  Returns -1 (with an error message)
+ * for a negative row count or padded sizes that are not positive multiples
+ * of 128.
+ * Replaces _exl3_C::linear_workspace_size (csrc/exl3/dense.cu:72-78).
+ */
+int64_t exl3_linear_workspace_size(int64_t max_rows, int64_t padded_in, int64_t padded_out);
+
+/*
+ * out[r][n] = RN_out( H128(C[r])[n] * svh[n] ),
+ * C[r][n]   = sum_k t[r][k] * W[k][n],  t[r] = H128(x[r] * suh)  (FP32),
+ * with W the exact FP16 weights decoded from the trellis, H128 the
+ * normalized Sylvester Hadamard transform over 128-element blocks.
+ *
+ *   x        [rows][logical_in] of x_dtype (VQ_BF16 or VQ_FP16)
+ *   trellis  int16 [tiles_k][tiles_n][trellis_words], trellis_words must be
+ *            8 * bits_x2; padded_in = 16 * tiles_k, padded_out = 16 * tiles_n
+ *   suh      fp16 [suh_numel == padded_in], svh fp16 [svh_numel == padded_out]
+ *   bits_x2  2..16 with codebook 1 (mcg, even rates) or 2 (mul1, also 3/5/7)
+ *   out      [rows][logical_out] of out_dtype (VQ_BF16, VQ_FP16 or VQ_FP32)
+ *   workspace FP32, >= exl3_linear_workspace_size(rows, ...) elements,
+ *            16-byte aligned, overlapping no other argument.
+ * The weights are decoded bit-exactly; the products are summed in FP32 on
+ * the matrix cores, with the activations split into FP16 high and low parts
+ * (about 22 significant bits), so the result agrees with the reference's
+ * sequential FP32 chain to FP32 rounding, not bit for bit.
+ * Replaces _exl3_C::linear_out (csrc/exl3/dense.cu:80-149; schema
+ * csrc/exl3/module.cpp:13-15).
+ */
+int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t x_cols,
+                    const void* trellis, int64_t tiles_k, int64_t tiles_n,
+                    int64_t trellis_words, const void* suh, int64_t suh_numel,
+                    const void* svh, int64_t svh_numel, int64_t bits_x2,
+                    int64_t codebook, int64_t logical_in, int64_t logical_out,
+                    void* out, int out_dtype, int64_t out_rows, int64_t out_cols,
+                    float* workspace, int64_t workspace_numel, void* stream);
+
+/*
+ * Decodes every tile of a trellis into its exact FP16 weights,
+ * out[k][n] (k < 16 * tiles_k, n < 16 * tiles_n, row-major, FP16 bits).
+ * The inspection form of the decode exl3_linear_out fuses; it has no
+ * operator of its own in the reference, whose decode is
+ * csrc/exl3/reference.cu:62-103 (core_value) / csrc/exl3/codec.cuh:45-180.
+ */
+int exl3_decode(const void* trellis, int64_t tiles_k, int64_t tiles_n, int64_t trellis_words,
+                int64_t bits_x2, int64_t codebook, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLLM_MI355X_H */

@@ -1,0 +1,142 @@
+"""EXL3 dense path on the GPU, through the _exl3_C operators and the C-ABI,
+against the CPU oracle (oracle/exl3_oracle.c, the reference's scalar
+operators restated).
+
+Bars:
+  * decoded weights: bit-exact (every format, aligned and unaligned bases);
+  * linear_out: the oracle computes the reference's exact FP32 chain; the
+    GPU sums on the matrix cores in another order with the activations split
+    into FP16 high/low parts, so FP32 outputs must agree to
+    |err| <= 2^-14 * rms(ref) + 2^-16 * |ref| (a few FP32 roundings of a
+    K-term sum; a wrong decode or index is off by O(rms)), and BF16 outputs
+    within one BF16 rounding: |err| <= 2^-8 |ref| + 2^-14 rms(ref).
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exl3_oracle as O
+from tests.exl3_cases import FORMATS, random_acts, random_matrix
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from vllm_mi355x.kernels.exl3 import ops as exl3_ops
+    exl3_ops.ensure_extension()
+    return exl3_ops
+
+
+def _dev(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def _to_torch_act(a: np.ndarray, code: int, device):
+    t = _dev(a, device)
+    return t.view(torch.bfloat16) if code == O.BF16 else t
+
+
+def _out_np(t: torch.Tensor) -> np.ndarray:
+    if t.dtype == torch.bfloat16:
+        return O.bf16_bits_to_f32(t.view(torch.int16).cpu().numpy().view(np.uint16))
+    return t.float().cpu().numpy()
+
+
+def _oracle_f32(out, code):
+    return O.bf16_bits_to_f32(out) if code == O.BF16 else out.astype(np.float32)
+
+
+def _assert_fp32_close(actual, expected, name):
+    rms = float(np.sqrt(np.mean(expected.astype(np.float64) ** 2)))
+    err = np.abs(actual.astype(np.float64) - expected)
+    bound = 2.0 ** -14 * rms + 2.0 ** -16 * np.abs(expected)
+    worst = int(np.argmax(err - bound))
+    assert (err <= bound).all(), f"{name}: err {err.flat[worst]:.3g} > {bound.flat[worst]:.3g} (rms {rms:.3g})"
+
+
+def _assert_round_close(actual, expected, name):
+    rms = float(np.sqrt(np.mean(expected.astype(np.float64) ** 2)))
+    err = np.abs(actual.astype(np.float64) - expected)
+    bound = 2.0 ** -8 * np.abs(expected) + 2.0 ** -14 * rms
+    worst = int(np.argmax(err - bound))
+    assert (err <= bound).all(), f"{name}: err {err.flat[worst]:.3g} > {bound.flat[worst]:.3g}"
+
+
+@pytest.mark.parametrize("bits_x2,codebook", FORMATS)
+@pytest.mark.parametrize("aligned", [True, False])
+def test_decode_bit_exact(ops, device, bits_x2, codebook, aligned):
+    print(f"decode bits_x2={bits_x2} codebook={codebook} aligned={aligned}", flush=True)
+    rng = np.random.default_rng(100 * bits_x2 + codebook)
+    trellis, _, _ = random_matrix(rng, 256, 384, bits_x2)
+    expected = O.decode(trellis, bits_x2, codebook).view(np.uint16)
+    t = _dev(trellis, device)
+    if not aligned:
+        # a base two bytes past a 4-byte boundary
+        flat = torch.empty(trellis.size + 1, dtype=torch.int16, device=device)
+        flat[1:] = t.reshape(-1)
+        t = flat[1:].view(trellis.shape)
+        assert t.data_ptr() % 4 == 2
+    got = ops.decode(t, bits_x2, codebook).view(torch.int16).cpu().numpy().view(np.uint16)
+    mismatch = np.argwhere(got != expected)
+    assert mismatch.size == 0, f"{len(mismatch)} mismatches, first at {mismatch[0]}"
+
+
+def _run_linear(ops, device, trellis, suh, svh, x, x_code, bits_x2, codebook, logical_out,
+                out_dtype):
+    rows = x.shape[0]
+    out = torch.empty(rows, logical_out, dtype=out_dtype, device=device)
+    ws = torch.empty(ops.linear_workspace_size(rows, suh.size, svh.size), dtype=torch.float32,
+                     device=device)
+    ops.linear_out(_to_torch_act(x, x_code, device), _dev(trellis, device), _dev(suh, device),
+                   _dev(svh, device), bits_x2, codebook, x.shape[1], logical_out, out, ws)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("bits_x2,codebook", FORMATS)
+@pytest.mark.parametrize("rows", [1, 3, 8, 17])
+def test_linear_matches_oracle(ops, device, bits_x2, codebook, rows):
+    print(f"linear bits_x2={bits_x2} codebook={codebook} rows={rows}", flush=True)
+    rng = np.random.default_rng(1000 * bits_x2 + 10 * codebook + rows)
+    # logical sizes below the padded H128 blocks exercise both crops
+    trellis, suh, svh = random_matrix(rng, 256, 384, bits_x2, scales="test")
+    logical_in, logical_out = 250, 300
+    x, code = random_acts(rng, rows, logical_in, "bf16")
+    got = _run_linear(ops, device, trellis, suh, svh, x, code, bits_x2, codebook, logical_out,
+                      torch.float32)
+    want = O.linear_out(x, code, trellis, suh, svh, bits_x2, codebook, logical_out, O.FP32)
+    _assert_fp32_close(_out_np(got), want, f"bits_x2={bits_x2} cb={codebook} rows={rows}")
+    got_bf = _run_linear(ops, device, trellis, suh, svh, x, code, bits_x2, codebook, logical_out,
+                         torch.bfloat16)
+    want_bf = O.linear_out(x, code, trellis, suh, svh, bits_x2, codebook, logical_out, O.BF16)
+    _assert_round_close(_out_np(got_bf), O.bf16_bits_to_f32(want_bf), "bf16 out")
+
+
+@pytest.mark.parametrize("shape", [(4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("bits_x2", [4, 6, 8])
+@pytest.mark.parametrize("rows", [1, 4, 8])
+def test_linear_benchmark_shapes(ops, device, shape, bits_x2, rows):
+    """The GEMV benchmark shapes (fp16 activations, mul1, sign scales)."""
+    print(f"linear shape={shape} bits_x2={bits_x2} rows={rows}", flush=True)
+    k, n = shape
+    rng = np.random.default_rng(7 * k + n + bits_x2 + rows)
+    trellis, suh, svh = random_matrix(rng, k, n, bits_x2)
+    x, code = random_acts(rng, rows, k, "fp16")
+    got = _run_linear(ops, device, trellis, suh, svh, x, code, bits_x2, 2, n, torch.float32)
+    want = O.linear_out(x, code, trellis, suh, svh, bits_x2, 2, n, O.FP32)
+    _assert_fp32_close(_out_np(got), want, f"{shape} bits_x2={bits_x2} rows={rows}")
+
+
+def test_linear_rejects_small_workspace(ops, device):
+    rng = np.random.default_rng(0)
+    trellis, suh, svh = random_matrix(rng, 128, 128, 8)
+    x = torch.zeros(2, 128, dtype=torch.bfloat16, device=device)
+    out = torch.empty(2, 128, dtype=torch.bfloat16, device=device)
+    ws = torch.empty(ops.linear_workspace_size(2, 128, 128) - 1, dtype=torch.float32, device=device)
+    with pytest.raises(RuntimeError, match="workspace is too small"):
+        ops.linear_out(x, _dev(trellis, device), _dev(suh, device), _dev(svh, device), 8, 2, 128,
+                       128, out, ws)

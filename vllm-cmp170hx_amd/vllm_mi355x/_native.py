@@ -1,0 +1,84 @@
+"""ctypes binding of libvllm_mi355x.so, the C-ABI library of the hand-written
+gfx950 kernels (declared in include/vllm_mi355x.h).
+
+There is no fallback: if the library is missing or fails to load, every
+operator raises.  Build it with ``python vllm-cmp170hx_amd/build.py``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIBRARY_NAME = "libvllm_mi355x.so"
+LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
+ABI_VERSION = 1
+
+BF16, FP16, FP32 = 0, 1, 2
+OK = 0
+
+c_i64 = ctypes.c_int64
+c_int = ctypes.c_int
+c_vp = ctypes.c_void_p
+
+# name -> (restype, argtypes), mirroring include/vllm_mi355x.h
+SIGNATURES = {
+    "vllm_mi355x_last_error": (ctypes.c_char_p, []),
+    "vllm_mi355x_abi_version": (c_int, []),
+    "exl3_linear_workspace_size": (c_i64, [c_i64, c_i64, c_i64]),
+    "exl3_linear_out": (c_int, [
+        c_vp, c_int, c_i64, c_i64,            # x, x_dtype, rows, x_cols
+        c_vp, c_i64, c_i64, c_i64,            # trellis, tiles_k, tiles_n, trellis_words
+        c_vp, c_i64, c_vp, c_i64,             # suh, suh_numel, svh, svh_numel
+        c_i64, c_i64, c_i64, c_i64,           # bits_x2, codebook, logical_in, logical_out
+        c_vp, c_int, c_i64, c_i64,            # out, out_dtype, out_rows, out_cols
+        c_vp, c_i64, c_vp,                    # workspace, workspace_numel, stream
+    ]),
+    "exl3_decode": (c_int, [c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NativeError(RuntimeError):
+    """A check of the native library failed (the reference raises
+    RuntimeError from TORCH_CHECK for the same conditions)."""
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library; raises if it is missing or of another ABI."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIBRARY_PATH):
+            raise ImportError(
+                f"{LIBRARY_NAME} is not built ({LIBRARY_PATH} is missing): run "
+                "python vllm-cmp170hx_amd/build.py")
+        lib = ctypes.CDLL(LIBRARY_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.vllm_mi355x_abi_version()
+        if version != ABI_VERSION:
+            raise ImportError(f"{LIBRARY_NAME} ABI {version}, expected {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().vllm_mi355x_last_error().decode("utf-8", "replace")
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise NativeError(last_error())
+
+
+def exported_symbols() -> list[str]:
+    return list(SIGNATURES)

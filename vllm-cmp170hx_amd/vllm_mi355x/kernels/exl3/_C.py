@@ -1,0 +1,141 @@
+"""The ``_exl3_C`` operator library on ROCm: the reference's schemas
+(csrc/exl3/module.cpp:12-67), each CUDA kernel implemented by a call into
+libvllm_mi355x.so with the tensors' device pointers on torch's current
+stream.  Tensor-level checks (device, dtype, contiguity, rank) are made here
+with the reference's messages (csrc/exl3/common.h:42-61, dense.cu:85-93);
+geometry, workspace and overlap checks are made by the native library.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ... import _native
+
+_DTYPE_CODES = {torch.bfloat16: _native.BF16, torch.float16: _native.FP16,
+                torch.float32: _native.FP32}
+
+# Bumped with the reference's own meaning (module.cpp:86-88): 3 = moe_out_v2
+# takes bits_x2, 2 = the MoE operators take swiglu_limit.
+ABI_VERSION = 3
+
+SCHEMAS = {
+    "linear_out": (
+        "linear_out(Tensor x, Tensor trellis, Tensor suh, Tensor svh, "
+        "int bits_x2, int codebook, int logical_in, int logical_out, "
+        "Tensor(a!) out, Tensor(b!) workspace) -> ()"),
+    "linear_out_splitk": (
+        "linear_out_splitk(Tensor x, Tensor trellis, Tensor suh, Tensor svh, "
+        "int bits_x2, int codebook, int logical_in, int logical_out, "
+        "Tensor(a!) out, Tensor(b!) workspace) -> ()"),
+    "linear_workspace_size": (
+        "linear_workspace_size(int max_rows, int padded_in, int padded_out) -> int"),
+    "linear_splitk_splits": (
+        "linear_splitk_splits(int rows, int padded_out, int sms, int bits_x2, "
+        "int codebook) -> int"),
+    "exl3_decode": (
+        "exl3_decode(Tensor trellis, int bits_x2, int codebook, Tensor(a!) out) -> ()"),
+}
+
+_library = None
+
+
+def _check_tensor(t: torch.Tensor, x: torch.Tensor, dtypes, name: str) -> None:
+    if not (t.is_cuda and t.device == x.device):
+        raise RuntimeError(f"{name} must be on the input CUDA device")
+    if t.dtype not in dtypes:
+        raise RuntimeError(f"{name} has incorrect dtype")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def linear_out_impl(x, trellis, suh, svh, bits_x2, codebook, logical_in, logical_out, out,
+                    workspace) -> None:
+    if not x.is_cuda:
+        raise RuntimeError("EXL3 x must be CUDA")
+    _check_tensor(x, x, (torch.bfloat16, torch.float16), "x")
+    _check_tensor(trellis, x, (torch.int16,), "trellis")
+    _check_tensor(suh, x, (torch.float16,), "suh")
+    _check_tensor(svh, x, (torch.float16,), "svh")
+    if out.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise RuntimeError("EXL3 linear out must be BF16, FP16 or FP32")
+    _check_tensor(out, x, (out.dtype,), "out")
+    _check_tensor(workspace, x, (torch.float32,), "workspace")
+    if not (x.dim() == 2 and trellis.dim() == 3 and suh.dim() == 1 and svh.dim() == 1
+            and out.dim() == 2):
+        raise RuntimeError(
+            "EXL3 linear requires rank-2 x/out, rank-3 trellis and rank-1 scales")
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        status = lib.exl3_linear_out(
+            x.data_ptr(), _DTYPE_CODES[x.dtype], x.size(0), x.size(1),
+            trellis.data_ptr(), trellis.size(0), trellis.size(1), trellis.size(2),
+            suh.data_ptr(), suh.numel(), svh.data_ptr(), svh.numel(),
+            int(bits_x2), int(codebook), int(logical_in), int(logical_out),
+            out.data_ptr(), _DTYPE_CODES[out.dtype], out.size(0), out.size(1),
+            workspace.data_ptr(), workspace.numel(), _stream(x.device))
+    _native.check(status)
+
+
+def linear_workspace_size_impl(max_rows, padded_in, padded_out) -> int:
+    size = _native.load().exl3_linear_workspace_size(max_rows, padded_in, padded_out)
+    if size < 0:
+        raise RuntimeError(_native.last_error())
+    return int(size)
+
+
+def linear_splitk_splits_impl(rows, padded_out, sms, bits_x2, codebook) -> int:
+    # One operator serves both entry points here: linear_out_splitk runs the
+    # linear_out kernels (its contract: same arguments, checks, workspace).
+    return 1
+
+
+def decode_impl(trellis, bits_x2, codebook, out) -> None:
+    if not trellis.is_cuda:
+        raise RuntimeError("EXL3 trellis must be CUDA")
+    _check_tensor(trellis, trellis, (torch.int16,), "trellis")
+    _check_tensor(out, trellis, (torch.float16,), "out")
+    if trellis.dim() != 3 or out.dim() != 2 or out.size(0) != 16 * trellis.size(0) \
+            or out.size(1) != 16 * trellis.size(1):
+        raise RuntimeError("EXL3 decode geometry mismatch")
+    lib = _native.load()
+    with torch.cuda.device(trellis.device):
+        status = lib.exl3_decode(trellis.data_ptr(), trellis.size(0), trellis.size(1),
+                                 trellis.size(2), int(bits_x2), int(codebook), out.data_ptr(),
+                                 _stream(trellis.device))
+    _native.check(status)
+
+
+def build_info() -> dict:
+    """The handshake the reference's loader compares (module.cpp:91-99);
+    ROCm has no CUDA runtime, so cuda_version is 0 and hip_version is set."""
+    hip = torch.version.hip or "0.0"
+    major, minor = (int(v) for v in hip.split(".")[:2])
+    return {
+        "abi_version": ABI_VERSION,
+        "torch_version": torch.__version__.split("+")[0],
+        "cuda_version": 0,
+        "hip_version": major * 1000 + minor * 10,
+        "cxx11_abi": int(torch._C._GLIBCXX_USE_CXX11_ABI),
+    }
+
+
+def register() -> None:
+    """Defines the _exl3_C operators once per process."""
+    global _library
+    if _library is not None:
+        return
+    _native.load()
+    lib = torch.library.Library("_exl3_C", "DEF")
+    for schema in SCHEMAS.values():
+        lib.define(schema)
+    lib.impl("linear_out", linear_out_impl, "CUDA")
+    lib.impl("linear_out_splitk", linear_out_impl, "CUDA")
+    lib.impl("exl3_decode", decode_impl, "CUDA")
+    lib.impl("linear_workspace_size", linear_workspace_size_impl, "CompositeImplicitAutograd")
+    lib.impl("linear_splitk_splits", linear_splitk_splits_impl, "CompositeImplicitAutograd")
+    _library = lib

@@ -1,0 +1,146 @@
+"""EXL3 operator bindings with the reference's Python API
+(vllm_sm80/kernels/exl3/ops.py), on the gfx950 library.
+
+The functions keep the reference's names, arguments, return values and
+error behaviour (RuntimeError for a failed check); the compute runs in
+hand-written HIP kernels behind ``torch.ops._exl3_C``.
+"""
+
+from __future__ import annotations
+
+from functools import lru_cache
+
+import torch
+
+from . import _C
+
+_loaded = False
+
+# One fixed FP32 scratch per (device, stream) for the ``exl3_linear`` custom
+# op; rows are processed in chunks whose workspace fits it
+# (ops.py:31-33, :1431-1452 of the reference).
+LINEAR_SCRATCH_ELEMENTS = 8 << 20
+
+# Output dtypes of the dense linear: BF16 / FP16 round the FP32 result once;
+# FP32 stores it (reference ops.py:114, plus FP16 for FP16 models).
+LINEAR_OUT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+_OPERATORS = ("linear_out", "linear_out_splitk", "linear_workspace_size",
+              "linear_splitk_splits", "exl3_decode")
+
+
+def _linear_fake(x, trellis, suh, svh, bits_x2, codebook, logical_in, logical_out, out,
+                 workspace):
+    torch._check(x.dtype in (torch.bfloat16, torch.float16))
+    torch._check(out.dtype in LINEAR_OUT_DTYPES)
+    torch._check(out.shape[0] == x.shape[0])
+    torch._check(out.shape[1] == logical_out)
+    torch._check(x.shape[1] == logical_in)
+    torch._check(workspace.dtype == torch.float32)
+
+
+def _validate_extension() -> None:
+    built = _C.build_info()
+    if built["abi_version"] != _C.ABI_VERSION:
+        raise ValueError(f"abi_version mismatch: {built['abi_version']} vs {_C.ABI_VERSION}")
+    for name in _OPERATORS:
+        torch._C._dispatch_find_schema_or_throw(f"_exl3_C::{name}", "")
+
+
+def ensure_extension() -> None:
+    """Loads and registers the operators once (reference ops.py:279-308)."""
+    global _loaded
+    if _loaded:
+        return
+    try:
+        _C.register()
+        _validate_extension()
+    except (ImportError, OSError, AttributeError, RuntimeError, ValueError) as exc:
+        raise RuntimeError(
+            "EXL3 requires libvllm_mi355x.so, built for gfx950: build it with "
+            f"python vllm-cmp170hx_amd/build.py. Detail: {exc}") from exc
+    for name in ("linear_out", "linear_out_splitk"):
+        torch.library.register_fake(f"_exl3_C::{name}")(_linear_fake)
+    _loaded = True
+
+
+@lru_cache(maxsize=None)
+def linear_workspace_size(max_rows: int, padded_in: int, padded_out: int) -> int:
+    ensure_extension()
+    return torch.ops._exl3_C.linear_workspace_size(max_rows, padded_in, padded_out)
+
+
+@lru_cache(maxsize=None)
+def linear_row_chunk(padded_in: int, padded_out: int) -> int:
+    """The most rows whose linear workspace fits the fixed scratch."""
+    rows, limit = 0, LINEAR_SCRATCH_ELEMENTS
+    while rows < limit:
+        middle = (rows + limit + 1) // 2
+        if linear_workspace_size(middle, padded_in, padded_out) <= LINEAR_SCRATCH_ELEMENTS:
+            rows = middle
+        else:
+            limit = middle - 1
+    if rows == 0:
+        raise ValueError("One EXL3 matrix row exceeds the fixed linear scratch")
+    return rows
+
+
+def linear_out(x, trellis, suh, svh, bits_x2: int, codebook: int, logical_in: int,
+               logical_out: int, out, workspace) -> None:
+    ensure_extension()
+    torch.ops._exl3_C.linear_out(x, trellis, suh, svh, bits_x2, codebook, logical_in,
+                                 logical_out, out, workspace)
+
+
+def linear_out_splitk(x, trellis, suh, svh, bits_x2: int, codebook: int, logical_in: int,
+                      logical_out: int, out, workspace) -> None:
+    """linear_out's contract (arguments, checks, workspace)."""
+    ensure_extension()
+    torch.ops._exl3_C.linear_out_splitk(x, trellis, suh, svh, bits_x2, codebook, logical_in,
+                                        logical_out, out, workspace)
+
+
+def linear_splitk_splits(rows: int, padded_out: int, sms: int, bits_x2: int,
+                         codebook: int) -> int:
+    ensure_extension()
+    return torch.ops._exl3_C.linear_splitk_splits(rows, padded_out, sms, bits_x2, codebook)
+
+
+def decode(trellis: torch.Tensor, bits_x2: int, codebook: int) -> torch.Tensor:
+    """The exact FP16 weights W [padded_in, padded_out] of a packed matrix."""
+    ensure_extension()
+    out = torch.empty(16 * trellis.shape[0], 16 * trellis.shape[1], dtype=torch.float16,
+                      device=trellis.device)
+    torch.ops._exl3_C.exl3_decode(trellis, bits_x2, codebook, out)
+    return out
+
+
+_scratch: dict = {}
+
+
+def _linear_scratch(device: torch.device) -> torch.Tensor:
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device.index, stream)
+    buf = _scratch.get(key)
+    if buf is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("EXL3 scratch must be allocated before graph capture")
+        buf = torch.empty(LINEAR_SCRATCH_ELEMENTS, dtype=torch.float32, device=device)
+        _scratch[key] = buf
+    return buf
+
+
+def exl3_linear(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+                bits_x2: int, codebook: int, logical_out: int, row_chunk: int | None = None,
+                out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """torch.ops.vllm.exl3_linear of the reference (ops.py:1455-1486): the
+    dense linear over row chunks of a fixed per-stream scratch."""
+    ensure_extension()
+    if row_chunk is None:
+        row_chunk = linear_row_chunk(suh.numel(), svh.numel())
+    workspace = _linear_scratch(x.device)
+    out = torch.empty((x.shape[0], logical_out), dtype=out_dtype, device=x.device)
+    for start in range(0, x.shape[0], row_chunk):
+        linear_out(x[start:start + row_chunk], trellis, suh, svh, bits_x2, codebook,
+                   x.shape[1], logical_out, out[start:start + row_chunk], workspace)
+    return out
