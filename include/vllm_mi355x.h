@@ -46,7 +46,7 @@ int vllm_mi355x_abi_version(void);
 /*
  * FP32 workspace elements exl3_linear_out needs for up to max_rows rows of
  * a padded_in x padded_out matrix: max_rows * (padded_in + padded_out) plus
- * min(max_rows, 8) * ceil(padded_in / 512) * padded_out for the K-split
+ * min(max_rows, 8) * (padded_in / 128) * padded_out for the K-split
  * partial sums of the small-M kernel.  Returns -1 (with an error message)
  * for a negative row count or padded sizes that are not positive multiples
  * of 128.
@@ -82,6 +82,18 @@ int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t x_cols,
                     int64_t codebook, int64_t logical_in, int64_t logical_out,
                     void* out, int out_dtype, int64_t out_rows, int64_t out_cols,
                     float* workspace, int64_t workspace_numel, void* stream);
+
+/*
+ * Test and tuning switch, process-wide: how exl3_linear_out finishes its
+ * small-M (<= 8 rows) launches.  -1 (default): the last workgroup of each
+ * 128-column block sums the K-split partials and writes the outputs, using
+ * one bank of arrival counters per stream (64 per device; streams beyond
+ * that use the separate kernel); 0: always a separate output kernel; 1: as
+ * -1.  Both finishes add in the same order, so results are bitwise equal.
+ * No counterpart in the reference (its nearest is the test-only
+ * set_gemm_shape_override, csrc/exl3/gemm.cu:400-409).
+ */
+int exl3_set_gemv_finish(int mode);
 
 /*
  * Decodes every tile of a trellis into its exact FP16 weights,

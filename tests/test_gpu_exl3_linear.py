@@ -9,7 +9,8 @@ Bars:
     into FP16 high/low parts, so FP32 outputs must agree to
     |err| <= 2^-14 * rms(ref) + 2^-16 * |ref| (a few FP32 roundings of a
     K-term sum; a wrong decode or index is off by O(rms)), and BF16 outputs
-    within one BF16 rounding: |err| <= 2^-8 |ref| + 2^-14 rms(ref).
+    within one BF16 ulp (a value next to a rounding boundary may round the
+    other way): |err| <= 2^-7 |ref| + 2^-14 rms(ref).
 """
 
 import os
@@ -61,7 +62,7 @@ def _assert_fp32_close(actual, expected, name):
 def _assert_round_close(actual, expected, name):
     rms = float(np.sqrt(np.mean(expected.astype(np.float64) ** 2)))
     err = np.abs(actual.astype(np.float64) - expected)
-    bound = 2.0 ** -8 * np.abs(expected) + 2.0 ** -14 * rms
+    bound = 2.0 ** -7 * np.abs(expected) + 2.0 ** -14 * rms
     worst = int(np.argmax(err - bound))
     assert (err <= bound).all(), f"{name}: err {err.flat[worst]:.3g} > {bound.flat[worst]:.3g}"
 
@@ -140,3 +141,86 @@ def test_linear_rejects_small_workspace(ops, device):
     with pytest.raises(RuntimeError, match="workspace is too small"):
         ops.linear_out(x, _dev(trellis, device), _dev(suh, device), _dev(svh, device), 8, 2, 128,
                        128, out, ws)
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_linear_repeated_calls_are_bitwise_identical(ops, device, rows):
+    """Many calls, alternating two streams (two counter banks of the fused
+    finish) and two output buffers: every result must be bitwise the first
+    one, and match the oracle."""
+    print(f"repeat rows={rows}", flush=True)
+    k, n, bits_x2 = 4096, 14336, 8
+    rng = np.random.default_rng(31 + rows)
+    trellis, suh, svh = random_matrix(rng, k, n, bits_x2)
+    x, code = random_acts(rng, rows, k, "fp16")
+    t, u, v = _dev(trellis, device), _dev(suh, device), _dev(svh, device)
+    xt = _dev(x, device)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    wss = [torch.empty(ops.linear_workspace_size(rows, k, n), dtype=torch.float32, device=device)
+           for _ in streams]
+    outs = [torch.empty(rows, n, dtype=torch.float32, device=device) for _ in range(2)]
+    first = None
+    for it in range(60):
+        i = it % 2
+        with torch.cuda.stream(streams[i]):
+            ops.linear_out(xt, t, u, v, bits_x2, 2, k, n, outs[i], wss[i])
+        streams[i].synchronize()
+        got = outs[i].clone()
+        if first is None:
+            first = got
+        else:
+            assert torch.equal(got, first), f"call {it} differs"
+    want = O.linear_out(x, code, trellis, suh, svh, bits_x2, 2, n, O.FP32)
+    _assert_fp32_close(first.cpu().numpy(), want, "repeated")
+
+
+def test_linear_graph_replay_matches_eager(ops, device):
+    k, n, bits_x2, rows = 2048, 4096, 8, 2
+    rng = np.random.default_rng(77)
+    trellis, suh, svh = random_matrix(rng, k, n, bits_x2)
+    x, _ = random_acts(rng, rows, k, "bf16")
+    t, u, v = _dev(trellis, device), _dev(suh, device), _dev(svh, device)
+    xt = _dev(x, device).view(torch.bfloat16)
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=device)
+    ws = torch.empty(ops.linear_workspace_size(rows, k, n), dtype=torch.float32, device=device)
+    ops.linear_out(xt, t, u, v, bits_x2, 2, k, n, out, ws)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            ops.linear_out(xt, t, u, v, bits_x2, 2, k, n, out, ws)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("shape,rows", [((4096, 14336), 1), ((14336, 4096), 1), ((4096, 14336), 8),
+                                        ((256, 384), 3)])
+def test_linear_fused_and_separate_finish_agree(ops, device, shape, rows):
+    """The fused finish (last workgroup per column block) and the separate
+    output kernel add the same values in the same order: bitwise equal."""
+    from vllm_mi355x import _native
+    print(f"finish modes shape={shape} rows={rows}", flush=True)
+    k, n = shape
+    rng = np.random.default_rng(k + rows)
+    trellis, suh, svh = random_matrix(rng, k, n, 8)
+    x, code = random_acts(rng, rows, k, "bf16")
+    results = []
+    lib = _native.load()
+    try:
+        for mode in (0, 1):
+            _native.check(lib.exl3_set_gemv_finish(mode))
+            results.append(_run_linear(ops, device, trellis, suh, svh, x, code, 8, 2, n,
+                                       torch.float32))
+    finally:
+        _native.check(lib.exl3_set_gemv_finish(-1))
+    assert torch.equal(results[0], results[1])
+    if k * n <= 4096 * 4096:
+        want = O.linear_out(x, code, trellis, suh, svh, 8, 2, n, O.FP32)
+        _assert_fp32_close(_out_np(results[0]), want, "finish modes")

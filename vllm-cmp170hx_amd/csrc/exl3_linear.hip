@@ -3,17 +3,19 @@
 // exl3_linear_workspace_size.
 //
 // Small-M path (rows <= 8 per launch), two kernels:
-//  1. gemv_kernel: one workgroup = 4 wavefronts = 32 output columns (two
-//     tile columns) x a K range of up to 4*depth steps of 32 inputs.  It
-//       a. issues all of its trellis loads first (dword loads; the 64 lanes
-//          of a wavefront read two whole 16x16 tiles per tile row),
-//       b. forms its activations meanwhile: t = H128(x * suh) for its K range
-//          and every row, split into FP16 high and low parts at a per-row
-//          power-of-two scale, stored in LDS in MFMA B-operand order,
-//       c. decodes 16 trellis states per lane per step straight into MFMA
-//          A-operand order and runs two v_mfma_f32_16x16x32_f16 per step,
-//       d. reduces its four wavefronts through LDS in a fixed order and
-//          writes one FP32 partial sum per (row, column).
+//  1. gemv_kernel: one workgroup = 4 wavefronts = 128 output columns (one
+//     H128 block) x 128 inputs (one H128 block, 4 steps of 32).  Wavefront w
+//     owns two tile columns (32 outputs) over the whole range.  It
+//       a. loads its activations, then issues all of its trellis loads
+//          (one coalesced dword per lane per tile row: every trellis byte
+//          is fetched once, in whole cache lines),
+//       b. wavefront w forms rows w, w + 4: t = H128(x * suh) of the block,
+//          stored in LDS, in MFMA B-operand order, as FP16 high and low
+//          parts at a per-row power-of-two scale,
+//       c. gathers each decoding lane's ring words with ds_bpermute, decodes
+//          16 trellis states per lane per step straight into MFMA A-operand
+//          order and runs two v_mfma_f32_16x16x32_f16 per step,
+//       d. writes one FP32 partial sum per (K split, row, column).
 //  2. gemv_output: sums the K-split partials in split order, applies the
 //     output H128 and svh, rounds to the output dtype.
 //
@@ -28,8 +30,12 @@
 // same k-slot order, so no lane shuffle of weights is ever needed.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "../../include/vllm_mi355x.h"
 #include "common.h"
@@ -58,24 +64,24 @@ bool known_format(int64_t bits_x2, int64_t codebook) {
   return false;
 }
 
+
 // Per-rate geometry of the small-M kernel.
+//
+// Up to 4 bits per weight (bits_x2 <= 8) a wavefront's two tiles of one tile
+// row are at most 64 dwords: each lane loads one of them with one coalesced
+// global_load_dword (every trellis byte is fetched once, in whole cache
+// lines), and each decoding lane then gathers the ring words of its encoder
+// lane from the loading lanes with ds_bpermute.  Wider rates load each lane's
+// window words directly.
 template <int kBitsX2>
 struct Gemv {
+  static constexpr bool kCoalesced = kBitsX2 <= 8;
   static constexpr int kWords = LaneLoad<kBitsX2>::kWords;
-  // steps (two tile rows each) each wavefront loads up front
-  static constexpr int kDepth = 32 / (2 * kWords);
-  static constexpr int kStepsPerGroup = 4 * kDepth;
+  // registers each lane loads per tile row (two tiles)
+  static constexpr int kRaw = kCoalesced ? 1 : 2 * kWords;
+  // steps of loads each wavefront keeps in flight
+  static constexpr int kDepth = 32 / (2 * kRaw);
 };
-
-int gemv_steps_per_group(int bits_x2) {
-  switch (bits_x2) {
-#define VQ_STEPS(B) case B: return Gemv<B>::kStepsPerGroup;
-    VQ_STEPS(2) VQ_STEPS(3) VQ_STEPS(4) VQ_STEPS(5) VQ_STEPS(6) VQ_STEPS(7) VQ_STEPS(8)
-    VQ_STEPS(10) VQ_STEPS(12) VQ_STEPS(14) VQ_STEPS(16)
-#undef VQ_STEPS
-  }
-  return 16;
-}
 
 // Ring word `w` of a tile.
 template <bool kAligned>
@@ -131,16 +137,92 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const uint8_t* __restr
 struct GemvArgs {
   const void* x;
   const uint16_t* suh;
+  const uint16_t* svh;
   const uint8_t* trellis;
   float* partial;        // [splits][rows][np]
+  void* out;             // [rows][logical_out]
+  int counter_bank;      // fused finish: the stream's counter bank, or -1
   int64_t logical_in;
+  int64_t logical_out;
   int64_t tiles_n;
   int64_t np;
   int x_dtype;
+  int out_dtype;
   int rows;              // 1..8
   int steps_total;       // padded_in / 32
-  int steps_per_group;   // multiple of 4
+  int splits;            // K splits (padded_in / 128)
 };
+
+// Arrival counters of the fused finish, in static device memory (zero when
+// the code object loads; every call returns the slots it used to zero):
+// kCounterBanks banks of kCounterSlots (one slot per 128-column block), one
+// bank per stream, so calls that overlap on different streams never share a
+// slot.
+constexpr int kCounterBanks = 64;
+constexpr int kCounterSlots = 2048;
+__device__ uint32_t g_gemv_counters[kCounterBanks * kCounterSlots];
+
+// A partial sum: agent-scope (bypassing caches that may hold another
+// call's data) in the fused finish, plain in the separate output kernel.
+template <bool kCoherent>
+__device__ __forceinline__ float load_partial(const float* p) {
+  if constexpr (kCoherent) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    return *p;
+  }
+}
+
+// Row r of one 128-column output block (the separate output kernel): lane l
+// sums columns l and l + 64 over the K splits (loads eight at a time in
+// flight), then H128, times svh, rounded to the output dtype.
+template <bool kCoherent>
+__device__ __forceinline__ void finish_row_block(const float* __restrict__ partial, int splits,
+                                                 int rows, int64_t np, int64_t r, int64_t base,
+                                                 const uint16_t* __restrict__ svh,
+                                                 int64_t logical_out, void* out, int out_dtype,
+                                                 int lane) {
+  const int64_t c0 = base + lane;
+  const int64_t c1 = c0 + 64;
+  const uint32_t scale0 = svh[c0];
+  const uint32_t scale1 = svh[c1];
+  const float* p = partial + r * np;
+  const int64_t stride = int64_t(rows) * np;
+  // even splits, then odd splits, each in order, then even + odd: the same
+  // additions as the fused finish
+  float e0 = 0.0f, e1 = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  int s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    float a0[8], a1[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      a0[u] = load_partial<kCoherent>(p + (s + u) * stride + c0);
+      a1[u] = load_partial<kCoherent>(p + (s + u) * stride + c1);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u += 2) {
+      e0 += a0[u];
+      e1 += a1[u];
+      o0 += a0[u + 1];
+      o1 += a1[u + 1];
+    }
+  }
+  for (; s < splits; ++s) {
+    const float x0 = load_partial<kCoherent>(p + s * stride + c0);
+    const float x1 = load_partial<kCoherent>(p + s * stride + c1);
+    if (s & 1) {
+      o0 += x0;
+      o1 += x1;
+    } else {
+      e0 += x0;
+      e1 += x1;
+    }
+  }
+  float v0 = e0 + o0, v1 = e1 + o1;
+  vq::h128_wave(v0, v1, lane);
+  if (c0 < logical_out) vq::store_act(out, out_dtype, r * logical_out + c0, v0 * vq::f16_to_f32(uint16_t(scale0)));
+  if (c1 < logical_out) vq::store_act(out, out_dtype, r * logical_out + c1, v1 * vq::f16_to_f32(uint16_t(scale1)));
+}
 
 // Power-of-two exponent e so that max * 2^e lies in [2^14, 2^15): the FP16
 // high part then stays below 2^15 and the low part keeps ~11 more bits.
@@ -151,25 +233,71 @@ __device__ __forceinline__ int scale_exponent(uint32_t max_bits) {
   return e > 127 ? 127 : (e < -126 ? -126 : e);
 }
 
-// Float index, within the LDS activation block, of local input k of row r:
-// the block is [step][g][row][8 slots] of FP32, later rewritten in place as
-// [step][g][row][hi 8 halves | lo 8 halves] = [step][g][B column][8 halves].
-__device__ __forceinline__ int act_index(int k, int r, int rows) {
-  const int step = k >> 5;
-  const int w = k & 31;
-  const int tr = w >> 4;
-  const int kk = w & 15;
-  const int g = (kk & 7) >> 1;
-  const int slot = 4 * tr + (kk & 1) + 2 * (kk >> 3);
-  return ((step * 4 + g) * rows + r) * 8 + slot;
+__device__ __forceinline__ float u16_act(uint16_t v, int dtype) {
+  return dtype == kBF16 ? vq::bf16_to_f32(v) : vq::f16_to_f32(v);
 }
 
-template <int kBitsX2, int kCodebook, bool kAligned>
+// Fused finish of one 128-column block by the whole workgroup: thread t
+// sums column t & 127 over the splits of parity t >> 7 (agent-scope loads,
+// eight in flight, split order), the two parity sums are added (even +
+// odd) through LDS, then wavefront w applies H128 and svh to rows w, w + 4.
+__device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int tid) {
+  const int col = tid & 127;
+  const int part = tid >> 7;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t base = 128 * int64_t(blockIdx.x);
+  const int64_t stride = int64_t(a.rows) * a.np;
+  for (int r = 0; r < a.rows; ++r) {
+    const float* p = a.partial + int64_t(r) * a.np + base + col;
+    float v = 0.0f;
+    int s = part;
+    for (; s + 14 < a.splits; s += 16) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = load_partial<true>(p + (s + 2 * u) * stride);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v += t[u];
+    }
+    for (; s < a.splits; s += 2) v += load_partial<true>(p + s * stride);
+    red[(part * a.rows + r) * 128 + col] = v;
+  }
+  __syncthreads();
+  for (int r = wave; r < a.rows; r += 4) {
+    float v0 = red[r * 128 + lane] + red[(a.rows + r) * 128 + lane];
+    float v1 = red[r * 128 + lane + 64] + red[(a.rows + r) * 128 + lane + 64];
+    vq::h128_wave(v0, v1, lane);
+    const int64_t c0 = base + lane;
+    const int64_t c1 = c0 + 64;
+    void* out = a.out;
+    if (c0 < a.logical_out) vq::store_act(out, a.out_dtype, r * a.logical_out + c0, v0 * vq::f16_to_f32(a.svh[c0]));
+    if (c1 < a.logical_out) vq::store_act(out, a.out_dtype, r * a.logical_out + c1, v1 * vq::f16_to_f32(a.svh[c1]));
+  }
+}
+
+// One workgroup = 4 wavefronts = 128 output columns (one H128 block) x up to
+// kBlocks 128-input blocks (4 steps of 32 inputs each).  Wavefront w owns
+// the column pair 4 * blockIdx.x + w (two tile columns, 32 outputs) over the
+// whole K range and streams its trellis through a ring of kDepth steps of
+// loads in flight.
+//
+// kRows (1, 2, 4 or 8) is the row count the kernel is built for; a call with
+// fewer rows (a.rows) computes its last row in the padding rows, which are
+// never stored.
+template <int kBitsX2, int kCodebook, bool kAligned, int kRows, int kBlocks>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   using G = Gemv<kBitsX2>;
   using R = Ring<kBitsX2>;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  __shared__ uint32_t row_max[kMaxGemvRows];
+  constexpr int kSteps = 4 * kBlocks;
+  constexpr int kDepth = G::kDepth < kSteps ? G::kDepth : kSteps;
+  constexpr int kCols = 2 * kRows;                        // B columns: hi, lo per row
+  constexpr int kActHalves = kSteps * 4 * kCols * 8;      // B operands of the range
+  constexpr int kTasks = kBlocks * kRows;                 // (block, row) forming tasks
+  constexpr int kFormTasks = (kTasks + 3) / 4;            // per wavefront
+  // activations in B-operand order, then 8 zero halves: the B operand of
+  // the unused columns.  Reused by the fused finish for its row sums.
+  __shared__ __attribute__((aligned(16))) _Float16 act[kActHalves + 8 > 2 * 128 * kRows * 2 ? kActHalves + 8 : 2 * 128 * kRows * 2];
+  __shared__ int block_exp[kBlocks][kRows];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -177,155 +305,242 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   const int g = lane >> 4;
   const int m = lane & 15;
   const int L = 4 * (m & 7) + g;
-  const int rows = a.rows;
-  const int step0 = blockIdx.y * a.steps_per_group;
-  const int nsteps = min(a.steps_per_group, a.steps_total - step0);
-  const int per_wave = nsteps >> 2;
+  const int blocks_total = a.steps_total / 4;
+  const int block0 = blockIdx.y * kBlocks;
+  const int nblocks = min(kBlocks, blocks_total - block0);
+  const int nsteps = 4 * nblocks;
+  const int64_t k0 = int64_t(block0) * 128;
 
-  // a. trellis loads of this wavefront's steps
+  // a. activation loads first (they must not queue behind the trellis).
+  //    Forming task t = wave + 4f is (block t / kRows, row t % kRows); lane l
+  //    holds elements l and l + 64 of the block.  Every load is
+  //    unconditional, at a clamped (always valid) index, and the value is
+  //    selected afterwards: loads under a branch would each wait for their
+  //    data before the branch closes.
+  const uint16_t* xs = static_cast<const uint16_t*>(a.x);
+  uint32_t xv[kFormTasks][2], sv[kFormTasks][2];
+#pragma unroll
+  for (int f = 0; f < kFormTasks; ++f) {
+    const int t = wave + 4 * f;
+    const int b = min(t / kRows, nblocks - 1);
+    const int64_t row = int64_t(min(t % kRows, a.rows - 1)) * a.logical_in;
+    const int64_t k_0 = k0 + 128 * b + lane;
+    const int64_t k_1 = k_0 + 64;
+    const int64_t c0 = k_0 < a.logical_in ? k_0 : 0;
+    const int64_t c1 = k_1 < a.logical_in ? k_1 : 0;
+    sv[f][0] = a.suh[c0];
+    sv[f][1] = a.suh[c1];
+    xv[f][0] = xs[row + c0];
+    xv[f][1] = xs[row + c1];
+  }
+#pragma unroll
+  for (int f = 0; f < kFormTasks; ++f) {
+    const int b = min((wave + 4 * f) / kRows, nblocks - 1);
+    const int64_t k_0 = k0 + 128 * b + lane;
+    if (!(k_0 < a.logical_in)) { sv[f][0] = 0u; xv[f][0] = 0u; }
+    if (!(k_0 + 64 < a.logical_in)) { sv[f][1] = 0u; xv[f][1] = 0u; }
+  }
+
+  // b. the first kDepth steps of trellis loads.  raw[j][h] holds tile row
+  //    2j + h of this wavefront's two tiles (coalesced: dword `lane` of the
+  //    2-tile chunk; direct: this lane's window words, tile m >> 3).
   int off[G::kWords];
   lane_word_offsets<kBitsX2>(L, off);
   const int64_t row_bytes = a.tiles_n * R::kTileBytes;
-  const uint8_t* column = a.trellis + (2 * int64_t(blockIdx.x) + (m >> 3)) * R::kTileBytes;
-  uint32_t words[G::kDepth][2][G::kWords];
+  const uint8_t* chunk = a.trellis + 2 * (4 * int64_t(blockIdx.x) + wave) * R::kTileBytes +
+                         8 * int64_t(block0) * row_bytes;
+  const int raw_off = lane < 8 * kBitsX2 ? 4 * lane : 0;  // lanes past the chunk reload dword 0
+  const int tile_off = (m >> 3) * R::kTileBytes;
+  uint32_t raw[kSteps][2][G::kRaw];
+  auto load_step = [&](int j) {
 #pragma unroll
-  for (int j = 0; j < G::kDepth; ++j) {
-    if (j < per_wave) {
-      const int64_t kt = 2 * int64_t(step0 + wave * per_wave + j);
+    for (int h = 0; h < 2; ++h) {
+      const uint8_t* row = chunk + (2 * j + h) * row_bytes;
+      if constexpr (G::kCoalesced) {
+        raw[j][h][0] = tile_word<kAligned>(row, raw_off);
+      } else {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint8_t* tile = column + (kt + h) * row_bytes;
+        for (int i = 0; i < G::kWords; ++i) raw[j][h][i] = tile_word<kAligned>(row + tile_off, off[i]);
+      }
+    }
+  };
 #pragma unroll
-        for (int i = 0; i < G::kWords; ++i) words[j][h][i] = tile_word<kAligned>(tile, off[i]);
+  for (int j = 0; j < kDepth; ++j) {
+    if (j < nsteps) load_step(j);
+  }
+  // coalesced: ds_bpermute byte addresses of the lanes holding this lane's words
+  int src[G::kWords];
+#pragma unroll
+  for (int i = 0; i < G::kWords; ++i) src[i] = 4 * ((m >> 3) * 4 * kBitsX2 + off[i] / 4);
+
+  // c. forming: t = H128(x * suh) of a (block, row), split at a power-of-two
+  //    scale into FP16 high / low parts, written straight into B-operand
+  //    order: act = [step][g][B column 2r + (0 hi | 1 lo)][8 halves].
+  if (tid < 8) act[kActHalves + tid] = _Float16(0.0f);
+  {
+    // half index of input k (within a block) at B column 0
+    auto slot_of = [&](int k) {
+      const int step = k >> 5;
+      const int w = k & 31;
+      const int kk = w & 15;
+      const int gg = (kk & 7) >> 1;
+      const int slot = 4 * (w >> 4) + (kk & 1) + 2 * (kk >> 3);
+      return ((step * 4 + gg) * kCols) * 8 + slot;
+    };
+    const int h0 = slot_of(lane);
+    const int h1 = slot_of(lane + 64);
+#pragma unroll
+    for (int f = 0; f < kFormTasks; ++f) {
+      const int t = wave + 4 * f;
+      const int b = t / kRows;
+      const int r = t % kRows;
+      if (t < kTasks && b < nblocks) {
+        float v0 = u16_act(uint16_t(xv[f][0]), a.x_dtype) * vq::f16_to_f32(uint16_t(sv[f][0]));
+        float v1 = u16_act(uint16_t(xv[f][1]), a.x_dtype) * vq::f16_to_f32(uint16_t(sv[f][1]));
+        vq::h128_wave(v0, v1, lane);
+        float mx = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+        const int e = scale_exponent(__builtin_bit_cast(uint32_t, mx));
+        if (lane == 0) block_exp[b][r] = e;
+        const float t0 = ldexpf(v0, e);
+        const float t1 = ldexpf(v1, e);
+        const _Float16 hi0 = _Float16(t0), hi1 = _Float16(t1);
+        const int base = b * 4 * 4 * kCols * 8 + (2 * r) * 8;
+        act[base + h0] = hi0;
+        act[base + h0 + 8] = _Float16(t0 - float(hi0));
+        act[base + h1] = hi1;
+        act[base + h1 + 8] = _Float16(t1 - float(hi1));
       }
     }
   }
 
-  // b. activations: t = H128(x * suh) over this group's K range, per row
-  if (tid < kMaxGemvRows) row_max[tid] = 0u;
-  __syncthreads();
-  float* act = reinterpret_cast<float*>(smem);
-  const int blocks = nsteps >> 2;
-  const int64_t k0 = int64_t(step0) * 32;
-  for (int task = wave; task < rows * blocks; task += 4) {
-    const int r = task / blocks;
-    const int b = task - r * blocks;
-    const int kl0 = b * 128 + lane;
-    const int kl1 = kl0 + 64;
-    const int64_t kg0 = k0 + kl0;
-    const int64_t kg1 = k0 + kl1;
-    const int64_t xrow = int64_t(r) * a.logical_in;
-    float v0 = kg0 < a.logical_in ? vq::load_act(a.x, a.x_dtype, xrow + kg0) * vq::f16_to_f32(a.suh[kg0]) : 0.0f;
-    float v1 = kg1 < a.logical_in ? vq::load_act(a.x, a.x_dtype, xrow + kg1) * vq::f16_to_f32(a.suh[kg1]) : 0.0f;
-    vq::h128_wave(v0, v1, lane);
-    act[act_index(kl0, r, rows)] = v0;
-    act[act_index(kl1, r, rows)] = v1;
-    float mx = fmaxf(fabsf(v0), fabsf(v1));
+  // d. stream: decode step j while later steps are in flight.  Each block's
+  //    products accumulate in acc1/acc2 from zero and are folded, unscaled,
+  //    into tot1/tot2 (high + low parts: B columns 2r, 2r + 1 sit in
+  //    adjacent lanes) at the block's end, blocks in order.
+  uint32_t wv[kSteps][2][G::kWords];
+  auto gather = [&](int j) {
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
-    if (lane == 0) atomicMax(&row_max[r], __builtin_bit_cast(uint32_t, mx));
-  }
-  __syncthreads();
-  const int chunks = nsteps * 4 * rows;
-  for (int c = tid; c < chunks; c += kThreads) {
-    const int e = scale_exponent(row_max[c % rows]);
-    f32x4_t* p = reinterpret_cast<f32x4_t*>(act + c * 8);
-    const f32x4_t v0 = p[0];
-    const f32x4_t v1 = p[1];
-    half8_t hi, lo;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float s = ldexpf(i < 4 ? v0[i] : v1[i - 4], e);
-      const _Float16 h = _Float16(s);
-      hi[i] = h;
-      lo[i] = _Float16(s - float(h));
+    for (int i = 0; i < G::kWords; ++i) {
+      if constexpr (G::kCoalesced) {
+        wv[j][0][i] = uint32_t(__builtin_amdgcn_ds_bpermute(src[i], int(raw[j][0][0])));
+        wv[j][1][i] = uint32_t(__builtin_amdgcn_ds_bpermute(src[i], int(raw[j][1][0])));
+      } else {
+        wv[j][0][i] = raw[j][0][i];
+        wv[j][1][i] = raw[j][1][i];
+      }
     }
-    reinterpret_cast<half8_t*>(p)[0] = hi;
-    reinterpret_cast<half8_t*>(p)[1] = lo;
-  }
-  __syncthreads();
-
-  // c. decode + MFMA
-  const int ncols = 2 * rows;
-  f32x4_t acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4_t acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+  };
+  const char* lds = reinterpret_cast<const char*>(act);
+  const int r_own = (m >> 1) < kRows ? (m >> 1) : 0;
+  f32x4_t acc1 = {}, acc2 = {};
+  float tot1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float tot2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  gather(0);
 #pragma unroll
-  for (int j = 0; j < G::kDepth; ++j) {
-    if (j < per_wave) {
-      const int sl = wave * per_wave + j;
+  for (int j = 0; j < kSteps; ++j) {
+    if (j < nsteps) {
+      if (j + 1 < kSteps && j + 1 < nsteps) gather(j + 1);
+      if (j + kDepth < kSteps && j + kDepth < nsteps) load_step(j + kDepth);
       uint32_t q0[4], q1[4];
-      decode_words<kBitsX2, kCodebook>(L, words[j][0], q0);
-      decode_words<kBitsX2, kCodebook>(L, words[j][1], q1);
+      decode_words<kBitsX2, kCodebook>(L, wv[j][0], q0);
+      decode_words<kBitsX2, kCodebook>(L, wv[j][1], q1);
+      // the activations are complete once every wavefront is past here (the
+      // first decode overlaps the wait)
+      if (j == 0) __syncthreads();
       const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
       const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
-      half8_t bop = {};
-      if (m < ncols) bop = *reinterpret_cast<const half8_t*>(smem + ((sl * 4 + g) * ncols + m) * 16);
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), bop, acc1, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), bop, acc2, 0, 0, 0);
+      const half8_t bop = *reinterpret_cast<const half8_t*>(
+          lds + (m < kCols ? ((j * 4 + g) * kCols + m) * 16 : kActHalves * 2));
+      const f32x4_t zero = {};
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), bop,
+                                                    (j & 3) == 0 ? zero : acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), bop,
+                                                    (j & 3) == 0 ? zero : acc2, 0, 0, 0);
+      if ((j & 3) == 3) {
+        const int e = block_exp[j >> 2][r_own];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          tot1[i] += ldexpf(acc1[i] + __shfl_xor(acc1[i], 1), -e);
+          tot2[i] += ldexpf(acc2[i] + __shfl_xor(acc2[i], 1), -e);
+        }
+      }
     }
   }
 
-  // d. reduce the four wavefronts: red[wave][column 0..31][B column 0..15]
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(smem);
-  if (m < ncols) {
+  // e. the partial sums of this K split: lane (g, 2r) holds rows 4g..4g+3 of
+  //    both MFMAs.  Agent-scope stores are written through to the
+  //    device-coherent level, so the fused finish (on any XCD) reads them
+  //    without a cache writeback of this workgroup.
+  float* dst = a.partial + int64_t(blockIdx.y) * a.rows * a.np + 32 * (4 * int64_t(blockIdx.x) + wave);
+  if (m < kCols && (m & 1) == 0 && (m >> 1) < a.rows) {
+    const int r = m >> 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 4 * g + i;
       const int col = (row & 7) + 16 * (row >> 3);
-      red[(wave * 32 + col) * 16 + m] = acc1[i];
-      red[(wave * 32 + col + 8) * 16 + m] = acc2[i];
+      __hip_atomic_store(dst + int64_t(r) * a.np + col, tot1[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(dst + int64_t(r) * a.np + col + 8, tot2[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  __syncthreads();
-  for (int t = tid; t < 32 * rows; t += kThreads) {
-    const int col = t & 31;
-    const int r = t >> 5;
-    float s = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      s += red[(w * 32 + col) * 16 + 2 * r] + red[(w * 32 + col) * 16 + 2 * r + 1];
+
+  // f. fused finish: the last workgroup of this 128-column block to arrive
+  //    sums every split's partials and writes the outputs.
+  if (a.counter_bank >= 0) {
+    uint32_t* counter = g_gemv_counters + a.counter_bank * kCounterSlots + blockIdx.x;
+    __shared__ int is_last;
+    // every store of this wavefront has completed (vmcnt counts stores on
+    // gfx9), then every wavefront of the workgroup is past that point
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t arrived =
+          __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      is_last = arrived == uint32_t(a.splits - 1);
     }
-    a.partial[(int64_t(blockIdx.y) * rows + r) * a.np + 32 * int64_t(blockIdx.x) + col] =
-        ldexpf(s, -scale_exponent(row_max[r]));
+    __syncthreads();
+    if (is_last) {
+      finish_block(a, reinterpret_cast<float*>(act), tid);
+      if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
-// One wavefront per (row, 128-column block): sum the K-split partials in
-// split order, H128, times svh, rounded to the output dtype.
+// Unfused finish: one wavefront per (row, 128-column block).
 __global__ __launch_bounds__(kThreads) void gemv_output(const float* __restrict__ partial, int splits,
                                                          int rows, int64_t np,
                                                          const uint16_t* __restrict__ svh,
                                                          int64_t logical_out, void* out, int out_dtype) {
   const int lane = threadIdx.x & 63;
-  const int64_t task = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t blocks = np / 128;
+  const int64_t task = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (task >= rows * blocks) return;
   const int64_t r = task / blocks;
-  const int64_t c0 = (task - r * blocks) * 128 + lane;
-  const int64_t c1 = c0 + 64;
-  float v0 = 0.0f, v1 = 0.0f;
-  for (int s = 0; s < splits; ++s) {
-    const float* p = partial + (int64_t(s) * rows + r) * np;
-    v0 += p[c0];
-    v1 += p[c1];
-  }
-  vq::h128_wave(v0, v1, lane);
-  if (c0 < logical_out) vq::store_act(out, out_dtype, r * logical_out + c0, v0 * vq::f16_to_f32(svh[c0]));
-  if (c1 < logical_out) vq::store_act(out, out_dtype, r * logical_out + c1, v1 * vq::f16_to_f32(svh[c1]));
+  finish_row_block<false>(partial, splits, rows, np, r, (task - r * blocks) * 128, svh, logical_out, out,
+                   out_dtype, lane);
 }
 
 // ---- dispatch ----------------------------------------------------------------
 
 template <int kBitsX2, int kCodebook>
-int launch_format(bool aligned, const GemvArgs* gemv, dim3 grid, size_t lds, hipStream_t stream,
+int launch_format(bool aligned, const GemvArgs* gemv, int gemv_blocks, dim3 grid, size_t lds, hipStream_t stream,
                   const uint8_t* trellis, int64_t tiles_k, int64_t tiles_n, uint16_t* decoded) {
   if (gemv) {
+#define VQ_GEMV(A, NR, NB)                                                                    \
+  hipLaunchKernelGGL((gemv_kernel<kBitsX2, kCodebook, A, NR, NB>), grid, dim3(kThreads), 0, stream, *gemv)
+#define VQ_GEMV_ROWS(A, NB)                                                  \
+  if (r <= 1) VQ_GEMV(A, 1, NB); else if (r <= 2) VQ_GEMV(A, 2, NB);        \
+  else if (r <= 4) VQ_GEMV(A, 4, NB); else VQ_GEMV(A, 8, NB);
+    const int r = gemv->rows;
+    const bool one = gemv_blocks == 1;
     if (aligned) {
-      hipLaunchKernelGGL((gemv_kernel<kBitsX2, kCodebook, true>), grid, dim3(kThreads), lds, stream, *gemv);
+      if (one) { VQ_GEMV_ROWS(true, 1) } else { VQ_GEMV_ROWS(true, 4) }
     } else {
-      hipLaunchKernelGGL((gemv_kernel<kBitsX2, kCodebook, false>), grid, dim3(kThreads), lds, stream, *gemv);
+      if (one) { VQ_GEMV_ROWS(false, 1) } else { VQ_GEMV_ROWS(false, 4) }
     }
+#undef VQ_GEMV_ROWS
+#undef VQ_GEMV
     return vq::check_launch("exl3 gemv_kernel");
   }
   const int64_t threads = tiles_k * tiles_n * 32;
@@ -340,12 +555,12 @@ int launch_format(bool aligned, const GemvArgs* gemv, dim3 grid, size_t lds, hip
   return vq::check_launch("exl3 decode_kernel");
 }
 
-int dispatch(int64_t bits_x2, int64_t codebook, bool aligned, const GemvArgs* gemv, dim3 grid,
-             size_t lds, hipStream_t stream, const uint8_t* trellis, int64_t tiles_k,
+int dispatch(int64_t bits_x2, int64_t codebook, bool aligned, const GemvArgs* gemv, int gemv_blocks,
+             dim3 grid, size_t lds, hipStream_t stream, const uint8_t* trellis, int64_t tiles_k,
              int64_t tiles_n, uint16_t* decoded) {
 #define VQ_CASE(B, C)                                                                   \
   if (bits_x2 == B && codebook == C)                                                    \
-    return launch_format<B, C>(aligned, gemv, grid, lds, stream, trellis, tiles_k, tiles_n, decoded);
+    return launch_format<B, C>(aligned, gemv, gemv_blocks, grid, lds, stream, trellis, tiles_k, tiles_n, decoded);
   VQ_CASE(2, 1) VQ_CASE(4, 1) VQ_CASE(6, 1) VQ_CASE(8, 1)
   VQ_CASE(10, 1) VQ_CASE(12, 1) VQ_CASE(14, 1) VQ_CASE(16, 1)
   VQ_CASE(2, 2) VQ_CASE(3, 2) VQ_CASE(4, 2) VQ_CASE(5, 2) VQ_CASE(6, 2) VQ_CASE(7, 2)
@@ -361,11 +576,39 @@ int check_padded(int64_t n) {
   return vq::kOk;
 }
 
-int64_t gemv_splits(int64_t padded_in, int bits_x2) {
-  const int64_t steps = padded_in / 32;
-  const int64_t spg = gemv_steps_per_group(bits_x2);
-  return (steps + spg - 1) / spg;
+// Counter bank of (current device, stream) for the fused finish, assigned on
+// first use; -1 once every bank of the device is taken (those streams use
+// the unfused two-kernel finish).
+int counter_bank(hipStream_t stream) {
+  static std::mutex mutex;
+  static std::map<std::pair<int, hipStream_t>, int> banks;
+  static std::map<int, int> used;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return -1;
+  std::lock_guard<std::mutex> lock(mutex);
+  const auto key = std::make_pair(device, stream);
+  const auto it = banks.find(key);
+  if (it != banks.end()) return it->second;
+  int& n = used[device];
+  if (n >= kCounterBanks) return -1;
+  banks[key] = n;
+  return n++;
 }
+
+// Most K splits the small-M kernel uses: one per 128-input block.
+int64_t gemv_splits(int64_t padded_in) { return padded_in / 128; }
+
+// 128-input blocks per workgroup: 1 while the fused finish stays short
+// (rows * splits <= 32) and the grid stays under ~4096 workgroups, else 4
+// (longer trellis streams per wavefront, fewer partial sums).
+int gemv_blocks(int64_t rows, int64_t padded_in, int64_t padded_out) {
+  const int64_t k_blocks = padded_in / 128;
+  return rows * k_blocks <= 32 && (padded_out / 128) * k_blocks <= 4096 ? 1 : 4;
+}
+
+// Finish of the small-M path: -1 automatic (fused while a counter bank is
+// free), 0 always the separate output kernel, 1 always fused when possible.
+std::atomic<int> g_finish_mode{-1};
 
 }  // namespace
 }  // namespace exl3
@@ -378,9 +621,8 @@ extern "C" int64_t exl3_linear_workspace_size(int64_t max_rows, int64_t padded_i
   }
   if (exl3::check_padded(padded_in) != vq::kOk || exl3::check_padded(padded_out) != vq::kOk) return -1;
   const int64_t small = max_rows < exl3::kMaxGemvRows ? max_rows : exl3::kMaxGemvRows;
-  // K-split partials: at most ceil(padded_in / 512) splits (16 steps of 32
-  // inputs per workgroup at the least).
-  const int64_t splits = (padded_in + 511) / 512;
+  // K-split partials of the small-M kernel: padded_in / 128 splits.
+  const int64_t splits = exl3::gemv_splits(padded_in);
   return max_rows * (padded_in + padded_out) + small * splits * padded_out;
 }
 
@@ -394,7 +636,7 @@ extern "C" int exl3_decode(const void* trellis, int64_t tiles_k, int64_t tiles_n
     return vq::fail("Unsupported EXL3 rate/codebook combination");
   }
   const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
-  return exl3::dispatch(bits_x2, codebook, aligned, nullptr, dim3(), 0,
+  return exl3::dispatch(bits_x2, codebook, aligned, nullptr, 0, dim3(), 0,
                         static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(trellis),
                         tiles_k, tiles_n, static_cast<uint16_t*>(out));
 }
@@ -455,42 +697,50 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
   const int steps_total = int(padded_in / 32);
-  const int spg_max = exl3::gemv_steps_per_group(int(bits_x2));
-  const int64_t splits0 = exl3::gemv_splits(padded_in, int(bits_x2));
-  // Even split, rounded up to whole 128-input blocks (4 steps).
-  int spg = int((steps_total + splits0 - 1) / splits0);
-  spg = (spg + 3) / 4 * 4;
-  if (spg > spg_max) spg = spg_max;
-  const int64_t splits = (steps_total + spg - 1) / spg;
+  const int blocks = exl3::gemv_blocks(rows < exl3::kMaxGemvRows ? rows : exl3::kMaxGemvRows,
+                                       padded_in, padded_out);
+  const int64_t splits = (padded_in / 128 + blocks - 1) / blocks;
   if (splits > 65535) return fail("EXL3 linear K is too large");
   float* partial = workspace;
+  const int64_t col_blocks = padded_out / 128;
+  const int mode = exl3::g_finish_mode.load();
+  const int bank = mode != 0 && col_blocks <= exl3::kCounterSlots ? exl3::counter_bank(s) : -1;
   for (int64_t r0 = 0; r0 < rows; r0 += exl3::kMaxGemvRows) {
     const int chunk = int(rows - r0 < exl3::kMaxGemvRows ? rows - r0 : exl3::kMaxGemvRows);
     exl3::GemvArgs a{};
     a.x = static_cast<const uint8_t*>(x) + r0 * logical_in * dtype_bytes(x_dtype);
     a.suh = static_cast<const uint16_t*>(suh);
+    a.svh = static_cast<const uint16_t*>(svh);
     a.trellis = static_cast<const uint8_t*>(trellis);
     a.partial = partial;
+    a.out = static_cast<uint8_t*>(out) + r0 * logical_out * dtype_bytes(out_dtype);
+    a.counter_bank = bank;
     a.logical_in = logical_in;
+    a.logical_out = logical_out;
     a.tiles_n = tiles_n;
     a.np = padded_out;
     a.x_dtype = x_dtype;
+    a.out_dtype = out_dtype;
     a.rows = chunk;
     a.steps_total = steps_total;
-    a.steps_per_group = spg;
-    const dim3 grid(unsigned(padded_out / 32), unsigned(splits));
-    size_t lds = size_t(spg) * 4 * chunk * 32;
-    if (lds < 4 * 32 * 16 * 4) lds = 4 * 32 * 16 * 4;
-    if (int rc = exl3::dispatch(bits_x2, codebook, aligned, &a, grid, lds, s, nullptr, 0, 0, nullptr)) {
+    a.splits = int(splits);
+    const dim3 grid{unsigned(col_blocks), unsigned(splits), 1u};
+    if (int rc = exl3::dispatch(bits_x2, codebook, aligned, &a, blocks, grid, 0, s, nullptr, 0, 0, nullptr)) {
       return rc;
     }
-    const int64_t tasks = chunk * (padded_out / 128);
-    hipLaunchKernelGGL(exl3::gemv_output, dim3(unsigned((tasks + 3) / 4)), dim3(exl3::kThreads), 0, s,
-                       partial, int(splits), chunk, padded_out, static_cast<const uint16_t*>(svh),
-                       logical_out,
-                       static_cast<uint8_t*>(out) + r0 * logical_out * dtype_bytes(out_dtype),
-                       out_dtype);
-    if (int rc = check_launch("exl3 gemv_output")) return rc;
+    if (bank < 0) {
+      const int64_t tasks = chunk * col_blocks;
+      hipLaunchKernelGGL(exl3::gemv_output, dim3(unsigned((tasks + 3) / 4)), dim3(exl3::kThreads), 0, s,
+                         partial, int(splits), chunk, padded_out, static_cast<const uint16_t*>(svh),
+                         logical_out, a.out, out_dtype);
+      if (int rc = check_launch("exl3 gemv_output")) return rc;
+    }
   }
   return kOk;
+}
+
+extern "C" int exl3_set_gemv_finish(int mode) {
+  if (mode < -1 || mode > 1) return vq::fail("EXL3 GEMV finish mode must be -1, 0 or 1");
+  exl3::g_finish_mode.store(mode);
+  return vq::kOk;
 }

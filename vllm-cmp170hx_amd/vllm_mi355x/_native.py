@@ -36,6 +36,7 @@ SIGNATURES = {
         c_vp, c_i64, c_vp,                    # workspace, workspace_numel, stream
     ]),
     "exl3_decode": (c_int, [c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp]),
+    "exl3_set_gemv_finish": (c_int, [c_int]),
 }
 
 _lib = None
