@@ -45,9 +45,10 @@ int vllm_mi355x_abi_version(void);
 
 /*
  * FP32 workspace elements exl3_linear_out needs for up to max_rows rows of
- * a padded_in x padded_out matrix: max_rows * (padded_in + padded_out) plus
- * min(max_rows, 8) * (padded_in / 128) * padded_out for the K-split
- * partial sums of the small-M kernel.  Returns -1 (with an error message)
+ * a padded_in x padded_out matrix: max_rows * (padded_in + padded_out + 1)
+ * (large-M path: FP16 high/low activations, FP32 core result, one row
+ * exponent per row) plus min(max_rows, 8) * (padded_in / 128) * padded_out
+ * for the K-split partial sums of the small-M kernel.  Returns -1 (with an error message)
  * for a negative row count or padded sizes that are not positive multiples
  * of 128.
  * Replaces _exl3_C::linear_workspace_size (csrc/exl3/dense.cu:72-78).

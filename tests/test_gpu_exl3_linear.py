@@ -224,3 +224,34 @@ def test_linear_fused_and_separate_finish_agree(ops, device, shape, rows):
     if k * n <= 4096 * 4096:
         want = O.linear_out(x, code, trellis, suh, svh, 8, 2, n, O.FP32)
         _assert_fp32_close(_out_np(results[0]), want, "finish modes")
+
+
+@pytest.mark.parametrize("rows", [9, 64, 300, 513])
+@pytest.mark.parametrize("bits_x2,codebook", [(8, 2), (4, 1), (6, 2), (3, 2)])
+def test_prefill_matches_oracle(ops, device, rows, bits_x2, codebook):
+    """Large-M path (decode to LDS + MFMA); rows are independent, so the
+    oracle checks a sample of them."""
+    print(f"prefill rows={rows} bits_x2={bits_x2} cb={codebook}", flush=True)
+    rng = np.random.default_rng(5000 + rows + bits_x2)
+    k, n = 1024, 2048 + 128  # a partial 256-column tile too
+    trellis, suh, svh = random_matrix(rng, k, n, bits_x2, scales="test")
+    logical_in, logical_out = k - 3, n - 5
+    x, code = random_acts(rng, rows, logical_in, "bf16")
+    got = _out_np(_run_linear(ops, device, trellis, suh, svh, x, code, bits_x2, codebook,
+                              logical_out, torch.float32))
+    sample = sorted({0, 1, rows // 2, rows - 2, rows - 1})
+    want = O.linear_out(x[sample], code, trellis, suh, svh, bits_x2, codebook, logical_out, O.FP32)
+    _assert_fp32_close(got[sample], want, f"prefill rows={rows}")
+
+
+def test_prefill_benchmark_shape(ops, device):
+    """8192 x 28672 at 4 bits, 512 fp16 rows: sampled rows against the oracle."""
+    print("prefill 8192x28672 M=512", flush=True)
+    k, n, rows = 8192, 28672, 512
+    rng = np.random.default_rng(99)
+    trellis, suh, svh = random_matrix(rng, k, n, 8)
+    x, code = random_acts(rng, rows, k, "fp16")
+    got = _out_np(_run_linear(ops, device, trellis, suh, svh, x, code, 8, 2, n, torch.float32))
+    sample = [0, 255, 511]
+    want = O.linear_out(x[sample], code, trellis, suh, svh, 8, 2, n, O.FP32)
+    _assert_fp32_close(got[sample], want, "prefill 8192x28672")

@@ -1,0 +1,291 @@
+// EXL3 dense linear for many rows (prefill), gfx950.
+//
+// Three launches on the caller's stream, like the reference's operator
+// (csrc/exl3/dense.cu:115-148: linear_input, GEMM, linear_output), but the
+// GEMM runs on the matrix cores:
+//  1. prefill_input: one workgroup per row forms t = H128(x * suh) over the
+//     whole row, picks a per-row power-of-two scale from the row maximum, and
+//     writes t as FP16 high and low parts (t * 2^e = hi + lo, ~22 bits).
+//  2. prefill_gemm: 256 x 256 output tiles, 8 wavefronts (4 along M x 2
+//     along N, 64 x 128 each = 2 x 4 v_mfma_f32_32x32x16_f16 tiles).  Per
+//     K step of 32 inputs the workgroup decodes the 32 x 256 weight slab
+//     (32 trellis tiles, two encoder lanes per thread) straight into LDS as
+//     W^T [n][k] in FP16 (exact values), stages the activation tiles, and
+//     every wavefront accumulates hi * W and lo * W into one FP32
+//     accumulator.  The next step's trellis words and activations are
+//     loaded into registers while the current step's MFMAs run.  Rows are
+//     unscaled (2^-e) in the epilogue and written as the FP32 core result.
+//  3. the shared finish: H128 over each 128-column block, times svh,
+//     rounded to the output dtype.
+//
+// Workspace (FP32 elements, rows x ...): [hi | lo halves: padded_in][core
+// result: padded_out] and one int row exponent per row after them.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "exl3_codec.h"
+#include "exl3_internal.h"
+
+namespace exl3 {
+namespace {
+
+constexpr int kBM = 256;            // rows per workgroup
+constexpr int kBN = 256;            // columns per workgroup
+constexpr int kBK = 32;             // inputs per K step (two tile rows)
+constexpr int kGemmThreads = 512;   // 8 wavefronts
+constexpr int kLdsK = kBK + 8;      // LDS row stride in halves (80 bytes)
+
+// ---- 1. activations ----------------------------------------------------------
+
+// One workgroup (256 threads) per row.  Pass 1 finds the row maximum of
+// |t|, pass 2 recomputes t (the same operations, so the same values) and
+// writes the scaled high / low parts.
+__global__ __launch_bounds__(256) void prefill_input(const void* __restrict__ x, int x_dtype,
+                                                     int64_t logical_in, int64_t padded_in,
+                                                     const uint16_t* __restrict__ suh,
+                                                     _Float16* __restrict__ hi,
+                                                     _Float16* __restrict__ lo,
+                                                     int* __restrict__ row_exp) {
+  __shared__ uint32_t row_max;
+  const int64_t r = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t blocks = padded_in / 128;
+  const uint16_t* xs = static_cast<const uint16_t*>(x) + r * logical_in;
+  if (threadIdx.x == 0) row_max = 0u;
+  __syncthreads();
+  auto form = [&](int64_t b, float& v0, float& v1) {
+    const int64_t k0 = b * 128 + lane;
+    const int64_t k1 = k0 + 64;
+    const uint32_t x0 = xs[k0 < logical_in ? k0 : 0];
+    const uint32_t x1 = xs[k1 < logical_in ? k1 : 0];
+    const uint32_t s0 = suh[k0];
+    const uint32_t s1 = suh[k1];
+    v0 = k0 < logical_in ? u16_act(uint16_t(x0), x_dtype) * vq::f16_to_f32(uint16_t(s0)) : 0.0f;
+    v1 = k1 < logical_in ? u16_act(uint16_t(x1), x_dtype) * vq::f16_to_f32(uint16_t(s1)) : 0.0f;
+    vq::h128_wave(v0, v1, lane);
+  };
+  float mx = 0.0f;
+  for (int64_t b = wave; b < blocks; b += 4) {
+    float v0, v1;
+    form(b, v0, v1);
+    mx = fmaxf(mx, fmaxf(fabsf(v0), fabsf(v1)));
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+  if (lane == 0) atomicMax(&row_max, __builtin_bit_cast(uint32_t, mx));
+  __syncthreads();
+  const int e = scale_exponent(row_max);
+  if (threadIdx.x == 0) row_exp[r] = e;
+  _Float16* h = hi + r * padded_in;
+  _Float16* l = lo + r * padded_in;
+  for (int64_t b = wave; b < blocks; b += 4) {
+    float v0, v1;
+    form(b, v0, v1);
+    const float t0 = ldexpf(v0, e);
+    const float t1 = ldexpf(v1, e);
+    const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
+    h[b * 128 + lane] = h0;
+    h[b * 128 + lane + 64] = h1;
+    l[b * 128 + lane] = _Float16(t0 - float(h0));
+    l[b * 128 + lane + 64] = _Float16(t1 - float(h1));
+  }
+}
+
+// ---- 2. decode-to-LDS MFMA GEMM -------------------------------------------------
+
+struct PrefillArgs {
+  const _Float16* hi;     // [rows][kp]
+  const _Float16* lo;     // [rows][kp]
+  const int* row_exp;     // [rows]
+  const uint8_t* trellis;
+  float* core;            // [rows][np]
+  int64_t rows;
+  int64_t kp;
+  int64_t np;
+  int64_t tiles_n;
+};
+
+template <int kBitsX2, int kCodebook, bool kAligned>
+__global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
+  using R = Ring<kBitsX2>;
+  constexpr int kWords = LaneLoad<kBitsX2>::kWords;
+  // W^T slab [n][k] and the two activation tiles [m][k], FP16, 80-byte rows
+  __shared__ __attribute__((aligned(16))) _Float16 w_lds[kBN * kLdsK];
+  __shared__ __attribute__((aligned(16))) _Float16 hi_lds[kBM * kLdsK];
+  __shared__ __attribute__((aligned(16))) _Float16 lo_lds[kBM * kLdsK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave & 3;           // 64-row band
+  const int wn = wave >> 2;          // 128-column band
+  const int64_t row0 = int64_t(blockIdx.x) * kBM;
+  const int64_t col0 = int64_t(blockIdx.y) * kBN;
+  const int64_t tile_col0 = col0 / 16;
+  const int steps = int(a.kp / kBK);
+
+  // activation staging: thread t copies 32 bytes of row t >> 1 of each tile
+  const int st_row = tid >> 1;
+  const int st_half = (tid & 1) * 16;  // halves
+  const int64_t src_row = min(row0 + st_row, a.rows - 1);
+  const _Float16* hi_src = a.hi + src_row * a.kp + st_half;
+  const _Float16* lo_src = a.lo + src_row * a.kp + st_half;
+
+  // decode tasks: (tile row tr, tile column tc, encoder lane L), two per thread
+  int task_tr[2], task_tc[2], task_l[2], off[2][kWords];
+  bool task_on[2];
+  const uint8_t* task_src[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int task = tid + kGemmThreads * i;
+    const int tile = task >> 5;
+    task_tr[i] = tile >> 4;
+    task_tc[i] = tile & 15;
+    task_l[i] = task & 31;
+    task_on[i] = tile_col0 + task_tc[i] < a.tiles_n;
+    int idx[kWords];
+    lane_word_index<kBitsX2>(task_l[i], idx);
+#pragma unroll
+    for (int w = 0; w < kWords; ++w) off[i][w] = 4 * idx[w];
+    const int64_t tc = task_on[i] ? tile_col0 + task_tc[i] : 0;  // absent tiles read tile 0
+    task_src[i] = a.trellis + (int64_t(task_tr[i]) * a.tiles_n + tc) * R::kTileBytes;
+  }
+  const int64_t step_bytes = 2 * a.tiles_n * R::kTileBytes;  // two tile rows
+
+  f32x16_t acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+
+  uint32_t words[2][kWords];
+  u32x4_t hv[2], lv[2];
+  auto fetch = [&](int step) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int w = 0; w < kWords; ++w)
+        words[i][w] = tile_word<kAligned>(task_src[i] + step * step_bytes, off[i][w]);
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      hv[v] = *reinterpret_cast<const u32x4_t*>(hi_src + int64_t(step) * kBK + 8 * v);
+      lv[v] = *reinterpret_cast<const u32x4_t*>(lo_src + int64_t(step) * kBK + 8 * v);
+    }
+  };
+
+  fetch(0);
+  for (int step = 0; step < steps; ++step) {
+    // decode the slab and stage the activations
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint32_t pair[4];
+      decode_words<kBitsX2, kCodebook>(task_l[i], words[i], pair);
+      if (!task_on[i]) pair[0] = pair[1] = pair[2] = pair[3] = 0u;
+      const int L = task_l[i];
+      const int k = task_tr[i] * 16 + 2 * (L & 3);
+      const int n = task_tc[i] * 16 + (L >> 2);
+      // pair p = values (2p, 2p+1): k and k+1 of one column
+      *reinterpret_cast<uint32_t*>(w_lds + n * kLdsK + k) = pair[0];
+      *reinterpret_cast<uint32_t*>(w_lds + n * kLdsK + k + 8) = pair[1];
+      *reinterpret_cast<uint32_t*>(w_lds + (n + 8) * kLdsK + k) = pair[2];
+      *reinterpret_cast<uint32_t*>(w_lds + (n + 8) * kLdsK + k + 8) = pair[3];
+    }
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      *reinterpret_cast<u32x4_t*>(hi_lds + st_row * kLdsK + st_half + 8 * v) = hv[v];
+      *reinterpret_cast<u32x4_t*>(lo_lds + st_row * kLdsK + st_half + 8 * v) = lv[v];
+    }
+    __syncthreads();
+    if (step + 1 < steps) fetch(step + 1);
+    // two k16 chunks: A = activations (rows l % 32, k 8 (l / 32) + i),
+    // B = W (k 8 (l / 32) + i, columns l % 32)
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      const int ko = kc * 16 + 8 * (lane >> 5);
+      half8_t ah[2], al[2], b[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int m = wm * 64 + i * 32 + (lane & 31);
+        ah[i] = *reinterpret_cast<const half8_t*>(hi_lds + m * kLdsK + ko);
+        al[i] = *reinterpret_cast<const half8_t*>(lo_lds + m * kLdsK + ko);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = wn * 128 + j * 32 + (lane & 31);
+        b[j] = *reinterpret_cast<const half8_t*>(w_lds + n * kLdsK + ko);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane l, register r of tile (i, j) is row 8 (r / 4) + 4 (l / 32)
+  // + r % 4, column l % 32
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (row < a.rows) {
+        const int e = a.row_exp[row];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t col = col0 + wn * 128 + j * 32 + (lane & 31);
+          if (col < a.np) a.core[row * a.np + col] = ldexpf(acc[i][j][r], -e);
+        }
+      }
+    }
+  }
+}
+
+template <int kBitsX2, int kCodebook>
+int launch_gemm(bool aligned, const PrefillArgs& a, hipStream_t stream) {
+  const dim3 grid(unsigned((a.rows + kBM - 1) / kBM), unsigned((a.np + kBN - 1) / kBN));
+  if (aligned) {
+    hipLaunchKernelGGL((prefill_gemm<kBitsX2, kCodebook, true>), grid, dim3(kGemmThreads), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((prefill_gemm<kBitsX2, kCodebook, false>), grid, dim3(kGemmThreads), 0, stream, a);
+  }
+  return vq::check_launch("exl3 prefill_gemm");
+}
+
+}  // namespace
+
+int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trellis,
+                   int64_t tiles_k, int64_t tiles_n, const uint16_t* suh, const uint16_t* svh,
+                   int bits_x2, int codebook, int64_t logical_in, int64_t logical_out, void* out,
+                   int out_dtype, float* workspace, hipStream_t stream) {
+  const int64_t kp = tiles_k * 16;
+  const int64_t np = tiles_n * 16;
+  if (rows > 65535 * int64_t(kBM)) return vq::fail("EXL3 linear has too many rows");
+  _Float16* hi = reinterpret_cast<_Float16*>(workspace);
+  _Float16* lo = hi + rows * kp;
+  float* core = workspace + rows * kp;
+  int* row_exp = reinterpret_cast<int*>(core + rows * np);
+  hipLaunchKernelGGL(prefill_input, dim3(unsigned(rows)), dim3(256), 0, stream, x, x_dtype,
+                     logical_in, kp, suh, hi, lo, row_exp);
+  if (int rc = vq::check_launch("exl3 prefill_input")) return rc;
+  PrefillArgs a{hi, lo, row_exp, trellis, core, rows, kp, np, tiles_n};
+  const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
+  int rc = vq::kOk;
+  bool done = false;
+#define VQ_CASE(B, C)                                        \
+  if (!done && bits_x2 == B && codebook == C) {               \
+    rc = launch_gemm<B, C>(aligned, a, stream);               \
+    done = true;                                              \
+  }
+  VQ_EXL3_FORMATS(VQ_CASE)
+#undef VQ_CASE
+  if (!done) return vq::fail("Unsupported EXL3 rate/codebook combination");
+  if (rc != vq::kOk) return rc;
+  return launch_output(core, 1, int(rows), np, svh, logical_out, out, out_dtype, stream);
+}
+
+}  // namespace exl3

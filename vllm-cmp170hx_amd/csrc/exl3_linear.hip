@@ -40,6 +40,7 @@
 #include "../../include/vllm_mi355x.h"
 #include "common.h"
 #include "exl3_codec.h"
+#include "exl3_internal.h"
 
 namespace exl3 {
 namespace {
@@ -48,22 +49,9 @@ using vq::kBF16;
 using vq::kFP16;
 using vq::kFP32;
 
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kMaxGemvRows = 8;
-
-// Formats the format admits (reference: csrc/exl3/gemm.cu:17-20,
-// kernels/exl3/utils.py:283-285): even rates 1..8 bits for both codebooks,
-// and 1.5 / 2.5 / 3.5 bits for mul1.
-bool known_format(int64_t bits_x2, int64_t codebook) {
-  if (codebook == 1) return bits_x2 >= 2 && bits_x2 <= 16 && bits_x2 % 2 == 0;
-  if (codebook == 2) return bits_x2 >= 2 && bits_x2 <= 16 && (bits_x2 % 2 == 0 || bits_x2 <= 7);
-  return false;
-}
-
 
 // Per-rate geometry of the small-M kernel.
 //
@@ -82,17 +70,6 @@ struct Gemv {
   // steps of loads each wavefront keeps in flight
   static constexpr int kDepth = 32 / (2 * kRaw);
 };
-
-// Ring word `w` of a tile.
-template <bool kAligned>
-__device__ __forceinline__ uint32_t tile_word(const uint8_t* tile, int byte_offset) {
-  if constexpr (kAligned) {
-    return *reinterpret_cast<const uint32_t*>(tile + byte_offset);
-  } else {
-    const uint16_t* h = reinterpret_cast<const uint16_t*>(tile + byte_offset);
-    return uint32_t(h[0]) | (uint32_t(h[1]) << 16);
-  }
-}
 
 // Byte offsets (within a tile) of the words encoder lane L needs.
 template <int kBitsX2>
@@ -222,19 +199,6 @@ __device__ __forceinline__ void finish_row_block(const float* __restrict__ parti
   vq::h128_wave(v0, v1, lane);
   if (c0 < logical_out) vq::store_act(out, out_dtype, r * logical_out + c0, v0 * vq::f16_to_f32(uint16_t(scale0)));
   if (c1 < logical_out) vq::store_act(out, out_dtype, r * logical_out + c1, v1 * vq::f16_to_f32(uint16_t(scale1)));
-}
-
-// Power-of-two exponent e so that max * 2^e lies in [2^14, 2^15): the FP16
-// high part then stays below 2^15 and the low part keeps ~11 more bits.
-__device__ __forceinline__ int scale_exponent(uint32_t max_bits) {
-  const int biased = int((max_bits >> 23) & 0xff);
-  if (max_bits == 0u) return 0;
-  const int e = 14 - (biased - 127);
-  return e > 127 ? 127 : (e < -126 ? -126 : e);
-}
-
-__device__ __forceinline__ float u16_act(uint16_t v, int dtype) {
-  return dtype == kBF16 ? vq::bf16_to_f32(v) : vq::f16_to_f32(v);
 }
 
 // Fused finish of one 128-column block by the whole workgroup: thread t
@@ -561,13 +525,22 @@ int dispatch(int64_t bits_x2, int64_t codebook, bool aligned, const GemvArgs* ge
 #define VQ_CASE(B, C)                                                                   \
   if (bits_x2 == B && codebook == C)                                                    \
     return launch_format<B, C>(aligned, gemv, gemv_blocks, grid, lds, stream, trellis, tiles_k, tiles_n, decoded);
-  VQ_CASE(2, 1) VQ_CASE(4, 1) VQ_CASE(6, 1) VQ_CASE(8, 1)
-  VQ_CASE(10, 1) VQ_CASE(12, 1) VQ_CASE(14, 1) VQ_CASE(16, 1)
-  VQ_CASE(2, 2) VQ_CASE(3, 2) VQ_CASE(4, 2) VQ_CASE(5, 2) VQ_CASE(6, 2) VQ_CASE(7, 2)
-  VQ_CASE(8, 2) VQ_CASE(10, 2) VQ_CASE(12, 2) VQ_CASE(14, 2) VQ_CASE(16, 2)
+  VQ_EXL3_FORMATS(VQ_CASE)
 #undef VQ_CASE
   return vq::fail("Unsupported EXL3 rate/codebook combination");
 }
+
+}  // namespace
+
+int launch_output(const float* partial, int splits, int rows, int64_t np, const uint16_t* svh,
+                  int64_t logical_out, void* out, int out_dtype, hipStream_t stream) {
+  const int64_t tasks = int64_t(rows) * (np / 128);
+  hipLaunchKernelGGL(gemv_output, dim3(unsigned((tasks + 3) / 4)), dim3(kThreads), 0, stream, partial,
+                     splits, rows, np, svh, logical_out, out, out_dtype);
+  return vq::check_launch("exl3 gemv_output");
+}
+
+namespace {
 
 int check_padded(int64_t n) {
   if (n <= 0 || n % 128 != 0 || n > INT_MAX) {
@@ -623,7 +596,9 @@ extern "C" int64_t exl3_linear_workspace_size(int64_t max_rows, int64_t padded_i
   const int64_t small = max_rows < exl3::kMaxGemvRows ? max_rows : exl3::kMaxGemvRows;
   // K-split partials of the small-M kernel: padded_in / 128 splits.
   const int64_t splits = exl3::gemv_splits(padded_in);
-  return max_rows * (padded_in + padded_out) + small * splits * padded_out;
+  // Large-M path: rows * (padded_in + padded_out) for the activations and
+  // the core result, plus one int32 row exponent per row.
+  return max_rows * (padded_in + padded_out + 1) + small * splits * padded_out;
 }
 
 extern "C" int exl3_decode(const void* trellis, int64_t tiles_k, int64_t tiles_n,
@@ -695,6 +670,12 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
   if (rows == 0) return kOk;
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rows > exl3::kMaxGemvRows) {
+    return exl3::prefill_linear(x, x_dtype, rows, static_cast<const uint8_t*>(trellis), tiles_k,
+                                tiles_n, static_cast<const uint16_t*>(suh),
+                                static_cast<const uint16_t*>(svh), int(bits_x2), int(codebook),
+                                logical_in, logical_out, out, out_dtype, workspace, s);
+  }
   const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
   const int steps_total = int(padded_in / 32);
   const int blocks = exl3::gemv_blocks(rows < exl3::kMaxGemvRows ? rows : exl3::kMaxGemvRows,
@@ -729,11 +710,11 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
       return rc;
     }
     if (bank < 0) {
-      const int64_t tasks = chunk * col_blocks;
-      hipLaunchKernelGGL(exl3::gemv_output, dim3(unsigned((tasks + 3) / 4)), dim3(exl3::kThreads), 0, s,
-                         partial, int(splits), chunk, padded_out, static_cast<const uint16_t*>(svh),
-                         logical_out, a.out, out_dtype);
-      if (int rc = check_launch("exl3 gemv_output")) return rc;
+      if (int rc = exl3::launch_output(partial, int(splits), chunk, padded_out,
+                                       static_cast<const uint16_t*>(svh), logical_out, a.out,
+                                       out_dtype, s)) {
+        return rc;
+      }
     }
   }
   return kOk;
