@@ -85,6 +85,44 @@ int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t x_cols,
                     float* workspace, int64_t workspace_numel, void* stream);
 
 /*
+ * FP32 workspace elements exl3_moe_out needs: with A = max_rows * topk,
+ * hpad / ipad the hidden / intermediate sizes rounded up to 128,
+ * A * (hpad + 2 * ipad) (activations, gate and up rows) plus the int32
+ * routing table (4 + A rounded up to 4 + 4 A) plus A * max(hpad, ipad) / 128
+ * int32 scale exponents; 0 when local_experts is 0; -1 (with an error
+ * message) for negative counts or nonpositive sizes.
+ * Replaces _exl3_C::moe_workspace_size and moe_workspace_size_v2
+ * (csrc/exl3/moe.cu:304-317, csrc/exl3/moe_v2.cu:2041-2061).
+ */
+int64_t exl3_moe_workspace_size(int64_t max_rows, int64_t hidden_size, int64_t intermediate_size,
+                                int64_t topk, int64_t local_experts);
+
+/*
+ * Routed experts: out[t] = sum over the local routes k of token t, in route
+ * order, of weights[t][k] * down_e(act(gate_e(x[t]), up_e(x[t]))), each
+ * projection an EXL3 linear of the expert (H128(x * suh), trellis, H128,
+ * svh), act = SiLU(min(g, L)) * clamp(u, -L, L) (L = swiglu_limit, 0 = no
+ * clamp).  x / out [rows][hidden] of x_dtype (VQ_BF16 or VQ_FP16; out the
+ * same), topk_ids [rows][topk] int32 (ids64 = 0) or int64 global expert ids
+ * (negative or out of range = not routed here), topk_weights FP32,
+ * expert_map [global_experts] int32 / int64 local ids (-1 = another rank),
+ * packed_ptrs [local][3][3] device addresses {trellis, suh, svh} of gate,
+ * up, down, packed_meta [local][3][4] {padded_in, padded_out, bits_x2,
+ * codebook} (the caller keeps the matrices alive).  bits_x2 = 0 decodes
+ * every expert's own format (moe_out); bits_x2 = 2..8 is the layer's one
+ * mul1 rate (moe_out_v2).  An expert whose matrices are not hpad x ipad /
+ * ipad x hpad, or (bits_x2 > 0) not of that rate, yields NaN rows.
+ * Replaces _exl3_C::moe_out (csrc/exl3/moe.cu:450-458) and
+ * _exl3_C::moe_out_v2 (csrc/exl3/moe_v2.h:19-30; schema module.cpp:19-26).
+ */
+int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hidden, const void* topk_ids,
+                 int ids64, const float* topk_weights, int64_t topk, const int64_t* packed_ptrs,
+                 const int64_t* packed_meta, int64_t local_experts, const void* expert_map,
+                 int map64, int64_t global_experts, int64_t intermediate_size, int64_t bits_x2,
+                 void* out, int out_dtype, float* workspace, int64_t workspace_numel,
+                 float swiglu_limit, void* stream);
+
+/*
  * Test and tuning switch, process-wide: how exl3_linear_out finishes its
  * small-M (<= 8 rows) launches.  -1 (default): the last workgroup of each
  * 128-column block sums the K-split partials and writes the outputs, using

@@ -291,7 +291,8 @@ int oracle_exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hidden
   const int64_t ipad = (intermediate + 127) / 128 * 128;
   const int64_t assignments = rows * topk;
   float** wdec = (float**)calloc((size_t)(local_experts * 3 + 1), sizeof(float*));
-  float* in = (float*)malloc((size_t)hpad * 4);
+  /* in holds an expert input (hpad) and later the down input (ipad) */
+  float* in = (float*)malloc((size_t)(hpad > ipad ? hpad : ipad) * 4);
   float* gate = (float*)malloc((size_t)ipad * 4);
   float* up = (float*)malloc((size_t)ipad * 4);
   float* down = (float*)malloc((size_t)(assignments ? assignments : 1) * hpad * 4);

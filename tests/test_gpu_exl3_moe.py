@@ -1,0 +1,288 @@
+"""EXL3 routed-expert MoE on the GPU (moe_out / moe_out_v2 through the
+_exl3_C operators and the C-ABI) against the CPU oracle's restatement of the
+reference's moe_out_reference (csrc/exl3/reference.cu:371-448).
+
+Bar: the oracle computes the reference's FP32 chain per assignment; the GPU
+runs the expert GEMVs on the matrix cores with the activations split into
+FP16 high/low parts and sums in another order, so the gate/up/down results
+carry a few FP32 roundings of difference that then pass through SiLU, the
+down projection and the routed sum.  Outputs (BF16 / FP16) must agree to
+|err| <= 2^-7 |ref| + 2^-13 rms(ref) (2^-10 rms(ref) where a reaching
+SwiGLU clamp exposes the absolute error of large gate sums), and
+rms(err) <= 2^-10 rms(ref): one output ulp for values next to a rounding
+boundary plus a small absolute term; a wrong decode, index, route or scale
+is off by O(rms).  moe_out and moe_out_v2 run the same arithmetic
+in the same order and must agree bitwise.
+
+Cases follow the reference's tests: expert maps with masked, padding and
+out-of-range ids (test_exl3_kernels.py:242-278), every mul1 rate of the
+fixed-rate variant, the SwiGLU clamp at the DeepSeek routed-expert shape
+(test_exl3_moe_swiglu_clamp.py:51-86), empty and fully masked routes, and
+the operator's error checks.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exl3_oracle as O
+from tests.exl3_cases import random_acts, random_matrix
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from vllm_mi355x.kernels.exl3 import ops as exl3_ops
+    exl3_ops.ensure_extension()
+    return exl3_ops
+
+
+def _dev(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def _out_np(t: torch.Tensor) -> np.ndarray:
+    if t.dtype == torch.bfloat16:
+        return O.bf16_bits_to_f32(t.view(torch.int16).cpu().numpy().view(np.uint16))
+    return t.float().cpu().numpy()
+
+
+def _oracle_f32(out, code):
+    return O.bf16_bits_to_f32(out) if code == O.BF16 else out.astype(np.float32)
+
+
+def _assert_moe_close(actual, expected, name, abs_rms=2.0 ** -13):
+    expected = expected.astype(np.float64)
+    rms = float(np.sqrt(np.mean(expected ** 2)))
+    err = np.abs(actual.astype(np.float64) - expected)
+    bound = 2.0 ** -7 * np.abs(expected) + abs_rms * rms
+    worst = int(np.argmax(err - bound))
+    assert np.isfinite(actual).all(), f"{name}: non-finite output"
+    assert (err <= bound).all(), (
+        f"{name}: err {err.flat[worst]:.3g} > {bound.flat[worst]:.3g} (rms {rms:.3g})")
+    assert np.sqrt(np.mean(err ** 2)) <= 2.0 ** -10 * rms, f"{name}: rms error"
+
+
+class Layer:
+    """Random local experts (gate, up, down) on the host and the device, with
+    the packed_ptrs / packed_meta tables (reference quant.py:1105-1134)."""
+
+    def __init__(self, rng, experts, hidden, intermediate, formats, device, scales="test"):
+        hpad, ipad = -(-hidden // 128) * 128, -(-intermediate // 128) * 128
+        self.host = []
+        for e in range(experts):
+            projections = []
+            for p, (k, n) in enumerate(((hpad, ipad), (hpad, ipad), (ipad, hpad))):
+                bits_x2, codebook = formats[(e + p) % len(formats)]
+                t, u, v = random_matrix(rng, k, n, bits_x2, scales=scales)
+                projections.append((t, u, v, bits_x2, codebook))
+            self.host.append(projections)
+        self.oracle = O.MoELayer(self.host)
+        self.keep = []
+        ptrs, meta = [], []
+        for projections in self.host:
+            ptrs.append([])
+            meta.append([])
+            for t, u, v, bits_x2, codebook in projections:
+                tensors = [_dev(a, device) for a in (t, u, v)]
+                self.keep.append(tensors)
+                ptrs[-1].append([a.data_ptr() for a in tensors])
+                meta[-1].append([u.size, v.size, bits_x2, codebook])
+        self.ptrs = torch.tensor(ptrs, dtype=torch.int64, device=device).reshape(experts, 3, 3)
+        self.meta = torch.tensor(meta, dtype=torch.int64, device=device).reshape(experts, 3, 4)
+
+
+def _run(ops, x, ids, weights, layer, expert_map, intermediate, limit=0.0, bits_x2=None,
+         poison=True):
+    rows, hidden = x.shape
+    size = ops.moe_workspace_size(rows, hidden, intermediate, ids.shape[1], layer.ptrs.shape[0])
+    workspace = torch.empty(max(size, 1), dtype=torch.float32, device=x.device)
+    if poison:
+        workspace.fill_(float("nan"))
+    out = torch.full_like(x, float("nan"))
+    if bits_x2 is None:
+        ops.moe_out(x, ids, weights, layer.ptrs, layer.meta, expert_map, intermediate, out,
+                    workspace, swiglu_limit=limit)
+    else:
+        ops.moe_out_v2(x, ids, weights, layer.ptrs, layer.meta, expert_map, intermediate, bits_x2,
+                       out, workspace, swiglu_limit=limit)
+    torch.cuda.synchronize()
+    return out
+
+
+def _acts(rng, rows, hidden, dtype, device, scale=1.0):
+    a, code = random_acts(rng, rows, hidden, dtype)
+    if scale != 1.0:
+        v = (O.bf16_bits_to_f32(a) if code == O.BF16 else a.astype(np.float32)) * scale
+        a = O.f32_to_bf16_bits(v) if code == O.BF16 else v.astype(np.float16)
+    t = _dev(a, device)
+    return a, code, (t.view(torch.bfloat16) if code == O.BF16 else t)
+
+
+@pytest.mark.parametrize("rows", [1, 5, 33])
+@pytest.mark.parametrize("id_dtype", [torch.int64, torch.int32])
+def test_moe_matches_oracle_with_expert_map_and_masked_routes(ops, device, rows, id_dtype):
+    print(f"moe mixed formats rows={rows} ids={id_dtype}", flush=True)
+    rng = np.random.default_rng(rows)
+    hidden, intermediate, local, global_experts, topk = 256, 200, 4, 8, 3
+    layer = Layer(rng, local, hidden, intermediate, [(10, 2), (7, 2), (6, 1), (16, 2)], device)
+    # global experts 1, 3, 4, 6 are local; the rest belong to another rank
+    expert_map = np.full(global_experts, -1, np.int64)
+    expert_map[[1, 3, 4, 6]] = np.arange(4)
+    ids = rng.integers(-1, global_experts + 1, (rows, topk))
+    ids[0] = [3, -1, global_experts]  # local, padding, out of range
+    weights = rng.uniform(0.05, 0.5, (rows, topk)).astype(np.float32)
+    x_host, code, x = _acts(rng, rows, hidden, "bf16", device)
+    out = _run(ops, x, _dev(ids, device).to(id_dtype), _dev(weights, device), layer,
+               _dev(expert_map, device).to(id_dtype), intermediate)
+    expected = O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map, intermediate)
+    _assert_moe_close(_out_np(out), _oracle_f32(expected, code), f"moe rows={rows}")
+
+
+@pytest.mark.parametrize("bits_x2", [2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("rows,dtype", [(1, "bf16"), (9, "fp16"), (40, "bf16")])
+def test_moe_v2_fixed_rate_matches_oracle_and_moe_out(ops, device, bits_x2, rows, dtype):
+    print(f"moe_v2 bits_x2={bits_x2} rows={rows} {dtype}", flush=True)
+    rng = np.random.default_rng(1000 * bits_x2 + rows)
+    hidden, intermediate, experts, topk = 384, 256, 6, 4
+    layer = Layer(rng, experts, hidden, intermediate, [(bits_x2, 2)], device, scales="sign")
+    ids = np.stack([rng.permutation(experts)[:topk] for _ in range(rows)])
+    weights = rng.random((rows, topk)).astype(np.float32)
+    expert_map = np.arange(experts, dtype=np.int64)
+    x_host, code, x = _acts(rng, rows, hidden, dtype, device)
+    args = (_dev(ids, device), _dev(weights, device), layer, _dev(expert_map, device), intermediate)
+    fixed = _run(ops, x, *args, bits_x2=bits_x2)
+    generic = _run(ops, x, *args)
+    expected = O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map, intermediate,
+                         out_dtype=code)
+    _assert_moe_close(_out_np(fixed), _oracle_f32(expected, code), f"v2 bits_x2={bits_x2}")
+    assert torch.equal(fixed.view(torch.int16), generic.view(torch.int16))
+
+
+def test_moe_skewed_routes_many_tasks(ops, device):
+    """Routes concentrated on a few experts: experts with many 8-row tasks,
+    experts with none, and a task table longer than the expert count."""
+    print("moe skewed", flush=True)
+    rng = np.random.default_rng(7)
+    hidden, intermediate, experts, topk, rows = 256, 384, 16, 4, 48
+    layer = Layer(rng, experts, hidden, intermediate, [(4, 2)], device, scales="sign")
+    p = 1.0 / np.arange(1, experts + 1) ** 1.1
+    p /= p.sum()
+    ids = np.stack([rng.choice(experts, topk, replace=False, p=p) for _ in range(rows)])
+    weights = rng.random((rows, topk)).astype(np.float32)
+    expert_map = np.arange(experts, dtype=np.int64)
+    x_host, code, x = _acts(rng, rows, hidden, "bf16", device)
+    out = _run(ops, x, _dev(ids, device), _dev(weights, device), layer, _dev(expert_map, device),
+               intermediate, bits_x2=4)
+    expected = O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map, intermediate)
+    _assert_moe_close(_out_np(out), _oracle_f32(expected, code), "moe skewed")
+
+
+def test_moe_swiglu_clamp_at_routed_expert_shape(ops, device):
+    """hidden 5120, intermediate 2304, 3 bpw mul1 (reference
+    test_exl3_moe_swiglu_clamp.py): the clamp matches the oracle, a limit
+    no activation reaches equals no limit, a reaching limit changes it."""
+    print("moe swiglu clamp 5120x2304", flush=True)
+    rng = np.random.default_rng(0)
+    hidden, intermediate, experts, topk, rows = 5120, 2304, 4, 2, 4
+    layer = Layer(rng, experts, hidden, intermediate, [(6, 2)], device, scales="sign")
+    ids = np.stack([rng.permutation(experts)[:topk] for _ in range(rows)]).astype(np.int32)
+    weights = rng.random((rows, topk)).astype(np.float32)
+    expert_map = np.arange(experts, dtype=np.int32)
+    x_host, code, x = _acts(rng, rows, hidden, "bf16", device, scale=4.0)
+    args = (_dev(ids, device), _dev(weights, device), layer, _dev(expert_map, device), intermediate)
+    results = {}
+    for limit in (0.0, 0.5, 1e30):
+        results[limit] = _run(ops, x, *args, limit=limit, bits_x2=6)
+    # A reaching clamp keeps only gate values near zero, whose absolute FP32
+    # error is that of the large pre-clamp sums (|g| ~ 300 here, summed in
+    # another order by the oracle's sequential chain): fp16-scale bar,
+    # 2^-10 rms(ref), there.
+    for limit, abs_rms in ((0.0, 2.0 ** -13), (0.5, 2.0 ** -10)):
+        expected = O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map, intermediate,
+                             swiglu_limit=limit)
+        _assert_moe_close(_out_np(results[limit]), _oracle_f32(expected, code), f"limit {limit}",
+                          abs_rms)
+    assert torch.equal(results[1e30], results[0.0])
+    assert not torch.equal(results[0.5], results[0.0])
+
+
+def test_moe_deterministic_and_workspace_independent(ops, device):
+    rng = np.random.default_rng(11)
+    hidden, intermediate, experts, topk, rows = 512, 256, 8, 4, 24
+    layer = Layer(rng, experts, hidden, intermediate, [(6, 2), (4, 2)], device, scales="sign")
+    ids = np.stack([rng.permutation(experts)[:topk] for _ in range(rows)])
+    weights = rng.random((rows, topk)).astype(np.float32)
+    _, _, x = _acts(rng, rows, hidden, "bf16", device)
+    args = (_dev(ids, device), _dev(weights, device), layer,
+            torch.arange(experts, device=device), intermediate)
+    first = _run(ops, x, *args, poison=True)
+    second = _run(ops, x, *args, poison=False)
+    third = _run(ops, x, *args, poison=True)
+    assert torch.equal(first.view(torch.int16), second.view(torch.int16))
+    assert torch.equal(first.view(torch.int16), third.view(torch.int16))
+
+
+def test_moe_fully_masked_and_empty(ops, device):
+    rng = np.random.default_rng(3)
+    hidden, intermediate, experts, topk, rows = 256, 128, 2, 2, 5
+    layer = Layer(rng, experts, hidden, intermediate, [(4, 2)], device)
+    _, _, x = _acts(rng, rows, hidden, "bf16", device)
+    weights = torch.rand(rows, topk, device=device)
+    emap = torch.arange(experts, device=device)
+    # every route masked or remote
+    ids = torch.tensor([[-1, 2]] * rows, device=device)
+    out = _run(ops, x, ids, weights, layer, emap, intermediate)
+    assert torch.equal(out, torch.zeros_like(out))
+    # no local experts at all
+    empty = Layer(rng, 0, hidden, intermediate, [(4, 2)], device)
+    empty.ptrs = torch.zeros(0, 3, 3, dtype=torch.int64, device=device)
+    empty.meta = torch.zeros(0, 3, 4, dtype=torch.int64, device=device)
+    out = _run(ops, x, torch.zeros(rows, topk, dtype=torch.int64, device=device), weights, empty,
+               torch.full((experts,), -1, device=device), intermediate)
+    assert torch.equal(out, torch.zeros_like(out))
+    # zero rows: nothing to do
+    out = _run(ops, x[:0], ids[:0], weights[:0], layer, emap, intermediate)
+    assert out.shape == (0, hidden)
+
+
+def test_moe_expert_geometry_mismatch_gives_nan_rows(ops, device):
+    """An expert whose metadata disagrees with the layer's padded sizes is
+    never read out of bounds: tokens routed to it come out NaN."""
+    rng = np.random.default_rng(5)
+    hidden, intermediate, experts, topk, rows = 256, 128, 3, 1, 6
+    layer = Layer(rng, experts, hidden, intermediate, [(4, 2)], device)
+    layer.meta[1, 0, 0] = 128  # gate claims 128 input rows
+    ids = torch.tensor([[0], [1], [2], [1], [0], [2]], device=device)
+    _, _, x = _acts(rng, rows, hidden, "bf16", device)
+    out = _run(ops, x, ids, torch.ones(rows, topk, device=device), layer,
+               torch.arange(experts, device=device), intermediate).float()
+    bad = (ids[:, 0] == 1)
+    assert torch.isnan(out[bad]).all()
+    assert torch.isfinite(out[~bad]).all()
+
+
+def test_moe_rejects_bad_arguments(ops, device):
+    rng = np.random.default_rng(9)
+    hidden, intermediate, experts, topk, rows = 256, 128, 2, 2, 3
+    layer = Layer(rng, experts, hidden, intermediate, [(4, 2)], device)
+    _, _, x = _acts(rng, rows, hidden, "bf16", device)
+    ids = torch.zeros(rows, topk, dtype=torch.int64, device=device)
+    weights = torch.ones(rows, topk, device=device)
+    emap = torch.arange(experts, device=device)
+    size = ops.moe_workspace_size(rows, hidden, intermediate, topk, experts)
+    ws = torch.empty(size, dtype=torch.float32, device=device)
+    out = torch.empty_like(x)
+    with pytest.raises(RuntimeError, match="workspace"):
+        ops.moe_out(x, ids, weights, layer.ptrs, layer.meta, emap, intermediate, out, ws[:size - 1])
+    with pytest.raises(RuntimeError, match="dtype"):
+        ops.moe_out(x, ids, weights, layer.ptrs, layer.meta, emap, intermediate,
+                    torch.empty(rows, hidden, dtype=torch.float16, device=device), ws)
+    with pytest.raises(RuntimeError, match="swiglu"):
+        ops.moe_out(x, ids, weights, layer.ptrs, layer.meta, emap, intermediate, out, ws,
+                    swiglu_limit=-1.0)
+    with pytest.raises(RuntimeError, match="geometry"):
+        ops.moe_out(x, ids[:1], weights[:1], layer.ptrs, layer.meta, emap, intermediate, out, ws)
+    with pytest.raises(RuntimeError, match="mul1"):
+        ops.moe_out_v2(x, ids, weights, layer.ptrs, layer.meta, emap, intermediate, 9, out, ws)

@@ -1,0 +1,607 @@
+// EXL3 routed-expert MoE for gfx950: the reference's moe_out / moe_out_v2
+// contract (csrc/exl3/moe.cu:304-446, csrc/exl3/moe_v2.h), rebuilt around a
+// grouped small-M MFMA kernel.
+//
+// Launch sequence on the caller's stream (as the reference's run_moe_out):
+//  1. moe_route: one workgroup groups the local assignments by local expert
+//     (counts, scan, sorted list) and cuts each expert's rows into tasks of
+//     at most 8 rows (the per-expert token sort).
+//  2. per projection (gate, up): moe_form builds t = H128(x[a / topk] * suh)
+//     of every local assignment, as FP16 high/low parts in MFMA B-operand
+//     order with a per-(assignment, 128-input block) power-of-two scale;
+//     moe_gemv runs every task against its expert's matrix: one workgroup =
+//     (task, 128 output columns) over the whole K range, trellis streamed
+//     with coalesced loads, decoded in registers, v_mfma_f32_16x16x32_f16,
+//     then the output H128 and svh in the same kernel.
+//  3. moe_form (activation): clamp, SiLU(gate) * up * suh_down, H128 - the
+//     down projection's activations, in the same B-operand form.
+//  4. moe_gemv for the down projection.
+//  5. moe_combine: per token, one FMA per local route in route order with
+//     the routing weight, rounded to the output dtype.
+//
+// Expert formats come from packed_meta on the device.  moe_out decodes any
+// admitted format at run time; moe_out_v2 (one bits_x2 for the layer, mul1)
+// runs the decode specialized for that rate.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+
+#include "../../include/vllm_mi355x.h"
+#include "common.h"
+#include "exl3_codec.h"
+#include "exl3_internal.h"
+
+namespace exl3 {
+namespace {
+
+constexpr int kRouteThreads = 1024;
+constexpr int64_t kMaxRouteExperts = 4096;
+constexpr int kTaskRows = 8;
+
+// Routing of one call (reference: csrc/exl3/moe.cu:19-55).
+struct Routing {
+  const void* ids;          // [rows][topk] int32 or int64 global expert ids
+  const void* expert_map;   // [global] int32 or int64: local id or -1
+  const int64_t* ptrs;      // [local][3][3]: trellis, suh, svh
+  const int64_t* meta;      // [local][3][4]: padded_in, padded_out, bits_x2, codebook
+  int64_t global_experts;
+  int64_t local_experts;
+  int64_t topk;
+  bool ids64;
+  bool map64;
+};
+
+__device__ __forceinline__ int64_t integer_at(const void* p, bool wide, int64_t i) {
+  return wide ? static_cast<const int64_t*>(p)[i] : static_cast<const int32_t*>(p)[i];
+}
+
+__device__ __forceinline__ int64_t local_expert(const Routing& r, int64_t a) {
+  const int64_t g = integer_at(r.ids, r.ids64, a);
+  if (g < 0 || g >= r.global_experts) return -1;
+  const int64_t l = integer_at(r.expert_map, r.map64, g);
+  return l >= 0 && l < r.local_experts ? l : -1;
+}
+
+// Workspace layout (reference sizes: moe.cu:304-317; plus scale exponents).
+struct MoeLayout {
+  int64_t hpad, ipad, assignments;
+  __host__ __device__ int64_t kmax() const { return hpad > ipad ? hpad : ipad; }
+  // FP32 offsets
+  __host__ __device__ int64_t input() const { return 0; }                       // A x hpad
+  __host__ __device__ int64_t gate() const { return assignments * hpad; }        // A x ipad
+  __host__ __device__ int64_t up() const { return gate() + assignments * ipad; } // A x ipad
+  // the down projection's B operands (A x ipad): a region of their own, since
+  // one block's halves would land on gate floats another wavefront still reads
+  __host__ __device__ int64_t act() const { return up() + assignments * ipad; }
+  __host__ __device__ int64_t ints() const { return act() + assignments * ipad; }
+  // int32 offsets from ints(): header[4], sorted[A rounded to 4], tasks[A] (int4),
+  // exponents[A][kmax / 128]
+  __host__ __device__ int64_t sorted() const { return 4; }
+  __host__ __device__ int64_t tasks() const { return 4 + (assignments + 3) / 4 * 4; }
+  __host__ __device__ int64_t exps() const { return tasks() + 4 * assignments; }
+  __host__ __device__ int64_t total() const { return ints() + exps() + assignments * (kmax() / 128); }
+};
+
+// ---- 1. route ------------------------------------------------------------------
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int64_t assignments,
+                                                           int* table) {
+  extern __shared__ int route_shared[];
+  const int experts = int(routing.local_experts);
+  int* count = route_shared;               // counts, then fill cursors
+  int* row_begin = count + experts;
+  int* task_begin = row_begin + experts;   // experts + 1 entries
+  __shared__ int scan_rows[kRouteThreads];
+  __shared__ int scan_tasks[kRouteThreads];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < experts; e += kRouteThreads) count[e] = 0;
+  __syncthreads();
+  for (int64_t a = tid; a < assignments; a += kRouteThreads) {
+    const int64_t e = local_expert(routing, a);
+    if (e >= 0) atomicAdd(&count[e], 1);
+  }
+  __syncthreads();
+  // exclusive scan of (rows, tasks) over experts: each thread a contiguous run
+  const int per = (experts + kRouteThreads - 1) / kRouteThreads;
+  const int e0 = min(experts, tid * per);
+  const int e1 = min(experts, e0 + per);
+  int rows = 0, tasks = 0;
+  for (int e = e0; e < e1; ++e) {
+    rows += count[e];
+    tasks += (count[e] + kTaskRows - 1) / kTaskRows;
+  }
+  scan_rows[tid] = rows;
+  scan_tasks[tid] = tasks;
+  __syncthreads();
+  for (int d = 1; d < kRouteThreads; d <<= 1) {
+    const int r = tid >= d ? scan_rows[tid - d] : 0;
+    const int t = tid >= d ? scan_tasks[tid - d] : 0;
+    __syncthreads();
+    scan_rows[tid] += r;
+    scan_tasks[tid] += t;
+    __syncthreads();
+  }
+  int row_at = scan_rows[tid] - rows;
+  int task_at = scan_tasks[tid] - tasks;
+  for (int e = e0; e < e1; ++e) {
+    const int c = count[e];
+    row_begin[e] = row_at;
+    task_begin[e] = task_at;
+    count[e] = row_at;  // fill cursor
+    row_at += c;
+    task_at += (c + kTaskRows - 1) / kTaskRows;
+  }
+  const int total_rows = scan_rows[kRouteThreads - 1];
+  const int total_tasks = scan_tasks[kRouteThreads - 1];
+  if (tid == 0) {
+    task_begin[experts] = total_tasks;
+    table[0] = total_rows;
+    table[1] = total_tasks;
+  }
+  __syncthreads();
+  int4* task_table = reinterpret_cast<int4*>(table + MoeLayout{0, 0, assignments}.tasks());
+  for (int t = tid; t < total_tasks; t += kRouteThreads) {
+    // last expert whose first task is at or before t (empty experts share
+    // their successor's start, so the search lands on the owner)
+    int lo = 0, hi = experts;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (task_begin[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int first = row_begin[lo] + (t - task_begin[lo]) * kTaskRows;
+    const int end = lo + 1 < experts ? row_begin[lo + 1] : total_rows;
+    task_table[t] = make_int4(lo, first, min(kTaskRows, end - first), 0);
+  }
+  int* sorted = table + 4;
+  for (int64_t a = tid; a < assignments; a += kRouteThreads) {
+    const int64_t e = local_expert(routing, a);
+    if (e >= 0) sorted[atomicAdd(&count[e], 1)] = int(a);
+  }
+}
+
+// ---- 2/3. activations in B-operand form ----------------------------------------
+
+// Half offset, within one assignment's [hi: k halves][lo: k halves], of
+// input k's high part: each 32-input step is [g 0..3][8 slots], slot order
+// {2g, 2g+1, 2g+8, 2g+9} of its two 16-input tile rows.
+__device__ __forceinline__ int64_t b_order(int64_t k) {
+  const int w = int(k & 31);
+  const int g = (w & 7) >> 1;
+  const int slot = 4 * (w >> 4) + (w & 1) + 2 * ((w >> 3) & 1);
+  return (k & ~int64_t(31)) + g * 8 + slot;
+}
+
+// Writes one 128-input block of t (lane l holds inputs l, l + 64), scaled by
+// the block's power-of-two exponent, into an assignment's B-operand arrays.
+__device__ __forceinline__ void store_block(_Float16* dst, int64_t kp, int64_t block, float v0,
+                                            float v1, int* exp_slot, int lane) {
+  float mx = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+  const int e = scale_exponent(__builtin_bit_cast(uint32_t, mx));
+  if (lane == 0) *exp_slot = e;
+  const float t0 = ldexpf(v0, e);
+  const float t1 = ldexpf(v1, e);
+  const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
+  const int64_t k0 = block * 128 + lane;
+  dst[b_order(k0)] = h0;
+  dst[kp + b_order(k0)] = _Float16(t0 - float(h0));
+  dst[b_order(k0 + 64)] = h1;
+  dst[kp + b_order(k0 + 64)] = _Float16(t1 - float(h1));
+}
+
+// kActivate false: gate/up input, t = H128(x[a / topk] * suh_projection);
+// true: down input from the gate/up results (already H128 * svh):
+// clamp, SiLU(g) * u * suh_down, H128, into the act region.
+// One wavefront per (local assignment, 128-input block).  An expert whose
+// matrix is not kp rows long gets NaN operands (its suh is not read).
+template <bool kActivate>
+__global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, int x_dtype,
+                                                int64_t hidden, int64_t intermediate, int projection,
+                                                const int* table, float* ws, MoeLayout lay,
+                                                float limit) {
+  const int lane = threadIdx.x & 63;
+  const int64_t kp = kActivate ? lay.ipad : lay.hpad;
+  const int64_t blocks = kp / 128;
+  const int64_t task = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (task >= int64_t(table[0]) * blocks) return;
+  const int64_t a = table[4 + task / blocks];
+  const int64_t b = task % blocks;
+  const int64_t e = local_expert(routing, a);
+  const int64_t* ptrs = routing.ptrs + e * 9;
+  const int64_t k0 = b * 128 + lane;
+  const int64_t k1 = k0 + 64;
+  float v0, v1;
+  _Float16* dst;
+  int* exps = reinterpret_cast<int*>(ws + lay.ints()) + lay.exps() + a * (lay.kmax() / 128);
+  if (routing.meta[e * 12 + projection * 4] != kp) {
+    dst = reinterpret_cast<_Float16*>(ws + (kActivate ? lay.act() : lay.input()) + a * kp);
+    store_block(dst, kp, b, __builtin_nanf(""), __builtin_nanf(""), exps + b, lane);
+    return;
+  }
+  if constexpr (!kActivate) {
+    const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[projection * 3 + 1]);
+    const uint16_t* row = static_cast<const uint16_t*>(x) + (a / routing.topk) * hidden;
+    const uint32_t x0 = row[k0 < hidden ? k0 : 0], x1 = row[k1 < hidden ? k1 : 0];
+    const uint32_t s0 = suh[k0 < hidden ? k0 : 0], s1 = suh[k1 < hidden ? k1 : 0];
+    v0 = k0 < hidden ? u16_act(uint16_t(x0), x_dtype) * vq::f16_to_f32(uint16_t(s0)) : 0.0f;
+    v1 = k1 < hidden ? u16_act(uint16_t(x1), x_dtype) * vq::f16_to_f32(uint16_t(s1)) : 0.0f;
+    dst = reinterpret_cast<_Float16*>(ws + lay.input() + a * lay.hpad);
+  } else {
+    const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[projection * 3 + 1]);
+    const float* g = ws + lay.gate() + a * lay.ipad;
+    const float* u = ws + lay.up() + a * lay.ipad;
+    float gv[2] = {g[k0], g[k1]};
+    float uv[2] = {u[k0], u[k1]};
+    const uint32_t sd[2] = {suh[k0 < intermediate ? k0 : 0], suh[k1 < intermediate ? k1 : 0]};
+    float v[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t k = i ? k1 : k0;
+      v[i] = 0.0f;
+      if (k < intermediate) {
+        float gg = gv[i], uu = uv[i];
+        if (limit > 0.0f) {
+          gg = fminf(gg, limit);
+          uu = fminf(fmaxf(uu, -limit), limit);
+        }
+        const float silu = gg / (1.0f + expf(-gg));
+        v[i] = (silu * uu) * vq::f16_to_f32(uint16_t(sd[i]));
+      }
+    }
+    v0 = v[0];
+    v1 = v[1];
+    dst = reinterpret_cast<_Float16*>(ws + lay.act() + a * lay.ipad);
+  }
+  vq::h128_wave(v0, v1, lane);
+  store_block(dst, kp, b, v0, v1, exps + b, lane);
+}
+
+// ---- grouped expert GEMV ----------------------------------------------------------
+
+// Decode of encoder lane L of a tile at run-time rate / codebook (moe_out):
+// the scalar ring arithmetic, four window words, values as FP16 pairs.
+__device__ __forceinline__ void decode_runtime(const uint8_t* tile, bool aligned, int bits_x2,
+                                               int codebook, int L, uint32_t (&pair)[4]) {
+  const int whole = bits_x2 >> 1;
+  const int odd = bits_x2 & 1;
+  const int ring = 128 * bits_x2;
+  const int words = 4 * bits_x2;
+  const int start = ((8 * L + 1) * whole + (odd ? 4 * L : 0) - 16 + ring) % ring;
+  int w = start >> 5;
+  uint32_t wd[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wd[i] = aligned ? tile_word<true>(tile, 4 * w) : tile_word<false>(tile, 4 * w);
+    w = w + 1 == words ? 0 : w + 1;
+  }
+  const int shift = start & 31;
+  uint32_t u[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const uint64_t two = (uint64_t(wd[i]) << 32) | wd[i + 1];
+    u[i] = uint32_t(two >> (32 - shift));
+  }
+  uint32_t s[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int o = j * whole + (odd ? (j + 1) / 2 : 0);
+    const int q = o >> 5;
+    const uint32_t hi = q == 0 ? u[0] : (q == 1 ? u[1] : u[2]);
+    const uint32_t lo = q == 0 ? u[1] : u[2];
+    s[j] = uint32_t(((uint64_t(hi) << 32 | lo) >> (48 - (o & 31))) & 0xffffu);
+  }
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    pair[p] = codebook == 1 ? codebook_pair<1>(s[2 * p], s[2 * p + 1])
+                            : codebook_pair<2>(s[2 * p], s[2 * p + 1]);
+  }
+}
+
+struct GemvTask {
+  int expert, first, rows;
+};
+
+// One workgroup = (task, 128 output columns); wavefront w owns the column
+// pair (two tile columns) 4 * blockIdx.x + w over the whole K range.
+// kBitsX2 = 0: the expert's format at run time.
+template <int kBitsX2>
+__global__ __launch_bounds__(256) void moe_gemv(Routing routing, int projection, int64_t kp,
+                                                int64_t np, const int* table, float* ws,
+                                                MoeLayout lay, int64_t in_offset,
+                                                int64_t out_offset) {
+  constexpr bool kFixed = kBitsX2 > 0;
+  constexpr int kDepth = 8;  // steps of trellis loads in flight
+  __shared__ __attribute__((aligned(16))) _Float16 bop[2][4][4][16][8];  // [buf][step][g][col][8]
+  __shared__ int bexp[2][kTaskRows];
+  __shared__ float red[kTaskRows][128];
+
+  const int64_t task = blockIdx.y;
+  if (task >= table[1]) return;
+  const int4 tk = reinterpret_cast<const int4*>(table + lay.tasks())[task];
+  const int expert = tk.x;
+  const int first = tk.y;
+  const int nrows = tk.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 4;
+  const int m = lane & 15;
+  const int L = 4 * (m & 7) + g;
+  const int* sorted = table + 4;
+  const int64_t* ptrs = routing.ptrs + expert * 9 + projection * 3;
+  const int64_t* meta = routing.meta + expert * 12 + projection * 4;
+  const uint8_t* trellis = reinterpret_cast<const uint8_t*>(ptrs[0]);
+  const uint16_t* svh = reinterpret_cast<const uint16_t*>(ptrs[2]);
+  const int64_t tiles_n = meta[1] / 16;
+  const int bits_x2 = kFixed ? kBitsX2 : int(meta[2]);
+  const int codebook = kFixed ? 2 : int(meta[3]);
+  // An expert whose geometry or format disagrees with the call (its matrix
+  // is not kp x np, or not the layer's rate in a fixed-rate launch, or no
+  // admitted format) would be read out of bounds: its rows get NaN instead.
+  const bool bad = meta[0] != kp || meta[1] != np ||
+                   (kFixed ? (meta[2] != kBitsX2 || meta[3] != 2)
+                           : !(meta[3] == 1 ? (bits_x2 >= 2 && bits_x2 <= 16 && bits_x2 % 2 == 0)
+                                            : (meta[3] == 2 && bits_x2 >= 2 && bits_x2 <= 16 &&
+                                               (bits_x2 % 2 == 0 || bits_x2 <= 7))));
+  if (bad) {
+    for (int r = wave; r < nrows; r += 4) {
+      float* dst = ws + out_offset + int64_t(table[4 + first + r]) * np + 128 * int64_t(blockIdx.x);
+      dst[lane] = __builtin_nanf("");
+      dst[lane + 64] = __builtin_nanf("");
+    }
+    return;
+  }
+  const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
+  const int tile_bytes = 16 * bits_x2;
+  const int64_t row_bytes = tiles_n * tile_bytes;
+  const int64_t steps = kp / 32;
+  const int64_t kblocks = kp / 128;
+  // the wavefront's two tiles of tile row 0
+  const uint8_t* chunk = trellis + 2 * (4 * int64_t(blockIdx.x) + wave) * tile_bytes;
+
+  // B-operand staging: thread t copies 16 bytes (step t >> 6, g, column)
+  const int st_step = tid >> 6;
+  const int st_g = (tid >> 4) & 3;
+  const int st_col = tid & 15;
+  const int st_row = min(st_col >> 1, nrows - 1);
+  const int64_t st_a = sorted[first + st_row];
+  const _Float16* st_src = reinterpret_cast<const _Float16*>(ws + in_offset + st_a * kp) +
+                           (st_col & 1) * kp + st_step * 32 + st_g * 8;
+  const int* exps = reinterpret_cast<const int*>(ws + lay.ints()) + lay.exps();
+  const int64_t exp_stride = lay.kmax() / 128;
+  auto stage = [&](int64_t kb, u32x4_t& v, int& e) {
+    v = *reinterpret_cast<const u32x4_t*>(st_src + kb * 128);
+    e = tid < kTaskRows ? exps[int64_t(sorted[first + min(tid, nrows - 1)]) * exp_stride + kb] : 0;
+  };
+
+  // trellis ring (fixed rate: one coalesced dword per lane per tile row, words
+  // gathered with ds_bpermute; run-time rate: decoded from the tile directly)
+  using FR = Ring<kFixed ? kBitsX2 : 8>;
+  constexpr int kWords = LaneLoad<kFixed ? kBitsX2 : 8>::kWords;
+  const int raw_off = lane < 8 * bits_x2 ? 4 * lane : 0;
+  int widx[kWords];
+  lane_word_index<kFixed ? kBitsX2 : 8>(L, widx);
+  int src[kWords];
+#pragma unroll
+  for (int i = 0; i < kWords; ++i) src[i] = 4 * ((m >> 3) * 4 * kBitsX2 + widx[i]);
+  uint32_t raw[kDepth][2];
+  auto load_step = [&](int slot, int64_t s) {
+    if constexpr (kFixed) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint8_t* row = chunk + (2 * s + h) * row_bytes;
+        raw[slot][h] = aligned ? tile_word<true>(row, raw_off) : tile_word<false>(row, raw_off);
+      }
+    }
+  };
+  (void)sizeof(FR);
+
+  f32x4_t acc1 = {}, acc2 = {};
+  float tot1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float tot2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int r_own = m >> 1;
+
+  // prologue: block 0's B operands, the first kDepth steps of trellis
+  u32x4_t sv;
+  int se;
+  stage(0, sv, se);
+#pragma unroll
+  for (int i = 0; i < kDepth; ++i) {
+    if (i < steps) load_step(i, i);
+  }
+  *reinterpret_cast<u32x4_t*>(&bop[0][st_step][st_g][st_col][0]) = sv;
+  if (tid < kTaskRows) bexp[0][tid] = se;
+  __syncthreads();
+
+  for (int64_t s0 = 0; s0 < steps; s0 += kDepth) {
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      const int64_t s = s0 + i;
+      if (s < steps) {
+        const int64_t kb = s >> 2;
+        const int buf = int(kb & 1);
+        if ((s & 3) == 0 && kb + 1 < kblocks) stage(kb + 1, sv, se);
+        uint32_t q0[4], q1[4];
+        if constexpr (kFixed) {
+          uint32_t w0[kWords], w1[kWords];
+#pragma unroll
+          for (int k = 0; k < kWords; ++k) {
+            w0[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][0])));
+            w1[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][1])));
+          }
+          if (s + kDepth < steps) load_step(i, s + kDepth);
+          decode_words<kBitsX2, 2>(L, w0, q0);
+          decode_words<kBitsX2, 2>(L, w1, q1);
+        } else {
+          const uint8_t* t0 = chunk + (2 * s) * row_bytes + (m >> 3) * tile_bytes;
+          decode_runtime(t0, aligned, bits_x2, codebook, L, q0);
+          decode_runtime(t0 + row_bytes, aligned, bits_x2, codebook, L, q1);
+        }
+        const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
+        const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
+        const half8_t b = *reinterpret_cast<const half8_t*>(&bop[buf][s & 3][g][m][0]);
+        const f32x4_t zero = {};
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), b,
+                                                      (s & 3) == 0 ? zero : acc1, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), b,
+                                                      (s & 3) == 0 ? zero : acc2, 0, 0, 0);
+        if ((s & 3) == 3) {
+          const int e = bexp[buf][r_own];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            tot1[k] += ldexpf(acc1[k] + __shfl_xor(acc1[k], 1), -e);
+            tot2[k] += ldexpf(acc2[k] + __shfl_xor(acc2[k], 1), -e);
+          }
+          if (kb + 1 < kblocks) {
+            *reinterpret_cast<u32x4_t*>(&bop[buf ^ 1][st_step][st_g][st_col][0]) = sv;
+            if (tid < kTaskRows) bexp[buf ^ 1][tid] = se;
+          }
+          __syncthreads();
+        }
+      }
+    }
+  }
+
+  // epilogue: rows' 128 columns through LDS, then H128 and svh per row
+  if ((m & 1) == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int row = 4 * g + k;
+      const int col = 32 * wave + (row & 7) + 16 * (row >> 3);
+      red[r_own][col] = tot1[k];
+      red[r_own][col + 8] = tot2[k];
+    }
+  }
+  __syncthreads();
+  for (int r = wave; r < nrows; r += 4) {
+    float v0 = red[r][lane];
+    float v1 = red[r][lane + 64];
+    vq::h128_wave(v0, v1, lane);
+    const int64_t c0 = 128 * int64_t(blockIdx.x) + lane;
+    const int64_t a = sorted[first + r];
+    float* dst = ws + out_offset + a * np;
+    dst[c0] = v0 * vq::f16_to_f32(svh[c0]);
+    dst[c0 + 64] = v1 * vq::f16_to_f32(svh[c0 + 64]);
+  }
+}
+
+// ---- 5. combine ------------------------------------------------------------------
+
+// One thread per (token, column): each local route's down output (already
+// H128 * svh) times its routing weight, one FMA per route in route order.
+__global__ __launch_bounds__(256) void moe_combine(Routing routing, const float* down,
+                                                   const float* weights, int64_t rows,
+                                                   int64_t hidden, int64_t hpad, void* out,
+                                                   int out_dtype, bool any_local) {
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= rows * hidden) return;
+  const int64_t r = idx / hidden;
+  const int64_t c = idx - r * hidden;
+  float sum = 0.0f;
+  if (any_local) {
+    for (int64_t k = 0; k < routing.topk; ++k) {
+      const int64_t a = r * routing.topk + k;
+      if (local_expert(routing, a) >= 0) sum = fmaf(down[a * hpad + c], weights[a], sum);
+    }
+  }
+  vq::store_act(out, out_dtype, idx, sum);
+}
+
+int64_t padded(int64_t n) { return (n + 127) / 128 * 128; }
+
+}  // namespace
+}  // namespace exl3
+
+extern "C" int64_t exl3_moe_workspace_size(int64_t max_rows, int64_t hidden_size,
+                                           int64_t intermediate_size, int64_t topk,
+                                           int64_t local_experts) {
+  if (max_rows < 0 || topk < 0 || local_experts < 0) {
+    vq::fail("EXL3 rows/topk/local_experts must be nonnegative");
+    return -1;
+  }
+  if (hidden_size <= 0 || intermediate_size <= 0 || hidden_size > INT_MAX - 127 ||
+      intermediate_size > INT_MAX - 127) {
+    vq::fail("EXL3 logical dimensions must be positive and fit int32 padding");
+    return -1;
+  }
+  if (local_experts == 0) return 0;
+  const exl3::MoeLayout lay{exl3::padded(hidden_size), exl3::padded(intermediate_size),
+                            max_rows * topk};
+  return lay.total();
+}
+
+extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hidden,
+                            const void* topk_ids, int ids64, const float* topk_weights,
+                            int64_t topk, const int64_t* packed_ptrs, const int64_t* packed_meta,
+                            int64_t local_experts, const void* expert_map, int map64,
+                            int64_t global_experts, int64_t intermediate_size, int64_t bits_x2,
+                            void* out, int out_dtype, float* workspace, int64_t workspace_numel,
+                            float swiglu_limit, void* stream) {
+  using namespace vq;
+  if (x_dtype != kBF16 && x_dtype != kFP16) return fail("x has incorrect dtype");
+  if (out_dtype != x_dtype) return fail("out has incorrect dtype");
+  if (!(swiglu_limit >= 0.0f) || swiglu_limit > 3.4e38f) {
+    return fail("EXL3 swiglu_limit must be finite and nonnegative");
+  }
+  if (rows < 0 || topk < 0 || hidden <= 0) return fail("EXL3 MoE row/topk/output geometry mismatch");
+  if (local_experts > exl3::kMaxRouteExperts) return fail("EXL3 MoE has too many local experts");
+  if (intermediate_size <= 0) return fail("EXL3 logical dimensions must be positive and fit int32 padding");
+  if (bits_x2 != 0 && !exl3::known_format(bits_x2, 2)) {
+    return fail("EXL3 MoE v2 supports mul1 rates only");
+  }
+  const int64_t assignments = rows * topk;
+  if (assignments > INT_MAX) return fail("EXL3 MoE has too many routed assignments");
+  const int64_t need = exl3_moe_workspace_size(rows, hidden, intermediate_size, topk, local_experts);
+  if (need < 0) return kInvalidArgument;
+  if (workspace_numel < need) return fail("EXL3 MoE workspace is too small");
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15) != 0) {
+    return fail("EXL3 MoE workspace must be 16-byte aligned");
+  }
+  if (rows == 0) return kOk;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const exl3::MoeLayout lay{exl3::padded(hidden), exl3::padded(intermediate_size), assignments};
+  exl3::Routing routing{topk_ids, expert_map, packed_ptrs, packed_meta, global_experts,
+                        local_experts, topk, ids64 != 0, map64 != 0};
+  const bool any = local_experts > 0 && assignments > 0;
+  if (any) {
+    int* table = reinterpret_cast<int*>(workspace + lay.ints());
+    hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads),
+                       size_t(3 * local_experts + 1) * sizeof(int), s, routing, assignments, table);
+    if (int rc = check_launch("exl3 moe_route")) return rc;
+    const int64_t max_tasks =
+        std::min<int64_t>(assignments, (assignments + exl3::kTaskRows - 1) / exl3::kTaskRows + local_experts);
+    if (max_tasks > 65535) return fail("EXL3 MoE has too many routed assignments");
+    auto gemv = [&](int projection, int64_t kp, int64_t np, int64_t in_off, int64_t out_off) {
+      const dim3 grid(unsigned(np / 128), unsigned(max_tasks));
+      switch (bits_x2) {
+#define VQ_MOE(B) case B: hipLaunchKernelGGL(exl3::moe_gemv<B>, grid, dim3(256), 0, s, routing, projection, kp, np, table, workspace, lay, in_off, out_off); break;
+        VQ_MOE(2) VQ_MOE(3) VQ_MOE(4) VQ_MOE(5) VQ_MOE(6) VQ_MOE(7) VQ_MOE(8)
+#undef VQ_MOE
+        default:
+          hipLaunchKernelGGL(exl3::moe_gemv<0>, grid, dim3(256), 0, s, routing, projection, kp, np,
+                             table, workspace, lay, in_off, out_off);
+      }
+      return check_launch("exl3 moe_gemv");
+    };
+    if (bits_x2 > 8) return fail("EXL3 MoE v2 supports mul1 rates up to 4 bits");
+    const int64_t form_h = (assignments * (lay.hpad / 128) + 3) / 4;
+    const int64_t form_i = (assignments * (lay.ipad / 128) + 3) / 4;
+    for (int p = 0; p < 2; ++p) {
+      hipLaunchKernelGGL(exl3::moe_form<false>, dim3(unsigned(form_h)), dim3(256), 0, s, routing, x,
+                         x_dtype, hidden, intermediate_size, p, table, workspace, lay, swiglu_limit);
+      if (int rc = check_launch("exl3 moe_form")) return rc;
+      if (int rc = gemv(p, lay.hpad, lay.ipad, lay.input(), p == 0 ? lay.gate() : lay.up())) return rc;
+    }
+    hipLaunchKernelGGL(exl3::moe_form<true>, dim3(unsigned(form_i)), dim3(256), 0, s, routing, x,
+                       x_dtype, hidden, intermediate_size, 2, table, workspace, lay, swiglu_limit);
+    if (int rc = check_launch("exl3 moe_form")) return rc;
+    if (int rc = gemv(2, lay.ipad, lay.hpad, lay.act(), lay.input())) return rc;
+  }
+  const int64_t elems = rows * hidden;
+  hipLaunchKernelGGL(exl3::moe_combine, dim3(unsigned((elems + 255) / 256)), dim3(256), 0, s,
+                     routing, workspace + lay.input(), topk_weights, rows, hidden, lay.hpad, out,
+                     out_dtype, any);
+  return check_launch("exl3 moe_combine");
+}

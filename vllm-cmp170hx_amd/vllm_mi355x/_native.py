@@ -37,6 +37,16 @@ SIGNATURES = {
     ]),
     "exl3_decode": (c_int, [c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp]),
     "exl3_set_gemv_finish": (c_int, [c_int]),
+    "exl3_moe_workspace_size": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "exl3_moe_out": (c_int, [
+        c_vp, c_int, c_i64, c_i64,            # x, x_dtype, rows, hidden
+        c_vp, c_int, c_vp, c_i64,             # topk_ids, ids64, topk_weights, topk
+        c_vp, c_vp, c_i64,                    # packed_ptrs, packed_meta, local_experts
+        c_vp, c_int, c_i64,                   # expert_map, map64, global_experts
+        c_i64, c_i64,                         # intermediate_size, bits_x2
+        c_vp, c_int, c_vp, c_i64,             # out, out_dtype, workspace, workspace_numel
+        ctypes.c_float, c_vp,                 # swiglu_limit, stream
+    ]),
 }
 
 _lib = None

@@ -35,6 +35,22 @@ SCHEMAS = {
         "int codebook) -> int"),
     "exl3_decode": (
         "exl3_decode(Tensor trellis, int bits_x2, int codebook, Tensor(a!) out) -> ()"),
+    "moe_out": (
+        "moe_out(Tensor x, Tensor topk_ids, Tensor topk_weights, "
+        "Tensor packed_ptrs, Tensor packed_meta, Tensor expert_map, "
+        "int intermediate_size, Tensor(a!) out, Tensor(b!) workspace, "
+        "float swiglu_limit=0.0) -> ()"),
+    "moe_out_v2": (
+        "moe_out_v2(Tensor x, Tensor topk_ids, Tensor topk_weights, "
+        "Tensor packed_ptrs, Tensor packed_meta, Tensor expert_map, "
+        "int intermediate_size, int bits_x2, Tensor(a!) out, "
+        "Tensor(b!) workspace, float swiglu_limit=0.0) -> ()"),
+    "moe_workspace_size": (
+        "moe_workspace_size(int max_rows, int hidden_size, int intermediate_size, "
+        "int topk, int local_experts) -> int"),
+    "moe_workspace_size_v2": (
+        "moe_workspace_size_v2(int max_rows, int hidden_size, int intermediate_size, "
+        "int topk, int local_experts) -> int"),
 }
 
 _library = None
@@ -110,6 +126,70 @@ def decode_impl(trellis, bits_x2, codebook, out) -> None:
     _native.check(status)
 
 
+def _check_integer(t, x, name):
+    if t.dtype not in (torch.int32, torch.int64):
+        raise RuntimeError(f"{name} must have int32 or int64 dtype")
+    _check_tensor(t, x, (t.dtype,), name)
+
+
+def _moe_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map, intermediate_size,
+              bits_x2, out, workspace, swiglu_limit) -> None:
+    """Checks of csrc/exl3/moe.cu:323-364, then the native operator."""
+    if not x.is_cuda:
+        raise RuntimeError("EXL3 x must be CUDA")
+    _check_tensor(x, x, (torch.bfloat16, torch.float16), "x")
+    _check_integer(topk_ids, x, "topk_ids")
+    _check_integer(expert_map, x, "expert_map")
+    _check_tensor(topk_weights, x, (torch.float32,), "topk_weights")
+    _check_tensor(packed_ptrs, x, (torch.int64,), "packed_ptrs")
+    _check_tensor(packed_meta, x, (torch.int64,), "packed_meta")
+    _check_tensor(out, x, (x.dtype,), "out")
+    _check_tensor(workspace, x, (torch.float32,), "workspace")
+    if not (x.dim() == 2 and out.dim() == 2 and topk_ids.dim() == 2 and topk_weights.dim() == 2
+            and expert_map.dim() == 1 and packed_ptrs.dim() == 3 and packed_meta.dim() == 3):
+        raise RuntimeError("EXL3 MoE tensor ranks mismatch")
+    rows, hidden = x.shape
+    if not (topk_ids.size(0) == rows and topk_weights.shape == topk_ids.shape
+            and out.shape == x.shape):
+        raise RuntimeError("EXL3 MoE row/topk/output geometry mismatch")
+    experts = packed_ptrs.size(0)
+    if not (packed_ptrs.size(1) == 3 and packed_ptrs.size(2) == 3 and packed_meta.size(0) == experts
+            and packed_meta.size(1) == 3 and packed_meta.size(2) == 4):
+        raise RuntimeError("EXL3 MoE pointer/metadata geometry mismatch")
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        status = lib.exl3_moe_out(
+            x.data_ptr(), _DTYPE_CODES[x.dtype], rows, hidden, topk_ids.data_ptr(),
+            int(topk_ids.dtype == torch.int64), topk_weights.data_ptr(), topk_ids.size(1),
+            packed_ptrs.data_ptr(), packed_meta.data_ptr(), experts, expert_map.data_ptr(),
+            int(expert_map.dtype == torch.int64), expert_map.numel(), int(intermediate_size),
+            int(bits_x2), out.data_ptr(), _DTYPE_CODES[out.dtype], workspace.data_ptr(),
+            workspace.numel(), float(swiglu_limit), _stream(x.device))
+    _native.check(status)
+
+
+def moe_out_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+                 intermediate_size, out, workspace, swiglu_limit=0.0) -> None:
+    _moe_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map, intermediate_size,
+              0, out, workspace, swiglu_limit)
+
+
+def moe_out_v2_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+                    intermediate_size, bits_x2, out, workspace, swiglu_limit=0.0) -> None:
+    if int(bits_x2) <= 0:
+        raise RuntimeError("EXL3 MoE v2 needs the layer's bits_x2")
+    _moe_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map, intermediate_size,
+              bits_x2, out, workspace, swiglu_limit)
+
+
+def moe_workspace_size_impl(max_rows, hidden_size, intermediate_size, topk, local_experts) -> int:
+    size = _native.load().exl3_moe_workspace_size(max_rows, hidden_size, intermediate_size, topk,
+                                                  local_experts)
+    if size < 0:
+        raise RuntimeError(_native.last_error())
+    return int(size)
+
+
 def build_info() -> dict:
     """The handshake the reference's loader compares (module.cpp:91-99);
     ROCm has no CUDA runtime, so cuda_version is 0 and hip_version is set."""
@@ -136,6 +216,10 @@ def register() -> None:
     lib.impl("linear_out", linear_out_impl, "CUDA")
     lib.impl("linear_out_splitk", linear_out_impl, "CUDA")
     lib.impl("exl3_decode", decode_impl, "CUDA")
+    lib.impl("moe_out", moe_out_impl, "CUDA")
+    lib.impl("moe_out_v2", moe_out_v2_impl, "CUDA")
     lib.impl("linear_workspace_size", linear_workspace_size_impl, "CompositeImplicitAutograd")
+    lib.impl("moe_workspace_size", moe_workspace_size_impl, "CompositeImplicitAutograd")
+    lib.impl("moe_workspace_size_v2", moe_workspace_size_impl, "CompositeImplicitAutograd")
     lib.impl("linear_splitk_splits", linear_splitk_splits_impl, "CompositeImplicitAutograd")
     _library = lib

@@ -26,7 +26,8 @@ LINEAR_SCRATCH_ELEMENTS = 8 << 20
 LINEAR_OUT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 _OPERATORS = ("linear_out", "linear_out_splitk", "linear_workspace_size",
-              "linear_splitk_splits", "exl3_decode")
+              "linear_splitk_splits", "exl3_decode", "moe_out", "moe_out_v2",
+              "moe_workspace_size", "moe_workspace_size_v2")
 
 
 def _linear_fake(x, trellis, suh, svh, bits_x2, codebook, logical_in, logical_out, out,
@@ -37,6 +38,21 @@ def _linear_fake(x, trellis, suh, svh, bits_x2, codebook, logical_in, logical_ou
     torch._check(out.shape[1] == logical_out)
     torch._check(x.shape[1] == logical_in)
     torch._check(workspace.dtype == torch.float32)
+
+
+def _moe_fake(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+              intermediate_size, out, workspace, swiglu_limit=0.0):
+    torch._check(x.dtype in (torch.bfloat16, torch.float16))
+    torch._check(out.dtype == x.dtype)
+    torch._check(out.shape == x.shape)
+    torch._check(topk_ids.shape == topk_weights.shape)
+    torch._check(workspace.dtype == torch.float32)
+
+
+def _moe_v2_fake(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+                 intermediate_size, bits_x2, out, workspace, swiglu_limit=0.0):
+    _moe_fake(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+              intermediate_size, out, workspace, swiglu_limit)
 
 
 def _validate_extension() -> None:
@@ -61,6 +77,8 @@ def ensure_extension() -> None:
             f"python vllm-cmp170hx_amd/build.py. Detail: {exc}") from exc
     for name in ("linear_out", "linear_out_splitk"):
         torch.library.register_fake(f"_exl3_C::{name}")(_linear_fake)
+    torch.library.register_fake("_exl3_C::moe_out")(_moe_fake)
+    torch.library.register_fake("_exl3_C::moe_out_v2")(_moe_v2_fake)
     _loaded = True
 
 
@@ -104,6 +122,41 @@ def linear_splitk_splits(rows: int, padded_out: int, sms: int, bits_x2: int,
                          codebook: int) -> int:
     ensure_extension()
     return torch.ops._exl3_C.linear_splitk_splits(rows, padded_out, sms, bits_x2, codebook)
+
+
+@lru_cache(maxsize=None)
+def moe_workspace_size(max_rows: int, hidden_size: int, intermediate_size: int, topk: int,
+                       local_experts: int) -> int:
+    ensure_extension()
+    return torch.ops._exl3_C.moe_workspace_size(max_rows, hidden_size, intermediate_size, topk,
+                                                local_experts)
+
+
+@lru_cache(maxsize=None)
+def moe_workspace_size_v2(max_rows: int, hidden_size: int, intermediate_size: int, topk: int,
+                          local_experts: int) -> int:
+    ensure_extension()
+    return torch.ops._exl3_C.moe_workspace_size_v2(max_rows, hidden_size, intermediate_size, topk,
+                                                   local_experts)
+
+
+def moe_out(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+            intermediate_size: int, out, workspace, swiglu_limit: float = 0.0) -> None:
+    """Routed experts; swiglu_limit > 0 clamps the FP32 gate from above and
+    up on both sides before SiLU(gate) * up (reference ops.py:585-616)."""
+    ensure_extension()
+    torch.ops._exl3_C.moe_out(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+                              intermediate_size, out, workspace, swiglu_limit)
+
+
+def moe_out_v2(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+               intermediate_size: int, bits_x2: int, out, workspace,
+               swiglu_limit: float = 0.0) -> None:
+    """moe_out for a layer whose routed matrices all have rate bits_x2
+    (mul1), with the decode specialized for that rate."""
+    ensure_extension()
+    torch.ops._exl3_C.moe_out_v2(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+                                 intermediate_size, bits_x2, out, workspace, swiglu_limit)
 
 
 def decode(trellis: torch.Tensor, bits_x2: int, codebook: int) -> torch.Tensor:
