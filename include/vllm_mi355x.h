@@ -87,7 +87,7 @@ int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t x_cols,
 /*
  * FP32 workspace elements exl3_moe_out needs: with A = max_rows * topk,
  * hpad / ipad the hidden / intermediate sizes rounded up to 128,
- * A * (hpad + 2 * ipad) (activations, gate and up rows) plus the int32
+ * A * (hpad + 3 * ipad) (activations, gate, up and down-input rows) plus the int32
  * routing table (4 + A rounded up to 4 + 4 A) plus A * max(hpad, ipad) / 128
  * int32 scale exponents; 0 when local_experts is 0; -1 (with an error
  * message) for negative counts or nonpositive sizes.
@@ -143,6 +143,86 @@ int exl3_set_gemv_finish(int mode);
  */
 int exl3_decode(const void* trellis, int64_t tiles_k, int64_t tiles_n, int64_t trellis_words,
                 int64_t bits_x2, int64_t codebook, void* out, void* stream);
+
+/* ---- Marlin-format int4 fused MoE ------------------------------------------
+ *
+ * Weights in vLLM's Marlin packing (csrc/ampere_marlin/decode_orig.cu:10-19):
+ * uint4b8 nibbles, int32 [E][K/16][2N]; group-128 scales [E][K/128][N] of
+ * the activation dtype (VQ_BF16 or VQ_FP16) with the in-chunk column
+ * permutation.  Dequant w = RN((q - 8) * s), one rounding, as the reference.
+ */
+
+/* Modes of marlin_moe_gemm. */
+#define VQ_MARLIN_PARTIAL 0 /* FP32 k-split partials part[ks][slot][N] */
+#define VQ_MARLIN_STORE 1   /* out[slot][n] = RN(sum) */
+#define VQ_MARLIN_TOPK 2    /* out[slot][n] = RN(RN(sum) * RN(topk_w[slot])) */
+
+/*
+ * Grouped expert GEMM over aligned blocks: for every block b < ntpp[0] /
+ * block_size with expert e = expert_ids[b] in [0, experts), every routed
+ * slot sid = sorted[b * block_size + t] < n_slots, and every column n < N:
+ * sum over k < K (K-split into ksplit equal ranges of whole 128-k groups)
+ * of a[sid / top_k][k] * w_e[k][n], FP32 on the matrix cores.  a: rows of
+ * a_stride elements (a_stride % 8 == 0), at least ceil(n_slots / top_k)
+ * rows; block_size a multiple of 8 up to 64.  part needs ksplit * n_slots *
+ * N floats (mode PARTIAL); out rows of out_stride elements (STORE / TOPK,
+ * ksplit 1).  Rows of unrouted slots are left untouched.
+ * Replaces _ampere_marlin_C::decode_gemm_orig / decode_gemm_v2
+ * (csrc/ampere_marlin/decode_orig.cu:361-390, decode_v2.cu:395-399) and
+ * prefill_tile_gemm (csrc/ampere_marlin/prefill_tiles.cu:12-26, upstream
+ * moe_wna16_marlin_gemm).
+ */
+int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
+                    const int32_t* w, const void* scales, int64_t experts, const int32_t* sorted,
+                    int64_t sorted_numel, const int32_t* expert_ids, int64_t expert_ids_numel,
+                    const int32_t* ntpp, const float* topk_w, int64_t top_k, int64_t n_slots,
+                    int64_t K, int64_t N, int64_t block_size, int mode, int64_t ksplit,
+                    float* part, int64_t part_numel, void* out, int64_t out_stride,
+                    int64_t out_rows, void* stream);
+
+/*
+ * SwiGLU of the w13 partials: G / U = RN(sum over ks in order of
+ * part[ks][slot][n] / [..][Nh + n]), h[slot][n] = RN(RN(SiLU(min(G, L))) *
+ * clamp(U, -L, L)) (limit = +inf: no clamp); slots with ids[slot] < 0 are
+ * skipped.  Replaces _ampere_marlin_C::decode_act_orig
+ * (csrc/ampere_marlin/decode_orig.cu:272-305, :392-401).
+ */
+int marlin_moe_act(const float* part, const int32_t* ids, int64_t ksplit, int64_t n_slots,
+                   int64_t nh, float limit, void* h, int act_dtype, void* stream);
+
+/*
+ * The dequantized weights of one packed matrix, out[k][n] (K x N, the
+ * activation dtype), through the GEMM's own fragment and dequant path.
+ * The inspection form of the decode marlin_moe_gemm fuses; the reference's
+ * is csrc/ampere_marlin/decode_orig.cu:56-67 (upstream dequant.h).
+ */
+int marlin_dequant(const int32_t* w, const void* scales, int act_dtype, int64_t K, int64_t N,
+                   void* out, void* stream);
+
+/*
+ * out[t][c] = RN(FP32 sum over slots k = 0..topk-1, in order, of
+ * in[t][k][c]); with ids, slots whose id is outside [0, experts) add
+ * nothing.  Replaces moe_sum (vllm_sm80/kernels/moe/routing.py:579-600,
+ * upstream _moe_C::moe_sum).
+ */
+int moe_sum(const void* in, int act_dtype, int64_t tokens, int64_t topk, int64_t hidden,
+            const int32_t* ids, int64_t experts, void* out, void* stream);
+
+/*
+ * Deterministic block alignment of routed rows: rows grouped by (mapped)
+ * expert in ascending expert order, ascending flat index inside an expert,
+ * each expert padded to a multiple of block_size with the sentinel numel;
+ * expert_ids[b] = expert of block b (-1 past the padded total); ntpp[0] =
+ * padded total.  Ids outside [0, num_experts) and experts mapped to -1 are
+ * dropped.  sorted needs numel + num_experts * (block_size - 1) entries
+ * (min(numel * block_size, that) when numel < num_experts).
+ * Replaces moe_align_block_size (vllm_sm80/kernels/moe/align.py:233-273,
+ * spec tests/kernels/moe_align_reference.py:18-70).
+ */
+int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
+                         int64_t block_size, const int32_t* expert_map, int32_t* sorted,
+                         int64_t sorted_numel, int32_t* expert_ids, int64_t expert_ids_numel,
+                         int32_t* ntpp, void* stream);
 
 #ifdef __cplusplus
 }

@@ -22,7 +22,7 @@ PACKAGE = os.path.join(HERE, "vllm_mi355x")
 LIBRARY = os.path.join(PACKAGE, "libvllm_mi355x.so")
 OBJDIR = os.path.join(HERE, "_build")
 
-SOURCES = ["common.cpp", "exl3_linear.hip", "exl3_gemm.hip", "exl3_moe.hip"]
+SOURCES = ["common.cpp", "exl3_linear.hip", "exl3_gemm.hip", "exl3_moe.hip", "marlin_moe.hip"]
 
 ARCH = "gfx950"
 COMMON_FLAGS = [

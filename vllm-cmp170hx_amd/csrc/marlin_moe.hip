@@ -1,0 +1,757 @@
+// Marlin-format int4 (uint4b8, group 128) fused MoE for gfx950: the grouped
+// expert GEMM, the SwiGLU activation, the deterministic token alignment and
+// the slot-order top-k sum behind the reference's _ampere_marlin_C operators
+// (csrc/ampere_marlin/decode_orig.cu, prefill_tiles.cu) and the upstream
+// moe_align_block_size / moe_sum they are called with.
+//
+// Weights stay in vLLM's Marlin packing (decode_orig.cu:10-19): int32
+// [E][K/16][2N], where each 16 (k) x 64 (n) tile of a k16 row is 32 x 16
+// bytes, one 16-byte fragment per NVIDIA lane (c = l % 4, g = l / 4) holding
+// four 16 x 16 blocks' nibbles for k {2c, 2c+1, 2c+8, 2c+9} and n {g, g+8}.
+//
+// gfx950 mapping (one wavefront = one 64-column tile):
+//  * a step is 32 k (two k16 rows); lane l = 16 q + r loads, coalesced, the
+//    16-byte fragment of NVIDIA lane 4 (r % 8) + q from k16 row r / 8 of the
+//    pair, so the wavefront reads 1 KB of contiguous weights per step;
+//  * lanes r and r + 8 swap words over DPP (row_ror:8) and each keeps, by
+//    one v_perm_b32 per word, the bytes of its own output column: lane r then
+//    holds 8 nibbles = one v_mfma_f32_16x16x32_{f16,bf16} A operand (row
+//    r = column 16 j + r of the tile, k 2q, 2q+1, 2q+8, 2q+9 and the same + 16);
+//  * dequant w = RN_act((q - 8) * s) exactly as the reference rounds it
+//    (decode_orig.cu:56-67): FP16 by the 0x6400 magic (exact q - 8) and one
+//    packed multiply; BF16 by an exact FP32 FMA and v_cvt_pk_bf16_f32;
+//  * the tokens of an aligned block (up to 64, in 16-token sub-blocks) are the
+//    MFMA's N dimension: activations are staged in LDS in the same k order,
+//    so one ds_read_b128 gives a lane its B operand; sub-blocks with no
+//    routed token are skipped;
+//  * a workgroup is (aligned block, 1 or 4 tiles, k-split); with one tile its
+//    four wavefronts split K and sum through LDS in a fixed order.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <type_traits>
+
+#include "../../include/vllm_mi355x.h"
+#include "common.h"
+
+namespace marlin {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int kMaxBlock = 64;  // tokens per aligned block (upstream block sizes 8..64)
+
+enum Mode : int { kPartial = 0, kStore = 1, kTopk = 2 };
+
+struct GemmArgs {
+  const uint16_t* a;      // activations, row r at a + r * a_stride
+  int64_t a_stride;
+  const u32x4_t* w;       // [E][K/16][N/2] 16-byte fragments
+  const uint16_t* s;      // [E][K/128][N] group scales (permuted columns)
+  const int32_t* sorted;  // [blocks * bs] routed slot ids, sentinel >= n_slots
+  const int32_t* eids;    // [blocks] expert of each block, -1 = none
+  const int32_t* ntpp;    // [1] padded routed rows
+  const float* topk_w;    // [n_slots] router weights (kTopk)
+  float* part;            // kPartial: [ksplit][n_slots][N]
+  uint16_t* out;          // kStore / kTopk: row slot at out + slot * out_stride
+  int64_t out_stride;
+  int top_k, n_slots, K, N, bs, experts, groups_per_split;
+};
+
+// ---- dequant ---------------------------------------------------------------------
+
+// One word of 8 nibbles (bytes [A.x, B.x, A.y, B.y] of the two k16 rows A and
+// B, x / y the nibble pairs of k {2q, 2q+8} / {2q+1, 2q+9}) -> four packed
+// pairs, k order (2q, 2q+1) (2q+8, 2q+9) (16+2q, 17+2q) (24+2q, 25+2q).
+// FP16: 0x6400 | nibble is 1024 + q exactly, minus 1032 is q - 8 exactly,
+// times (s, s) rounds once.
+__device__ __forceinline__ void dequant_f16(uint32_t c, uint32_t s2, uint32_t (&o)[4]) {
+  const half2_t s = __builtin_bit_cast(half2_t, s2);
+  const half2_t bias = {_Float16(1032.0f), _Float16(1032.0f)};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t m = ((c >> (4 * i)) & 0x000f000fu) | 0x64006400u;
+    o[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, m) - bias) * s);
+  }
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  const bf16x2_t v = {__bf16(lo), __bf16(hi)};  // v_cvt_pk_bf16_f32, round to nearest even
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// BF16: (q - 8) * s is exact in FP32 (4 x 8 significant bits), so
+// fma(q, s, -8 s) is that product and the conversion rounds once.
+__device__ __forceinline__ void dequant_bf16(uint32_t c, float s, float ns8, uint32_t (&o)[4]) {
+  const uint32_t lo = c & 0x0f0f0f0fu;         // [2q, 16+2q, 2q+1, 17+2q]
+  const uint32_t hi = (c >> 4) & 0x0f0f0f0fu;  // [2q+8, 24+2q, 2q+9, 25+2q]
+  auto two = [&](uint32_t w, int b0, int b1) {
+    const float x0 = __builtin_fmaf(float((w >> (8 * b0)) & 0xffu), s, ns8);
+    const float x1 = __builtin_fmaf(float((w >> (8 * b1)) & 0xffu), s, ns8);
+    return pack_bf16(x0, x1);
+  };
+  o[0] = two(lo, 0, 2);
+  o[1] = two(hi, 0, 2);
+  o[2] = two(lo, 1, 3);
+  o[3] = two(hi, 1, 3);
+}
+
+// The 16-byte fragment of this lane's NVIDIA lane in k16 row 2 step + r / 8.
+__device__ __forceinline__ const u32x4_t* fragment(const u32x4_t* w_e, int64_t N, int tile, int step,
+                                                   int lane) {
+  const int q = lane >> 4, r = lane & 15;
+  const int64_t krow = 2 * int64_t(step) + (r >> 3);
+  return w_e + krow * (N >> 1) + tile * 32 + 4 * (r & 7) + q;
+}
+
+// Swap with lane r ^ 8 of the 16-lane row and keep this lane's column's bytes.
+__device__ __forceinline__ uint32_t combine(uint32_t own, int lane) {
+  const uint32_t other = uint32_t(__builtin_amdgcn_update_dpp(0, int(own), 0x128, 0xf, 0xf, false));
+  // r < 8: own = row A, half 0 (bytes 0, 2); r >= 8: own = row B, half 1 (bytes 1, 3)
+  return __builtin_amdgcn_perm(other, own, (lane & 8) ? 0x03070105u : 0x06020400u);
+}
+
+template <bool kBF16>
+struct Scales {
+  uint32_t pair[4];  // FP16: (s_j, s_j)
+  float s[4], ns8[4];  // BF16: s_j, -8 s_j
+  __device__ __forceinline__ void set(u32x4_t v, int lane) {
+    const bool high = (lane & 8) != 0;  // column g + 8: the odd stored position
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (kBF16) {
+        s[j] = __builtin_bit_cast(float, high ? (v[j] & 0xffff0000u) : (v[j] << 16));
+        ns8[j] = -8.0f * s[j];
+      } else {
+        pair[j] = __builtin_amdgcn_perm(v[j], v[j], high ? 0x03020302u : 0x01000100u);
+      }
+    }
+  }
+  __device__ __forceinline__ u32x4_t operand(uint32_t c, int j) const {
+    uint32_t o[4];
+    if constexpr (kBF16) {
+      dequant_bf16(c, s[j], ns8[j], o);
+    } else {
+      dequant_f16(c, pair[j], o);
+    }
+    return u32x4_t{o[0], o[1], o[2], o[3]};
+  }
+};
+
+template <bool kBF16>
+__device__ __forceinline__ f32x4_t mfma(u32x4_t a, u32x4_t b, f32x4_t c) {
+  if constexpr (kBF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                                  __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+  }
+}
+
+template <bool kBF16>
+__device__ __forceinline__ float round_act(float v) {
+  if constexpr (kBF16) {
+    return vq::bf16_to_f32(vq::f32_to_bf16(v));
+  } else {
+    return float(_Float16(v));
+  }
+}
+
+template <bool kBF16>
+__device__ __forceinline__ uint16_t to_act(float v) {
+  if constexpr (kBF16) {
+    return vq::f32_to_bf16(v);
+  } else {
+    return __builtin_bit_cast(uint16_t, _Float16(v));
+  }
+}
+
+// ---- grouped GEMM -----------------------------------------------------------------
+
+// kWavesK: wavefronts splitting K inside a workgroup (4: one tile per
+// workgroup; 1: four tiles); kSub: 16-token sub-blocks (block size <= 16 kSub).
+template <bool kBF16, int kWavesK, int kSub, int kMode>
+__global__ __launch_bounds__(kThreads) void marlin_gemm(GemmArgs g) {
+  constexpr int kTilesWG = 4 / kWavesK;
+  constexpr int kRounds = kWavesK == 1 ? 2 : 1;     // groups per wavefront per chunk
+  constexpr int kChunkGroups = kWavesK * kRounds;   // 128-k groups per LDS chunk
+  constexpr int kChunkSteps = 4 * kChunkGroups;
+  constexpr int kTok = 16 * kSub;
+  constexpr int kStepBytes = 4 * kTok * 16;          // [q][token][8 halves]
+  constexpr int kChunkBytes = kChunkSteps * kStepBytes;
+  constexpr int kStage = kChunkSteps * kTok * 4 / kThreads;  // 16-byte loads per thread
+  static_assert(kStage >= 1 && kChunkSteps * kTok * 4 % kThreads == 0, "staging split");
+  constexpr int kRedBytes = (kWavesK - 1) * 64 * 4 * kSub * 16 * kTilesWG;
+  constexpr int kLds = 2 * kChunkBytes > kRedBytes ? 2 * kChunkBytes : kRedBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
+  __shared__ int s_slot[kMaxBlock];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wk = wave % kWavesK;
+  const int wt = wave / kWavesK;
+  const int tile = int(blockIdx.x) * kTilesWG + wt;
+  const bool tile_ok = tile < (g.N >> 6);
+  const int b = blockIdx.y;
+  const int ks = blockIdx.z;
+  if (int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
+  const int e = g.eids[b];
+  if (e < 0 || e >= g.experts) return;
+  if (tid < kMaxBlock) {
+    int slot = -1;
+    if (tid < g.bs) {
+      const int sid = g.sorted[int64_t(b) * g.bs + tid];
+      if (sid >= 0 && sid < g.n_slots) slot = sid;
+    }
+    s_slot[tid] = slot;
+  }
+  __syncthreads();
+  const uint64_t valid = __ballot(s_slot[lane] >= 0);
+  if (valid == 0) return;
+  const int nvalid = 64 - __builtin_clzll(valid);
+  const int nsub = (nvalid + 15) >> 4;  // sub-blocks holding a routed token
+
+  const int gps = g.groups_per_split;
+  const int g0 = ks * gps;
+  const int nch = (gps + kChunkGroups - 1) / kChunkGroups;
+  const int64_t groups_total = g.K >> 7;
+  const u32x4_t* w_e = g.w + int64_t(e) * (g.K >> 4) * (g.N >> 1);
+  const uint16_t* s_e = g.s + int64_t(e) * groups_total * g.N;
+
+  // activation staging: thread item i -> (step, token, 16-byte segment)
+  u32x4_t stage_regs[kStage];
+  auto stage_load = [&](int c) {
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+      const int i = tid + u * kThreads;
+      const int seg = i & 3;
+      const int tok = (i >> 2) % kTok;
+      const int st = i / (4 * kTok);
+      const int grp = g0 + c * kChunkGroups + (st >> 2);
+      const int slot = tok < kMaxBlock ? s_slot[tok] : -1;
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (slot >= 0 && grp < g0 + gps) {
+        const int64_t row = slot / g.top_k;
+        const int64_t k = int64_t(grp) * 128 + (st & 3) * 32 + 8 * seg;
+        v = *reinterpret_cast<const u32x4_t*>(g.a + row * g.a_stride + k);
+      }
+      stage_regs[u] = v;
+    }
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+      const int i = tid + u * kThreads;
+      const int seg = i & 3;
+      const int tok = (i >> 2) % kTok;
+      const int st = i / (4 * kTok);
+      uint8_t* base = lds + buf * kChunkBytes + st * kStepBytes + tok * 16 + 4 * seg;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        *reinterpret_cast<uint32_t*>(base + d * kTok * 16) = stage_regs[u][d];
+      }
+    }
+  };
+
+  // this wavefront's groups: i -> chunk i / kRounds, round i % kRounds
+  auto group_of = [&](int i) { return g0 + (i / kRounds) * kChunkGroups + (i % kRounds) * kWavesK + wk; };
+  const int my_groups = nch * kRounds;
+  u32x4_t ring_w[2][4];
+  u32x4_t ring_s[2];
+  auto load_group = [&](int slot, int i) {
+    const int grp = group_of(i);
+    if (tile_ok && grp < g0 + gps) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) ring_w[slot][st] = *fragment(w_e, g.N, tile, 4 * grp + st, lane);
+      ring_s[slot] = *reinterpret_cast<const u32x4_t*>(s_e + int64_t(grp) * g.N + tile * 64 +
+                                                       8 * (lane & 7));
+    }
+  };
+
+  f32x4_t acc[4][kSub];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int sb = 0; sb < kSub; ++sb) acc[j][sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  load_group(0, 0);
+  stage_load(0);
+  stage_store(0);
+  if (nch > 1) stage_load(1);
+  __syncthreads();
+
+  const int q = lane >> 4;
+  const int col = lane & 15;
+  // group i of this wavefront from ring slot kSlot (static: the ring stays in
+  // registers); the last group of a chunk refills the other LDS buffer
+  auto body = [&](int i, auto slot_tag) {
+    constexpr int kSlot = decltype(slot_tag)::value;
+    const int c = i / kRounds;
+    const int r = i % kRounds;
+    const int grp = group_of(i);
+    if (i + 1 < my_groups) load_group(kSlot ^ 1, i + 1);
+    if (tile_ok && grp < g0 + gps) {
+      const uint8_t* abuf = lds + (c & 1) * kChunkBytes;
+      Scales<kBF16> sc;
+      sc.set(ring_s[kSlot], lane);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const u32x4_t v = ring_w[kSlot][st];
+        const int stepc = (r * kWavesK + wk) * 4 + st;
+        u32x4_t bop[kSub];
+#pragma unroll
+        for (int sb = 0; sb < kSub; ++sb) {
+          if (sb < nsub) {
+            bop[sb] = *reinterpret_cast<const u32x4_t*>(abuf + stepc * kStepBytes +
+                                                        (q * kTok + 16 * sb + col) * 16);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x4_t a = sc.operand(combine(v[j], lane), j);
+#pragma unroll
+          for (int sb = 0; sb < kSub; ++sb) {
+            if (sb < nsub) acc[j][sb] = mfma<kBF16>(a, bop[sb], acc[j][sb]);
+          }
+        }
+      }
+    }
+    if (r == kRounds - 1) {
+      if (c + 1 < nch) stage_store((c + 1) & 1);
+      if (c + 2 < nch) stage_load(c + 2);
+      __syncthreads();
+    }
+  };
+  for (int i = 0; i < my_groups; i += 2) {
+    body(i, std::integral_constant<int, 0>{});
+    if (i + 1 < my_groups) body(i + 1, std::integral_constant<int, 1>{});
+  }
+
+  // split-K inside the workgroup: wavefronts 1.. of a tile hand their sums to
+  // wavefront 0 of it, which adds them in order 1, 2, 3
+  if constexpr (kWavesK > 1) {
+    float* red = reinterpret_cast<float*>(lds);
+    auto red_at = [&](int from, int j, int sb) {
+      return red + ((((wt * (kWavesK - 1) + from - 1) * 4 + j) * kSub + sb) * 64 + lane) * 4;
+    };
+    if (wk > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int sb = 0; sb < kSub; ++sb)
+          if (sb < nsub) *reinterpret_cast<f32x4_t*>(red_at(wk, j, sb)) = acc[j][sb];
+    }
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int from = 1; from < kWavesK; ++from)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int sb = 0; sb < kSub; ++sb)
+          if (sb < nsub) acc[j][sb] += *reinterpret_cast<const f32x4_t*>(red_at(from, j, sb));
+  }
+  if (!tile_ok) return;
+
+  // C fragment: lane holds columns 16 j + 4 q .. +3 of token 16 sb + col
+#pragma unroll
+  for (int sb = 0; sb < kSub; ++sb) {
+    if (sb >= nsub) continue;
+    const int slot = s_slot[16 * sb + col];
+    if (slot < 0) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = int64_t(tile) * 64 + 16 * j + 4 * q;
+      const f32x4_t v = acc[j][sb];
+      if constexpr (kMode == kPartial) {
+        *reinterpret_cast<f32x4_t*>(g.part + (int64_t(ks) * g.n_slots + slot) * g.N + n) = v;
+      } else {
+        float x[4] = {v[0], v[1], v[2], v[3]};
+        if constexpr (kMode == kTopk) {
+          const float w = round_act<kBF16>(g.topk_w[slot]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) x[u] = round_act<kBF16>(x[u]) * w;  // exact product
+        }
+        const u32x2_t packed = {uint32_t(to_act<kBF16>(x[0])) | (uint32_t(to_act<kBF16>(x[1])) << 16),
+                                uint32_t(to_act<kBF16>(x[2])) | (uint32_t(to_act<kBF16>(x[3])) << 16)};
+        *reinterpret_cast<u32x2_t*>(g.out + int64_t(slot) * g.out_stride + n) = packed;
+      }
+    }
+  }
+}
+
+// ---- dequant of one matrix (the GEMM's own operand path, for exact checks) ----
+
+// W [K][N] in the activation dtype: one wavefront per (step, tile), the same
+// fragment load, lane exchange and dequant as marlin_gemm, each operand
+// element written at its (k, n).
+template <bool kBF16>
+__global__ __launch_bounds__(kThreads) void marlin_dequant_kernel(const u32x4_t* w, const uint16_t* s,
+                                                                  int K, int N, uint16_t* out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int tiles = N >> 6;
+  if (item >= int64_t(K >> 5) * tiles) return;
+  const int step = int(item / tiles);
+  const int tile = int(item % tiles);
+  Scales<kBF16> sc;
+  sc.set(*reinterpret_cast<const u32x4_t*>(s + int64_t(step >> 2) * N + tile * 64 + 8 * (lane & 7)),
+         lane);
+  const u32x4_t v = *fragment(w, N, tile, step, lane);
+  const int q = lane >> 4, r = lane & 15;
+  const int kofs[8] = {2 * q, 2 * q + 1, 2 * q + 8, 2 * q + 9, 16 + 2 * q, 17 + 2 * q, 24 + 2 * q, 25 + 2 * q};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const u32x4_t a = sc.operand(combine(v[j], lane), j);
+    const int64_t n = int64_t(tile) * 64 + 16 * j + r;
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      const uint32_t word = a[h >> 1];
+      out[(int64_t(step) * 32 + kofs[h]) * N + n] = uint16_t((h & 1) ? word >> 16 : word & 0xffffu);
+    }
+  }
+}
+
+// ---- activation (decode_orig.cu:272-305) -----------------------------------------
+
+// h[slot][n] = RN(RN(SiLU(min(G, L))) * clamp(U, -L, L)), G and U the
+// activation-dtype roundings of the k-split FP32 sums in ks order; slots
+// whose routed id is negative are skipped.
+template <bool kBF16>
+__global__ __launch_bounds__(kThreads) void marlin_act_kernel(const float* part, const int32_t* ids,
+                                                              int ksplit, int n_slots, int nh,
+                                                              float limit, uint16_t* h) {
+  const int slot = blockIdx.y;
+  const int n = int(blockIdx.x) * kThreads + threadIdx.x;
+  if (n >= nh || ids[slot] < 0) return;
+  const int64_t plane = int64_t(n_slots) * 2 * nh;
+  const float* p = part + int64_t(slot) * 2 * nh + n;
+  float gs = 0.0f, us = 0.0f;
+  for (int k = 0; k < ksplit; ++k) {
+    gs += p[k * plane];
+    us += p[k * plane + nh];
+  }
+  const float gv = fminf(round_act<kBF16>(gs), limit);
+  const float uv = fmaxf(fminf(round_act<kBF16>(us), limit), -limit);
+  const float sl = round_act<kBF16>(gv / (1.0f + expf(-gv)));
+  h[int64_t(slot) * nh + n] = to_act<kBF16>(sl * uv);
+}
+
+// ---- top-k sum (kernels/moe/routing.py:579-600) -------------------------------------
+
+// out[t][c] = RN(sum over slots k = 0..topk-1 in order of in[t][k][c]) in FP32;
+// with ids, a slot whose id is outside [0, experts) adds nothing.
+template <bool kBF16>
+__global__ __launch_bounds__(kThreads) void moe_sum_kernel(const uint16_t* in, int topk, int64_t hidden,
+                                                           const int32_t* ids, int experts,
+                                                           uint16_t* out) {
+  const int64_t t = blockIdx.y;
+  const int64_t c = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (c >= hidden) return;
+  float acc = 0.0f;
+  for (int k = 0; k < topk; ++k) {
+    if (ids) {
+      const int id = ids[t * topk + k];
+      if (id < 0 || id >= experts) continue;
+    }
+    const uint16_t v = in[(t * topk + k) * hidden + c];
+    acc += kBF16 ? vq::bf16_to_f32(v) : vq::f16_to_f32(v);
+  }
+  out[t * hidden + c] = to_act<kBF16>(acc);
+}
+
+// ---- deterministic alignment (tests/kernels/moe_align_reference.py) -------------------
+
+constexpr int kAlignThreads = 1024;
+
+__device__ __forceinline__ int routed_expert(const int32_t* ids, const int32_t* expert_map, int64_t i,
+                                             int experts) {
+  int e = ids[i];
+  if (e < 0 || e >= experts) return -1;
+  if (expert_map) {
+    e = expert_map[e];
+    if (e < 0 || e >= experts) return -1;
+  }
+  return e;
+}
+
+// One workgroup: counts, padded exclusive scan, expert per block, then the
+// routed rows placed in ascending flat order inside each expert: rounds of
+// 1024 rows, each wavefront ranks its rows per expert with ballots and the
+// 16 wavefronts take turns adding to the per-expert cursors.
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+    const int32_t* ids, int64_t numel, int experts, int bs, const int32_t* expert_map,
+    int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp) {
+  extern __shared__ int align_shared[];
+  int* count = align_shared;          // experts: counts, then cursors
+  int* start = count + experts;       // experts: padded exclusive starts
+  __shared__ int scan[kAlignThreads];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  for (int e = tid; e < experts; e += kAlignThreads) count[e] = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < numel; i += kAlignThreads) {
+    const int e = routed_expert(ids, expert_map, i, experts);
+    if (e >= 0) atomicAdd(&count[e], 1);
+  }
+  __syncthreads();
+  const int per = (experts + kAlignThreads - 1) / kAlignThreads;
+  const int e0 = min(experts, tid * per);
+  const int e1 = min(experts, e0 + per);
+  int run = 0;
+  for (int e = e0; e < e1; ++e) run += (count[e] + bs - 1) / bs * bs;
+  scan[tid] = run;
+  __syncthreads();
+  for (int d = 1; d < kAlignThreads; d <<= 1) {
+    const int v = tid >= d ? scan[tid - d] : 0;
+    __syncthreads();
+    scan[tid] += v;
+    __syncthreads();
+  }
+  int at = scan[tid] - run;
+  for (int e = e0; e < e1; ++e) {
+    start[e] = at;
+    at += (count[e] + bs - 1) / bs * bs;
+    count[e] = 0;
+  }
+  const int total = scan[kAlignThreads - 1];
+  __syncthreads();
+  if (tid == 0) ntpp[0] = total;
+  for (int64_t b = tid; b < blocks; b += kAlignThreads) {
+    int owner = -1;
+    if (b < total / bs) {
+      // last expert whose first block is at or before b
+      int lo = 0, hi = experts;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (start[mid] / bs <= b) lo = mid; else hi = mid;
+      }
+      owner = lo;
+    }
+    eids[b] = owner;
+  }
+  for (int64_t i = tid; i < sorted_size; i += kAlignThreads) sorted[i] = int32_t(numel);
+  __syncthreads();
+  for (int64_t base = 0; base < numel; base += kAlignThreads) {
+    const int64_t i = base + tid;
+    const int e = i < numel ? routed_expert(ids, expert_map, i, experts) : -1;
+    uint64_t active = __ballot(e >= 0);
+    int rank = 0, n_same = 0;
+    bool leader = false;
+    while (active) {
+      const int first = __builtin_ctzll(active);
+      const int ev = __shfl(e, first);
+      const uint64_t same = __ballot(e == ev);
+      if (e == ev) {
+        rank = __builtin_popcountll(same & ((uint64_t(1) << lane) - 1));
+        n_same = __builtin_popcountll(same);
+        leader = lane == first;
+      }
+      active &= ~same;
+    }
+    for (int turn = 0; turn < kAlignThreads / 64; ++turn) {
+      if (wave == turn && e >= 0) {
+        const int cursor = count[e];
+        const int64_t dest = int64_t(start[e]) + cursor + rank;
+        if (dest < sorted_size) sorted[dest] = int32_t(i);
+        if (leader) count[e] = cursor + n_same;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ---- host ----------------------------------------------------------------------------
+
+template <bool kBF16, int kWavesK, int kSub>
+int launch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t s) {
+  constexpr int kTilesWG = 4 / kWavesK;
+  const dim3 grid(unsigned((g.N / 64 + kTilesWG - 1) / kTilesWG), unsigned(blocks), unsigned(ksplit));
+  switch (mode) {
+    case kPartial: hipLaunchKernelGGL((marlin_gemm<kBF16, kWavesK, kSub, kPartial>), grid, dim3(kThreads), 0, s, g); break;
+    case kStore: hipLaunchKernelGGL((marlin_gemm<kBF16, kWavesK, kSub, kStore>), grid, dim3(kThreads), 0, s, g); break;
+    default: hipLaunchKernelGGL((marlin_gemm<kBF16, kWavesK, kSub, kTopk>), grid, dim3(kThreads), 0, s, g); break;
+  }
+  return vq::check_launch("marlin_gemm");
+}
+
+template <bool kBF16>
+int dispatch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t s) {
+  if (g.bs <= 16) return launch_gemm<kBF16, 4, 1>(g, mode, blocks, ksplit, s);
+  if (g.bs <= 32) return launch_gemm<kBF16, 4, 2>(g, mode, blocks, ksplit, s);
+  return launch_gemm<kBF16, 1, 4>(g, mode, blocks, ksplit, s);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace marlin
+
+extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
+                               const int32_t* w, const void* scales, int64_t experts,
+                               const int32_t* sorted, int64_t sorted_numel, const int32_t* expert_ids,
+                               int64_t expert_ids_numel, const int32_t* ntpp, const float* topk_w,
+                               int64_t top_k, int64_t n_slots, int64_t K, int64_t N,
+                               int64_t block_size, int mode, int64_t ksplit, float* part,
+                               int64_t part_numel, void* out, int64_t out_stride, int64_t out_rows,
+                               void* stream) {
+  using namespace vq;
+  if (act_dtype != kBF16 && act_dtype != kFP16) return fail("a: bf16 or fp16 activations");
+  if (K <= 0 || N <= 0 || K % 128 != 0 || N % 64 != 0) return fail("K % 128, N % 64");
+  if (K > INT_MAX / 2 || N > INT_MAX / 2) return fail("K and N must fit int32");
+  if (block_size < 8 || block_size > marlin::kMaxBlock || block_size % 8 != 0) {
+    return fail("moe block size must be a multiple of 8 up to 64");
+  }
+  if (top_k <= 0 || n_slots < 0 || n_slots > INT_MAX || experts <= 0 || experts > INT_MAX) {
+    return fail("routing sizes out of range");
+  }
+  if (a_rows < 0 || a_stride < K || a_stride % 8 != 0) {
+    return fail("a: unit inner stride, row stride a multiple of 8 and at least K");
+  }
+  if ((n_slots + top_k - 1) / top_k > a_rows) return fail("a has fewer rows than the routed slots need");
+  if (!marlin::aligned16(a) || !marlin::aligned16(w) || !marlin::aligned16(scales)) {
+    return fail("a, w and s must be 16-byte aligned");
+  }
+  // every routed block holds at least one slot, and routed blocks come first
+  const int64_t blocks =
+      std::min(std::min<int64_t>(sorted_numel / block_size, expert_ids_numel), n_slots);
+  if (blocks > 65535) return fail("too many aligned blocks");
+  const int64_t groups = K / 128;
+  if (ksplit <= 0 || groups % ksplit != 0 || ksplit > 65535) {
+    return fail("ksplit must divide K / 128");
+  }
+  if (mode == marlin::kPartial) {
+    if (!part || part_numel < ksplit * n_slots * N) return fail("w13 partial buffer");
+    if (!marlin::aligned16(part)) return fail("w13 partial buffer must be 16-byte aligned");
+  } else if (mode == marlin::kStore || mode == marlin::kTopk) {
+    if (ksplit != 1) return fail("a stored output takes one k-slice");
+    if (!out || out_stride < N || out_stride % 4 != 0 || out_rows < n_slots) return fail("output too small");
+    if ((reinterpret_cast<uintptr_t>(out) & 7) != 0) return fail("output must be 8-byte aligned");
+    if (mode == marlin::kTopk && !topk_w) return fail("topk weights required");
+  } else {
+    return fail("unknown marlin_moe_gemm mode");
+  }
+  if (n_slots == 0 || blocks == 0) return kOk;
+  marlin::GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a);
+  g.a_stride = a_stride;
+  g.w = reinterpret_cast<const marlin::u32x4_t*>(w);
+  g.s = static_cast<const uint16_t*>(scales);
+  g.sorted = sorted;
+  g.eids = expert_ids;
+  g.ntpp = ntpp;
+  g.topk_w = topk_w;
+  g.part = part;
+  g.out = static_cast<uint16_t*>(out);
+  g.out_stride = out_stride;
+  g.top_k = int(top_k);
+  g.n_slots = int(n_slots);
+  g.K = int(K);
+  g.N = int(N);
+  g.bs = int(block_size);
+  g.experts = int(experts);
+  g.groups_per_split = int(groups / ksplit);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  return act_dtype == kBF16 ? marlin::dispatch_gemm<true>(g, mode, int(blocks), int(ksplit), s)
+                            : marlin::dispatch_gemm<false>(g, mode, int(blocks), int(ksplit), s);
+}
+
+extern "C" int marlin_moe_act(const float* part, const int32_t* ids, int64_t ksplit, int64_t n_slots,
+                              int64_t nh, float limit, void* h, int act_dtype, void* stream) {
+  using namespace vq;
+  if (act_dtype != kBF16 && act_dtype != kFP16) return fail("h: bf16 or fp16");
+  if (ksplit <= 0 || nh <= 0 || n_slots < 0 || n_slots > 65535 || nh > INT_MAX / 2) {
+    return fail("act: ksplit > 0, 0 < Nh, n_slots <= 65535");
+  }
+  if (std::isnan(limit)) return fail("act: limit must not be NaN");
+  if (n_slots == 0) return kOk;
+  const dim3 grid(unsigned((nh + marlin::kThreads - 1) / marlin::kThreads), unsigned(n_slots));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (act_dtype == kBF16) {
+    hipLaunchKernelGGL(marlin::marlin_act_kernel<true>, grid, dim3(marlin::kThreads), 0, s, part, ids,
+                       int(ksplit), int(n_slots), int(nh), limit, static_cast<uint16_t*>(h));
+  } else {
+    hipLaunchKernelGGL(marlin::marlin_act_kernel<false>, grid, dim3(marlin::kThreads), 0, s, part, ids,
+                       int(ksplit), int(n_slots), int(nh), limit, static_cast<uint16_t*>(h));
+  }
+  return check_launch("marlin_act");
+}
+
+extern "C" int marlin_dequant(const int32_t* w, const void* scales, int act_dtype, int64_t K, int64_t N,
+                              void* out, void* stream) {
+  using namespace vq;
+  if (act_dtype != kBF16 && act_dtype != kFP16) return fail("bf16 or fp16 scales");
+  if (K <= 0 || N <= 0 || K % 128 != 0 || N % 64 != 0) return fail("K % 128, N % 64");
+  if (!marlin::aligned16(w) || !marlin::aligned16(scales)) return fail("w and s must be 16-byte aligned");
+  const int64_t items = (K / 32) * (N / 64);
+  if ((items + 3) / 4 > INT_MAX) return fail("matrix too large");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(unsigned((items + 3) / 4));
+  const auto* wp = reinterpret_cast<const marlin::u32x4_t*>(w);
+  const auto* sp = static_cast<const uint16_t*>(scales);
+  if (act_dtype == kBF16) {
+    hipLaunchKernelGGL(marlin::marlin_dequant_kernel<true>, grid, dim3(marlin::kThreads), 0, s, wp, sp,
+                       int(K), int(N), static_cast<uint16_t*>(out));
+  } else {
+    hipLaunchKernelGGL(marlin::marlin_dequant_kernel<false>, grid, dim3(marlin::kThreads), 0, s, wp, sp,
+                       int(K), int(N), static_cast<uint16_t*>(out));
+  }
+  return check_launch("marlin_dequant");
+}
+
+extern "C" int moe_sum(const void* in, int act_dtype, int64_t tokens, int64_t topk, int64_t hidden,
+                       const int32_t* ids, int64_t experts, void* out, void* stream) {
+  using namespace vq;
+  if (act_dtype != kBF16 && act_dtype != kFP16) return fail("moe_sum: bf16 or fp16");
+  if (tokens < 0 || tokens > 65535 || topk <= 0 || hidden <= 0 || experts < 0 || experts > INT_MAX ||
+      topk > INT_MAX) {
+    return fail("moe_sum: sizes out of range");
+  }
+  if (tokens == 0) return kOk;
+  const dim3 grid(unsigned((hidden + marlin::kThreads - 1) / marlin::kThreads), unsigned(tokens));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const auto* ip = static_cast<const uint16_t*>(in);
+  auto* op = static_cast<uint16_t*>(out);
+  if (act_dtype == kBF16) {
+    hipLaunchKernelGGL(marlin::moe_sum_kernel<true>, grid, dim3(marlin::kThreads), 0, s, ip, int(topk),
+                       hidden, ids, int(experts), op);
+  } else {
+    hipLaunchKernelGGL(marlin::moe_sum_kernel<false>, grid, dim3(marlin::kThreads), 0, s, ip, int(topk),
+                       hidden, ids, int(experts), op);
+  }
+  return check_launch("moe_sum");
+}
+
+extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
+                                    int64_t block_size, const int32_t* expert_map, int32_t* sorted,
+                                    int64_t sorted_numel, int32_t* expert_ids, int64_t expert_ids_numel,
+                                    int32_t* ntpp, void* stream) {
+  using namespace vq;
+  if (numel < 0 || numel > INT_MAX || block_size <= 0 || block_size > 1024) {
+    return fail("align: numel and block size out of range");
+  }
+  if (num_experts <= 0 || num_experts > 8192) return fail("align: 1 <= num_experts <= 8192");
+  const int64_t worst = numel + num_experts * (block_size - 1);
+  if (worst > INT_MAX) return fail("align: padded total must fit int32");
+  const int64_t need = numel < num_experts ? std::min(numel * block_size, worst) : worst;
+  if (sorted_numel < need) return fail("align: sorted_token_ids is smaller than numel + E (bs - 1)");
+  if (expert_ids_numel * block_size < need) return fail("align: expert_ids too small");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(marlin::moe_align_kernel, dim3(1), dim3(marlin::kAlignThreads),
+                     size_t(2 * num_experts) * sizeof(int), s, topk_ids, numel, int(num_experts),
+                     int(block_size), expert_map, sorted, sorted_numel, expert_ids, expert_ids_numel,
+                     ntpp);
+  return check_launch("moe_align_block_size");
+}

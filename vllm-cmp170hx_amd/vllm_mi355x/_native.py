@@ -47,6 +47,21 @@ SIGNATURES = {
         c_vp, c_int, c_vp, c_i64,             # out, out_dtype, workspace, workspace_numel
         ctypes.c_float, c_vp,                 # swiglu_limit, stream
     ]),
+    "marlin_moe_gemm": (c_int, [
+        c_vp, c_int, c_i64, c_i64,            # a, act_dtype, a_rows, a_stride
+        c_vp, c_vp, c_i64,                    # w, scales, experts
+        c_vp, c_i64, c_vp, c_i64, c_vp,       # sorted, numel, expert_ids, numel, ntpp
+        c_vp, c_i64, c_i64,                   # topk_w, top_k, n_slots
+        c_i64, c_i64, c_i64, c_int, c_i64,    # K, N, block_size, mode, ksplit
+        c_vp, c_i64, c_vp, c_i64, c_i64,      # part, part_numel, out, out_stride, out_rows
+        c_vp,                                 # stream
+    ]),
+    "marlin_moe_act": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, ctypes.c_float, c_vp, c_int,
+                               c_vp]),
+    "marlin_dequant": (c_int, [c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_vp]),
+    "moe_sum": (c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp]),
+    "moe_align_block_size": (c_int, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64,
+                                     c_vp, c_vp]),
 }
 
 _lib = None

@@ -1,0 +1,132 @@
+"""Fused Marlin int4 MoE forward on gfx950.
+
+The launch sequence of the reference's decode path
+(vllm_sm80/kernels/marlin_moe/decode.py:301-339) and of upstream
+fused_marlin_moe: deterministic block alignment -> w13 grouped GEMM (FP32
+k-split partials) -> SwiGLU with the optional clamp -> w2 grouped GEMM with
+the router weight (RN(RN(sum) * RN(w))) -> slot-order top-k sum.  Rounding
+points are the reference's; the block size and the w13 K split are chosen
+here for gfx950 (one aligned block holds up to 64 tokens of one expert, so
+an expert's weights are streamed once per block).
+
+Weights: w1 int32 [E, K/16, 4N] (gate columns 0..N-1, up N..2N-1), w2
+int32 [E, N/16, 2K], scales [E, K/128, 2N] / [E, N/128, K] of the
+activation dtype, hidden_states [M, K] bf16 or fp16.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _C
+from ..moe.align import align_sizes, kernel_moe_align_block_size
+from ..moe.routing import moe_sum
+
+
+def choose_block_size(tokens: int, topk: int, experts: int) -> int:
+    """Tokens per aligned block: enough that most experts fit in one block
+    (their weights are then read once), at most 64."""
+    per_expert = tokens * topk / max(experts, 1)
+    for bs, limit in ((8, 4), (16, 10), (32, 22)):
+        if per_expert <= limit:
+            return bs
+    return 64
+
+
+def choose_w13_ksplit(blocks: int, n13: int, k: int, bs: int, target: int = 768) -> int:
+    """K split of the w13 GEMM: enough workgroups to cover the GPU, at least
+    one 128-k group per wavefront."""
+    groups = k // 128
+    tiles_per_wg = 1 if bs <= 32 else 4
+    wgs = max(1, blocks) * max(1, n13 // 64 // tiles_per_wg)
+    ksplit = 1
+    waves_k = 4 if bs <= 32 else 1
+    while (wgs * ksplit < target and groups % (2 * ksplit) == 0
+           and groups // (2 * ksplit) >= waves_k):
+        ksplit *= 2
+    return ksplit
+
+
+def workspace_shapes(tokens: int, topk: int, hidden: int, inter: int, experts: int,
+                     block_size: int, ksplit: int) -> dict:
+    slots = tokens * topk
+    size, blocks = align_sizes(slots, experts, block_size)
+    return {"sorted": (size,), "expert_ids": (blocks,), "ntpp": (1,),
+            "part": (ksplit * slots * 2 * inter,), "h": (slots, inter), "c3": (slots, hidden)}
+
+
+def marlin_dequant(w: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """W [K, N] of one packed matrix (int32 [K/16, 2N], scales [K/128, N]):
+    RN((q - 8) * s) through the GEMM's own fragment and dequant code."""
+    from ... import _native
+    K, N = w.size(0) * 16, w.size(1) // 2
+    out = torch.empty((K, N), dtype=s.dtype, device=w.device)
+    with torch.cuda.device(w.device):
+        status = _native.load().marlin_dequant(
+            w.data_ptr(), s.data_ptr(), _C._DTYPE_CODES[s.dtype], K, N, out.data_ptr(),
+            torch.cuda.current_stream(w.device).cuda_stream)
+    _native.check(status)
+    return out
+
+
+def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                     w1_scale: torch.Tensor, w2_scale: torch.Tensor, topk_weights: torch.Tensor,
+                     topk_ids: torch.Tensor, clamp_limit: float | None = None,
+                     expert_map: torch.Tensor | None = None, block_size: int | None = None,
+                     ksplit: int | None = None, workspace: dict | None = None,
+                     output: torch.Tensor | None = None) -> torch.Tensor:
+    """out [M, K] = sum over the top-k slots (slot order) of
+    RN(RN(w2_e(h)) * RN(router weight)), h = RN(RN(SiLU(min(g, L))) *
+    clamp(u, -L, L)), (g | u) = RN(w1_e(x)).  Slots routed outside the local
+    experts (id out of range, or mapped to -1) add nothing."""
+    M, K = hidden_states.shape
+    E = w1.size(0)
+    N = w2.size(1) * 16
+    topk = topk_ids.size(1)
+    if w1.shape != (E, K // 16, 4 * N) or w2.shape != (E, N // 16, 2 * K):
+        raise RuntimeError("unsupported packed weight layout")
+    if w1_scale.shape != (E, K // 128, 2 * N) or w2_scale.shape != (E, N // 128, K):
+        raise RuntimeError("scales are not group-128")
+    if hidden_states.dtype not in _C._DTYPE_CODES or w1_scale.dtype != hidden_states.dtype \
+            or w2_scale.dtype != hidden_states.dtype:
+        raise RuntimeError("activations and scales must share a bf16 or fp16 dtype")
+    if topk_weights.shape != topk_ids.shape or topk_ids.size(0) != M:
+        raise RuntimeError("routing shape mismatch")
+    out = output if output is not None else torch.empty_like(hidden_states)
+    if M == 0:
+        return out
+    limit = math.inf if clamp_limit is None else float(clamp_limit)
+    slots = M * topk
+    ids = topk_ids.to(torch.int32).contiguous()
+    local = ids
+    if expert_map is not None:
+        emap = expert_map.to(torch.int32)
+        inside = (ids >= 0) & (ids < emap.numel())
+        local = torch.where(inside, emap[torch.where(inside, ids, 0).long()], -1).contiguous()
+    bs = block_size or choose_block_size(M, topk, E)
+    blocks_est = min(slots, E)
+    ks = ksplit or choose_w13_ksplit(blocks_est, 2 * N, K, bs)
+    shapes = workspace_shapes(M, topk, K, N, E, bs, ks)
+    ws = workspace if workspace is not None else {}
+    buf = {}
+    for name, shape in shapes.items():
+        dtype = {"part": torch.float32, "h": hidden_states.dtype,
+                 "c3": hidden_states.dtype}.get(name, torch.int32)
+        t = ws.get(name)
+        numel = math.prod(shape)
+        if t is None or t.numel() < numel or t.dtype != dtype:
+            t = torch.empty(numel, dtype=dtype, device=hidden_states.device)
+            ws[name] = t
+        buf[name] = t.view(-1)[:numel].view(shape)
+    kernel_moe_align_block_size(local, E, bs, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
+                                None)
+    tw = topk_weights.to(torch.float32).contiguous().view(-1)
+    _C.gemm(hidden_states, w1, w1_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
+            topk, slots, K, 2 * N, bs, _C.MODE_PARTIAL, ks, part=buf["part"])
+    _C.act(buf["part"], local.view(-1), ks, slots, N, limit, buf["h"])
+    _C.gemm(buf["h"], w2, w2_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], tw, 1, slots,
+            N, K, bs, _C.MODE_TOPK, 1, out=buf["c3"])
+    moe_sum(buf["c3"].view(M, topk, K), out, local, E)
+    return out
