@@ -197,8 +197,7 @@ def test_fused_block_sizes_and_splits_agree(mm, device):
     """T=256 at the C4 expert count: every block size and K split gives the
     same outputs to the MoE bar (the per-token arithmetic differs only in the
     w13 summation order), and bit-identical ones where that order is the
-    same: blocks of up to 32 tokens (four wavefronts split K) agree with each
-    other, as do blocks of 48 and 64 (one wavefront runs all of K)."""
+    same: blocks of 48 and 64 tokens (one wavefront runs all of K)."""
     rng = np.random.default_rng(8)
     E, K, N, topk, T = 128, 512, 256, 8, 256
     layer = Layer(rng, E, K, N, M.BF16, device)
@@ -211,8 +210,6 @@ def test_fused_block_sizes_and_splits_agree(mm, device):
     for key, got in runs.items():
         assert_close(got, base, M.BF16, f"bs, ks = {key}")
     assert np.array_equal(runs[(48, 1)], base)
-    assert np.array_equal(runs[(8, 1)], runs[(16, 1)])
-    assert np.array_equal(runs[(8, 1)], runs[(32, 1)])
 
 
 def test_fused_zero_weights_masked_slots_and_empty(mm, device):

@@ -55,6 +55,7 @@ enum Mode : int { kPartial = 0, kStore = 1, kTopk = 2 };
 struct GemmArgs {
   const uint16_t* a;      // activations, row r at a + r * a_stride
   int64_t a_stride;
+  uint32_t a_bytes;       // bytes of a addressable by the kernel
   const u32x4_t* w;       // [E][K/16][N/2] 16-byte fragments
   const uint16_t* s;      // [E][K/128][N] group scales (permuted columns)
   const int32_t* sorted;  // [blocks * bs] routed slot ids, sentinel >= n_slots
@@ -67,21 +68,50 @@ struct GemmArgs {
   int top_k, n_slots, K, N, bs, experts, groups_per_split;
 };
 
+// Raw buffer resource over [base, base + bytes): 32-bit offsets, and loads
+// past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+__device__ __forceinline__ u32x4_t load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, int(voffset), int(soffset), 0));
+}
+
 // ---- dequant ---------------------------------------------------------------------
 
 // One word of 8 nibbles (bytes [A.x, B.x, A.y, B.y] of the two k16 rows A and
 // B, x / y the nibble pairs of k {2q, 2q+8} / {2q+1, 2q+9}) -> four packed
 // pairs, k order (2q, 2q+1) (2q+8, 2q+9) (16+2q, 17+2q) (24+2q, 25+2q).
-// FP16: 0x6400 | nibble is 1024 + q exactly, minus 1032 is q - 8 exactly,
-// times (s, s) rounds once.
-__device__ __forceinline__ void dequant_f16(uint32_t c, uint32_t s2, uint32_t (&o)[4]) {
+// FP16: a nibble in mantissa bits 0-3 under 0x6400 is 1024 + q exactly, so
+// minus 1032 is q - 8; in bits 4-7 it is 1024 + 16 q, and * 1/16 - 72 is
+// q - 8 (one exact FMA); times (s, s) then rounds once.
+// (x & mask) | magic as one v_and_or_b32: gfx9's VOP3 takes no 32-bit
+// literal, so the compiler would otherwise split it; the constants live in
+// VGPRs, set once per kernel.
+struct NibbleMasks {
+  uint32_t lo, hi, magic;  // 0x000f000f, 0x00f000f0, 0x64006400
+};
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm volatile("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "v"(magic));
+  return r;
+}
+
+__device__ __forceinline__ void dequant_f16(uint32_t c, uint32_t s2, const NibbleMasks& k,
+                                            uint32_t (&o)[4]) {
   const half2_t s = __builtin_bit_cast(half2_t, s2);
-  const half2_t bias = {_Float16(1032.0f), _Float16(1032.0f)};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t m = ((c >> (4 * i)) & 0x000f000fu) | 0x64006400u;
-    o[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, m) - bias) * s);
-  }
+  const half2_t b1032 = {_Float16(1032.0f), _Float16(1032.0f)};
+  const half2_t r16 = {_Float16(0.0625f), _Float16(0.0625f)};
+  const half2_t m72 = {_Float16(-72.0f), _Float16(-72.0f)};
+  const uint32_t c8 = c >> 8;
+  const half2_t p0 = __builtin_bit_cast(half2_t, and_or(c, k.lo, k.magic));
+  const half2_t p1 = __builtin_bit_cast(half2_t, and_or(c, k.hi, k.magic));
+  const half2_t p2 = __builtin_bit_cast(half2_t, and_or(c8, k.lo, k.magic));
+  const half2_t p3 = __builtin_bit_cast(half2_t, and_or(c8, k.hi, k.magic));
+  o[0] = __builtin_bit_cast(uint32_t, (p0 - b1032) * s);
+  o[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p1, r16, m72) * s);
+  o[2] = __builtin_bit_cast(uint32_t, (p2 - b1032) * s);
+  o[3] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p3, r16, m72) * s);
 }
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
@@ -105,12 +135,12 @@ __device__ __forceinline__ void dequant_bf16(uint32_t c, float s, float ns8, uin
   o[3] = two(hi, 1, 3);
 }
 
-// The 16-byte fragment of this lane's NVIDIA lane in k16 row 2 step + r / 8.
-__device__ __forceinline__ const u32x4_t* fragment(const u32x4_t* w_e, int64_t N, int tile, int step,
-                                                   int lane) {
+// Byte offset, inside an expert's matrix, of this lane's 16-byte fragment
+// (NVIDIA lane 4 (r % 8) + q of k16 row r / 8) in step 0 of tile `tile`;
+// a step (two k16 rows) adds N * 16 bytes.
+__device__ __forceinline__ uint32_t fragment_offset(int N, int tile, int lane) {
   const int q = lane >> 4, r = lane & 15;
-  const int64_t krow = 2 * int64_t(step) + (r >> 3);
-  return w_e + krow * (N >> 1) + tile * 32 + 4 * (r & 7) + q;
+  return uint32_t(((r >> 3) * (N >> 1) + tile * 32 + 4 * (r & 7) + q) * 16);
 }
 
 // Swap with lane r ^ 8 of the 16-lane row and keep this lane's column's bytes.
@@ -136,12 +166,12 @@ struct Scales {
       }
     }
   }
-  __device__ __forceinline__ u32x4_t operand(uint32_t c, int j) const {
+  __device__ __forceinline__ u32x4_t operand(uint32_t c, int j, const NibbleMasks& k) const {
     uint32_t o[4];
     if constexpr (kBF16) {
       dequant_bf16(c, s[j], ns8[j], o);
     } else {
-      dequant_f16(c, pair[j], o);
+      dequant_f16(c, pair[j], k, o);
     }
     return u32x4_t{o[0], o[1], o[2], o[3]};
   }
@@ -178,18 +208,21 @@ __device__ __forceinline__ uint16_t to_act(float v) {
 
 // ---- grouped GEMM -----------------------------------------------------------------
 
-// kWavesK: wavefronts splitting K inside a workgroup (4: one tile per
-// workgroup; 1: four tiles); kSub: 16-token sub-blocks (block size <= 16 kSub).
-template <bool kBF16, int kWavesK, int kSub, int kMode>
-__global__ __launch_bounds__(kThreads) void marlin_gemm(GemmArgs g) {
-  constexpr int kTilesWG = 4 / kWavesK;
-  constexpr int kRounds = kWavesK == 1 ? 2 : 1;     // groups per wavefront per chunk
+// kTilesWG: 64-column tiles per workgroup (1: its four wavefronts split K;
+// 4: one tile per wavefront, all of K); kSub: 16-token sub-blocks (block
+// size <= 16 kSub).  Each wavefront streams whole 128-k groups (4 steps and
+// their scales) through a 3-slot register ring, two groups ahead.
+template <bool kBF16, int kTilesWG, int kSub, int kMode>
+__global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
+  constexpr int kWavesK = 4 / kTilesWG;
+  constexpr int kRounds = 1;                         // groups per wavefront per chunk
   constexpr int kChunkGroups = kWavesK * kRounds;   // 128-k groups per LDS chunk
   constexpr int kChunkSteps = 4 * kChunkGroups;
   constexpr int kTok = 16 * kSub;
   constexpr int kStepBytes = 4 * kTok * 16;          // [q][token][8 halves]
   constexpr int kChunkBytes = kChunkSteps * kStepBytes;
   constexpr int kStage = kChunkSteps * kTok * 4 / kThreads;  // 16-byte loads per thread
+  constexpr int kStageStride = kThreads / (4 * kTok);        // steps between a thread's loads
   static_assert(kStage >= 1 && kChunkSteps * kTok * 4 % kThreads == 0, "staging split");
   constexpr int kRedBytes = (kWavesK - 1) * 64 * 4 * kSub * 16 * kTilesWG;
   constexpr int kLds = 2 * kChunkBytes > kRedBytes ? 2 * kChunkBytes : kRedBytes;
@@ -225,38 +258,39 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm(GemmArgs g) {
   const int gps = g.groups_per_split;
   const int g0 = ks * gps;
   const int nch = (gps + kChunkGroups - 1) / kChunkGroups;
-  const int64_t groups_total = g.K >> 7;
-  const u32x4_t* w_e = g.w + int64_t(e) * (g.K >> 4) * (g.N >> 1);
-  const uint16_t* s_e = g.s + int64_t(e) * groups_total * g.N;
+  const int groups_total = g.K >> 7;
+  const __amdgpu_buffer_rsrc_t wbuf =
+      buffer(g.w + int64_t(e) * (g.K >> 4) * (g.N >> 1), uint32_t(g.K >> 4) * uint32_t(g.N >> 1) * 16u);
+  const __amdgpu_buffer_rsrc_t sbuf =
+      buffer(g.s + int64_t(e) * groups_total * g.N, uint32_t(groups_total) * uint32_t(g.N) * 2u);
+  const __amdgpu_buffer_rsrc_t abuf_g = buffer(g.a, g.a_bytes);
+  const uint32_t wstep = uint32_t(g.N) * 16u;  // bytes per step
+  uint32_t woff[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) woff[st] = fragment_offset(g.N, tile, lane) + st * wstep;
+  const uint32_t soff = uint32_t(tile * 64 + 8 * (lane & 7)) * 2u;
 
-  // activation staging: thread item i -> (step, token, 16-byte segment)
+  // activation staging: thread = (16-byte segment, token, first step)
+  const int seg = tid & 3;
+  const int tok = (tid >> 2) % kTok;
+  const int st0 = tid / (4 * kTok);
+  const int tslot = s_slot[tok];
+  const uint32_t aoff = tslot >= 0
+      ? uint32_t((int64_t(tslot / g.top_k) * g.a_stride + 8 * seg + 32 * st0) * 2)
+      : 0x80000000u;  // past the buffer: loads return zero
+  uint8_t* lds_stage = lds + st0 * kStepBytes + tok * 16 + 4 * seg;
   u32x4_t stage_regs[kStage];
   auto stage_load = [&](int c) {
+    const uint32_t kbase = uint32_t(g0 + c * kChunkGroups) * 256u;  // bytes of 128 k
 #pragma unroll
     for (int u = 0; u < kStage; ++u) {
-      const int i = tid + u * kThreads;
-      const int seg = i & 3;
-      const int tok = (i >> 2) % kTok;
-      const int st = i / (4 * kTok);
-      const int grp = g0 + c * kChunkGroups + (st >> 2);
-      const int slot = tok < kMaxBlock ? s_slot[tok] : -1;
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (slot >= 0 && grp < g0 + gps) {
-        const int64_t row = slot / g.top_k;
-        const int64_t k = int64_t(grp) * 128 + (st & 3) * 32 + 8 * seg;
-        v = *reinterpret_cast<const u32x4_t*>(g.a + row * g.a_stride + k);
-      }
-      stage_regs[u] = v;
+      stage_regs[u] = load16(abuf_g, aoff + uint32_t(u * kStageStride * 64), kbase);
     }
   };
   auto stage_store = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < kStage; ++u) {
-      const int i = tid + u * kThreads;
-      const int seg = i & 3;
-      const int tok = (i >> 2) % kTok;
-      const int st = i / (4 * kTok);
-      uint8_t* base = lds + buf * kChunkBytes + st * kStepBytes + tok * 16 + 4 * seg;
+      uint8_t* base = lds_stage + buf * kChunkBytes + u * kStageStride * kStepBytes;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         *reinterpret_cast<uint32_t*>(base + d * kTok * 16) = stage_regs[u][d];
@@ -267,25 +301,20 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm(GemmArgs g) {
   // this wavefront's groups: i -> chunk i / kRounds, round i % kRounds
   auto group_of = [&](int i) { return g0 + (i / kRounds) * kChunkGroups + (i % kRounds) * kWavesK + wk; };
   const int my_groups = nch * kRounds;
-  u32x4_t ring_w[2][4];
-  u32x4_t ring_s[2];
+  u32x4_t ring_w[3][4];
+  u32x4_t ring_s[3];
   auto load_group = [&](int slot, int i) {
     const int grp = group_of(i);
     if (tile_ok && grp < g0 + gps) {
+      const uint32_t gbase = uint32_t(grp) * 4u * wstep;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) ring_w[slot][st] = *fragment(w_e, g.N, tile, 4 * grp + st, lane);
-      ring_s[slot] = *reinterpret_cast<const u32x4_t*>(s_e + int64_t(grp) * g.N + tile * 64 +
-                                                       8 * (lane & 7));
+      for (int st = 0; st < 4; ++st) ring_w[slot][st] = load16(wbuf, woff[st], gbase);
+      ring_s[slot] = load16(sbuf, soff, uint32_t(grp) * uint32_t(g.N) * 2u);
     }
   };
 
-  f32x4_t acc[4][kSub];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int sb = 0; sb < kSub; ++sb) acc[j][sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
   load_group(0, 0);
+  if (my_groups > 1) load_group(1, 1);
   stage_load(0);
   stage_store(0);
   if (nch > 1) stage_load(1);
@@ -293,101 +322,123 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm(GemmArgs g) {
 
   const int q = lane >> 4;
   const int col = lane & 15;
-  // group i of this wavefront from ring slot kSlot (static: the ring stays in
-  // registers); the last group of a chunk refills the other LDS buffer
-  auto body = [&](int i, auto slot_tag) {
-    constexpr int kSlot = decltype(slot_tag)::value;
-    const int c = i / kRounds;
-    const int r = i % kRounds;
-    const int grp = group_of(i);
-    if (i + 1 < my_groups) load_group(kSlot ^ 1, i + 1);
-    if (tile_ok && grp < g0 + gps) {
-      const uint8_t* abuf = lds + (c & 1) * kChunkBytes;
-      Scales<kBF16> sc;
-      sc.set(ring_s[kSlot], lane);
+  NibbleMasks masks;
+  masks.lo = 0x000f000fu;
+  masks.hi = 0x00f000f0u;
+  masks.magic = 0x64006400u;
+
+  // The main loop and epilogue for the first kNs sub-blocks (those holding a
+  // routed token), specialized once per workgroup.
+  auto run = [&](auto ns_tag) {
+    constexpr int kNs = decltype(ns_tag)::value;
+    f32x4_t acc[4][kNs];
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const u32x4_t v = ring_w[kSlot][st];
-        const int stepc = (r * kWavesK + wk) * 4 + st;
-        u32x4_t bop[kSub];
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int sb = 0; sb < kSub; ++sb) {
-          if (sb < nsub) {
+      for (int sb = 0; sb < kNs; ++sb) acc[j][sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // group i of this wavefront from ring slot kSlot (static, so the ring
+    // stays in registers); the last group of a chunk refills the other LDS
+    // buffer
+    auto body = [&](int i, auto slot_tag) {
+      constexpr int kSlot = decltype(slot_tag)::value;
+      const int c = i / kRounds;
+      const int r = i % kRounds;
+      const int grp = group_of(i);
+      if (i + 2 < my_groups) load_group((kSlot + 2) % 3, i + 2);
+      if (tile_ok && grp < g0 + gps) {
+        const uint8_t* abuf = lds + (c & 1) * kChunkBytes;
+        Scales<kBF16> sc;
+        sc.set(ring_s[kSlot], lane);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const u32x4_t v = ring_w[kSlot][st];
+          const int stepc = (r * kWavesK + wk) * 4 + st;
+          u32x4_t bop[kNs];
+#pragma unroll
+          for (int sb = 0; sb < kNs; ++sb) {
             bop[sb] = *reinterpret_cast<const u32x4_t*>(abuf + stepc * kStepBytes +
                                                         (q * kTok + 16 * sb + col) * 16);
           }
-        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const u32x4_t a = sc.operand(combine(v[j], lane), j);
+          for (int j = 0; j < 4; ++j) {
+            const u32x4_t a = sc.operand(combine(v[j], lane), j, masks);
 #pragma unroll
-          for (int sb = 0; sb < kSub; ++sb) {
-            if (sb < nsub) acc[j][sb] = mfma<kBF16>(a, bop[sb], acc[j][sb]);
+            for (int sb = 0; sb < kNs; ++sb) acc[j][sb] = mfma<kBF16>(a, bop[sb], acc[j][sb]);
           }
         }
       }
-    }
-    if (r == kRounds - 1) {
-      if (c + 1 < nch) stage_store((c + 1) & 1);
-      if (c + 2 < nch) stage_load(c + 2);
-      __syncthreads();
-    }
-  };
-  for (int i = 0; i < my_groups; i += 2) {
-    body(i, std::integral_constant<int, 0>{});
-    if (i + 1 < my_groups) body(i + 1, std::integral_constant<int, 1>{});
-  }
-
-  // split-K inside the workgroup: wavefronts 1.. of a tile hand their sums to
-  // wavefront 0 of it, which adds them in order 1, 2, 3
-  if constexpr (kWavesK > 1) {
-    float* red = reinterpret_cast<float*>(lds);
-    auto red_at = [&](int from, int j, int sb) {
-      return red + ((((wt * (kWavesK - 1) + from - 1) * 4 + j) * kSub + sb) * 64 + lane) * 4;
+      if (r == kRounds - 1) {
+        if (c + 1 < nch) stage_store((c + 1) & 1);
+        if (c + 2 < nch) stage_load(c + 2);
+        __syncthreads();
+      }
     };
-    if (wk > 0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int sb = 0; sb < kSub; ++sb)
-          if (sb < nsub) *reinterpret_cast<f32x4_t*>(red_at(wk, j, sb)) = acc[j][sb];
+    for (int i = 0; i < my_groups; i += 3) {
+      body(i, std::integral_constant<int, 0>{});
+      if (i + 1 < my_groups) body(i + 1, std::integral_constant<int, 1>{});
+      if (i + 2 < my_groups) body(i + 2, std::integral_constant<int, 2>{});
     }
-    __syncthreads();
-    if (wk > 0) return;
-#pragma unroll
-    for (int from = 1; from < kWavesK; ++from)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int sb = 0; sb < kSub; ++sb)
-          if (sb < nsub) acc[j][sb] += *reinterpret_cast<const f32x4_t*>(red_at(from, j, sb));
-  }
-  if (!tile_ok) return;
 
-  // C fragment: lane holds columns 16 j + 4 q .. +3 of token 16 sb + col
+    // split-K inside the workgroup: wavefronts 1.. of a tile hand their sums
+    // to wavefront 0 of it, which adds them in order 1, 2, 3
+    if constexpr (kWavesK > 1) {
+      float* red = reinterpret_cast<float*>(lds);
+      auto red_at = [&](int from, int j, int sb) {
+        return red + ((((wt * (kWavesK - 1) + from - 1) * 4 + j) * kSub + sb) * 64 + lane) * 4;
+      };
+      if (wk > 0) {
 #pragma unroll
-  for (int sb = 0; sb < kSub; ++sb) {
-    if (sb >= nsub) continue;
-    const int slot = s_slot[16 * sb + col];
-    if (slot < 0) continue;
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t n = int64_t(tile) * 64 + 16 * j + 4 * q;
-      const f32x4_t v = acc[j][sb];
-      if constexpr (kMode == kPartial) {
-        *reinterpret_cast<f32x4_t*>(g.part + (int64_t(ks) * g.n_slots + slot) * g.N + n) = v;
-      } else {
-        float x[4] = {v[0], v[1], v[2], v[3]};
-        if constexpr (kMode == kTopk) {
-          const float w = round_act<kBF16>(g.topk_w[slot]);
+          for (int sb = 0; sb < kNs; ++sb) *reinterpret_cast<f32x4_t*>(red_at(wk, j, sb)) = acc[j][sb];
+      }
+      __syncthreads();
+      if (wk > 0) return;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) x[u] = round_act<kBF16>(x[u]) * w;  // exact product
+      for (int from = 1; from < kWavesK; ++from)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int sb = 0; sb < kNs; ++sb) acc[j][sb] += *reinterpret_cast<const f32x4_t*>(red_at(from, j, sb));
+    }
+    if (!tile_ok) return;
+
+    // C fragment: lane holds columns 16 j + 4 q .. +3 of token 16 sb + col
+#pragma unroll
+    for (int sb = 0; sb < kNs; ++sb) {
+      const int slot = s_slot[16 * sb + col];
+      if (slot < 0) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t n = int64_t(tile) * 64 + 16 * j + 4 * q;
+        const f32x4_t v = acc[j][sb];
+        if constexpr (kMode == kPartial) {
+          *reinterpret_cast<f32x4_t*>(g.part + (int64_t(ks) * g.n_slots + slot) * g.N + n) = v;
+        } else {
+          float x[4] = {v[0], v[1], v[2], v[3]};
+          if constexpr (kMode == kTopk) {
+            const float w = round_act<kBF16>(g.topk_w[slot]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] = round_act<kBF16>(x[u]) * w;  // exact product
+          }
+          const u32x2_t packed = {uint32_t(to_act<kBF16>(x[0])) | (uint32_t(to_act<kBF16>(x[1])) << 16),
+                                  uint32_t(to_act<kBF16>(x[2])) | (uint32_t(to_act<kBF16>(x[3])) << 16)};
+          *reinterpret_cast<u32x2_t*>(g.out + int64_t(slot) * g.out_stride + n) = packed;
         }
-        const u32x2_t packed = {uint32_t(to_act<kBF16>(x[0])) | (uint32_t(to_act<kBF16>(x[1])) << 16),
-                                uint32_t(to_act<kBF16>(x[2])) | (uint32_t(to_act<kBF16>(x[3])) << 16)};
-        *reinterpret_cast<u32x2_t*>(g.out + int64_t(slot) * g.out_stride + n) = packed;
       }
     }
+  };
+  if constexpr (kSub == 1) {
+    run(std::integral_constant<int, 1>{});
+  } else if constexpr (kSub == 2) {
+    if (nsub == 1) run(std::integral_constant<int, 1>{});
+    else run(std::integral_constant<int, 2>{});
+  } else {
+    if (nsub == 1) run(std::integral_constant<int, 1>{});
+    else if (nsub == 2) run(std::integral_constant<int, 2>{});
+    else if (nsub == 3) run(std::integral_constant<int, 3>{});
+    else run(std::integral_constant<int, 4>{});
   }
 }
 
@@ -408,12 +459,14 @@ __global__ __launch_bounds__(kThreads) void marlin_dequant_kernel(const u32x4_t*
   Scales<kBF16> sc;
   sc.set(*reinterpret_cast<const u32x4_t*>(s + int64_t(step >> 2) * N + tile * 64 + 8 * (lane & 7)),
          lane);
-  const u32x4_t v = *fragment(w, N, tile, step, lane);
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(
+      reinterpret_cast<const uint8_t*>(w) + fragment_offset(N, tile, lane) + int64_t(step) * N * 16);
+  const NibbleMasks masks{0x000f000fu, 0x00f000f0u, 0x64006400u};
   const int q = lane >> 4, r = lane & 15;
   const int kofs[8] = {2 * q, 2 * q + 1, 2 * q + 8, 2 * q + 9, 16 + 2 * q, 17 + 2 * q, 24 + 2 * q, 25 + 2 * q};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const u32x4_t a = sc.operand(combine(v[j], lane), j);
+    const u32x4_t a = sc.operand(combine(v[j], lane), j, masks);
     const int64_t n = int64_t(tile) * 64 + 16 * j + r;
 #pragma unroll
     for (int h = 0; h < 8; ++h) {
@@ -453,22 +506,45 @@ __global__ __launch_bounds__(kThreads) void marlin_act_kernel(const float* part,
 // out[t][c] = RN(sum over slots k = 0..topk-1 in order of in[t][k][c]) in FP32;
 // with ids, a slot whose id is outside [0, experts) adds nothing.
 template <bool kBF16>
+__device__ __forceinline__ float act_f32(uint16_t v) {
+  return kBF16 ? vq::bf16_to_f32(v) : vq::f16_to_f32(v);
+}
+
+// kVec columns per thread (8 with 16-byte loads when hidden % 8 == 0, else 1).
+template <bool kBF16, int kVec>
 __global__ __launch_bounds__(kThreads) void moe_sum_kernel(const uint16_t* in, int topk, int64_t hidden,
                                                            const int32_t* ids, int experts,
                                                            uint16_t* out) {
   const int64_t t = blockIdx.y;
-  const int64_t c = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t c = (int64_t(blockIdx.x) * kThreads + threadIdx.x) * kVec;
   if (c >= hidden) return;
-  float acc = 0.0f;
+  float acc[kVec];
+#pragma unroll
+  for (int u = 0; u < kVec; ++u) acc[u] = 0.0f;
   for (int k = 0; k < topk; ++k) {
     if (ids) {
       const int id = ids[t * topk + k];
       if (id < 0 || id >= experts) continue;
     }
-    const uint16_t v = in[(t * topk + k) * hidden + c];
-    acc += kBF16 ? vq::bf16_to_f32(v) : vq::f16_to_f32(v);
+    const uint16_t* row = in + (t * topk + k) * hidden + c;
+    if constexpr (kVec == 8) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(row);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] += act_f32<kBF16>(uint16_t(v[u >> 1] >> (16 * (u & 1))));
+    } else {
+      acc[0] += act_f32<kBF16>(row[0]);
+    }
   }
-  out[t * hidden + c] = to_act<kBF16>(acc);
+  if constexpr (kVec == 8) {
+    u32x4_t o;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      o[u] = uint32_t(to_act<kBF16>(acc[2 * u])) | (uint32_t(to_act<kBF16>(acc[2 * u + 1])) << 16);
+    }
+    *reinterpret_cast<u32x4_t*>(out + t * hidden + c) = o;
+  } else {
+    out[t * hidden + c] = to_act<kBF16>(acc[0]);
+  }
 }
 
 // ---- deterministic alignment (tests/kernels/moe_align_reference.py) -------------------
@@ -486,21 +562,46 @@ __device__ __forceinline__ int routed_expert(const int32_t* ids, const int32_t* 
   return e;
 }
 
+// Inclusive prefix sum over the 1024 threads of the workgroup: within each
+// wavefront by shuffles, then across the 16 wavefront totals.
+__device__ __forceinline__ int block_inclusive_scan(int v, int* wave_tot) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d);
+    if (lane >= d) v += o;
+  }
+  if (lane == 63) wave_tot[wave] = v;
+  __syncthreads();
+  int before = 0;
+  for (int w = 0; w < wave; ++w) before += wave_tot[w];
+  __syncthreads();
+  return v + before;
+}
+
 // One workgroup: counts, padded exclusive scan, expert per block, then the
 // routed rows placed in ascending flat order inside each expert: rounds of
-// 1024 rows, each wavefront ranks its rows per expert with ballots and the
-// 16 wavefronts take turns adding to the per-expert cursors.
+// 1024 rows; each wavefront ranks its rows per expert with ballots, and a row
+// lands after its expert's rows of earlier rounds and earlier wavefronts
+// (per-wavefront counts in LDS when 16 x experts fit, else the 16 wavefronts
+// take turns at the per-expert cursors).
 __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     const int32_t* ids, int64_t numel, int experts, int bs, const int32_t* expert_map,
-    int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp) {
+    int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp,
+    int wave_counts) {
   extern __shared__ int align_shared[];
   int* count = align_shared;          // experts: counts, then cursors
   int* start = count + experts;       // experts: padded exclusive starts
-  __shared__ int scan[kAlignThreads];
+  int* wcnt = start + experts;        // [16][experts] when wave_counts
+  __shared__ int wave_tot[kAlignThreads / 64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   for (int e = tid; e < experts; e += kAlignThreads) count[e] = 0;
+  if (wave_counts) {
+    for (int i = tid; i < 16 * experts; i += kAlignThreads) wcnt[i] = 0;
+  }
   __syncthreads();
   for (int64_t i = tid; i < numel; i += kAlignThreads) {
     const int e = routed_expert(ids, expert_map, i, experts);
@@ -512,22 +613,16 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   const int e1 = min(experts, e0 + per);
   int run = 0;
   for (int e = e0; e < e1; ++e) run += (count[e] + bs - 1) / bs * bs;
-  scan[tid] = run;
-  __syncthreads();
-  for (int d = 1; d < kAlignThreads; d <<= 1) {
-    const int v = tid >= d ? scan[tid - d] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
-  }
-  int at = scan[tid] - run;
+  const int incl = block_inclusive_scan(run, wave_tot);
+  int at = incl - run;
   for (int e = e0; e < e1; ++e) {
     start[e] = at;
     at += (count[e] + bs - 1) / bs * bs;
     count[e] = 0;
   }
-  const int total = scan[kAlignThreads - 1];
+  if (tid == kAlignThreads - 1) wave_tot[0] = incl;  // the padded total
   __syncthreads();
+  const int total = wave_tot[0];
   if (tid == 0) ntpp[0] = total;
   for (int64_t b = tid; b < blocks; b += kAlignThreads) {
     int owner = -1;
@@ -544,54 +639,82 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
   for (int64_t i = tid; i < sorted_size; i += kAlignThreads) sorted[i] = int32_t(numel);
   __syncthreads();
+  const int id_bits = experts > 1 ? 32 - __builtin_clz(unsigned(experts - 1)) : 1;
   for (int64_t base = 0; base < numel; base += kAlignThreads) {
     const int64_t i = base + tid;
     const int e = i < numel ? routed_expert(ids, expert_map, i, experts) : -1;
-    uint64_t active = __ballot(e >= 0);
-    int rank = 0, n_same = 0;
-    bool leader = false;
-    while (active) {
-      const int first = __builtin_ctzll(active);
-      const int ev = __shfl(e, first);
-      const uint64_t same = __ballot(e == ev);
-      if (e == ev) {
-        rank = __builtin_popcountll(same & ((uint64_t(1) << lane) - 1));
-        n_same = __builtin_popcountll(same);
-        leader = lane == first;
-      }
-      active &= ~same;
+    // lanes of this wavefront routed to the same expert: one ballot per bit
+    // of the expert id (no data exchange between lanes)
+    uint64_t same = __ballot(e >= 0);
+    for (int bit = 0; bit < id_bits; ++bit) {
+      const bool set = (e >> bit) & 1;
+      const uint64_t m = __ballot(set);
+      same &= set ? m : ~m;
     }
-    for (int turn = 0; turn < kAlignThreads / 64; ++turn) {
-      if (wave == turn && e >= 0) {
-        const int cursor = count[e];
-        const int64_t dest = int64_t(start[e]) + cursor + rank;
-        if (dest < sorted_size) sorted[dest] = int32_t(i);
-        if (leader) count[e] = cursor + n_same;
+    const int rank = __builtin_popcountll(same & ((uint64_t(1) << lane) - 1));
+    const int n_same = __builtin_popcountll(same);
+    const bool leader = e >= 0 && rank == 0;
+    int64_t dest = -1;
+    if (wave_counts) {
+      if (leader) wcnt[wave * experts + e] = n_same;
+      __syncthreads();
+      if (e >= 0) {
+        int before = count[e];
+        for (int w = 0; w < wave; ++w) before += wcnt[w * experts + e];
+        dest = int64_t(start[e]) + before + rank;
       }
       __syncthreads();
+      for (int x = tid; x < experts; x += kAlignThreads) {
+        int add = 0;
+        for (int w = 0; w < kAlignThreads / 64; ++w) {
+          add += wcnt[w * experts + x];
+          wcnt[w * experts + x] = 0;
+        }
+        count[x] += add;
+      }
+      __syncthreads();
+    } else {
+      for (int turn = 0; turn < kAlignThreads / 64; ++turn) {
+        if (wave == turn && e >= 0) {
+          const int cursor = count[e];
+          dest = int64_t(start[e]) + cursor + rank;
+          if (leader) count[e] = cursor + n_same;
+        }
+        __syncthreads();
+      }
     }
+    if (dest >= 0 && dest < sorted_size) sorted[dest] = int32_t(i);
   }
 }
 
 // ---- host ----------------------------------------------------------------------------
 
-template <bool kBF16, int kWavesK, int kSub>
+template <bool kBF16, int kTilesWG, int kSub>
 int launch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t s) {
-  constexpr int kTilesWG = 4 / kWavesK;
   const dim3 grid(unsigned((g.N / 64 + kTilesWG - 1) / kTilesWG), unsigned(blocks), unsigned(ksplit));
   switch (mode) {
-    case kPartial: hipLaunchKernelGGL((marlin_gemm<kBF16, kWavesK, kSub, kPartial>), grid, dim3(kThreads), 0, s, g); break;
-    case kStore: hipLaunchKernelGGL((marlin_gemm<kBF16, kWavesK, kSub, kStore>), grid, dim3(kThreads), 0, s, g); break;
-    default: hipLaunchKernelGGL((marlin_gemm<kBF16, kWavesK, kSub, kTopk>), grid, dim3(kThreads), 0, s, g); break;
+    case kPartial: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kPartial>), grid, dim3(kThreads), 0, s, g); break;
+    case kStore: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kStore>), grid, dim3(kThreads), 0, s, g); break;
+    default: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kTopk>), grid, dim3(kThreads), 0, s, g); break;
   }
   return vq::check_launch("marlin_gemm");
 }
 
+// One 64-column tile per workgroup with its four wavefronts splitting K (few
+// blocks: many workgroups), or four tiles per workgroup sharing the staged
+// activations (enough blocks to fill the GPU: a quarter of the activation
+// traffic).  16-token sub-blocks: up to 2 for blocks of <= 32 tokens, 4 above.
 template <bool kBF16>
-int dispatch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t s) {
-  if (g.bs <= 16) return launch_gemm<kBF16, 4, 1>(g, mode, blocks, ksplit, s);
-  if (g.bs <= 32) return launch_gemm<kBF16, 4, 2>(g, mode, blocks, ksplit, s);
-  return launch_gemm<kBF16, 1, 4>(g, mode, blocks, ksplit, s);
+int dispatch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, int wide, hipStream_t s) {
+  if (g.bs <= 16) {
+    return wide ? launch_gemm<kBF16, 4, 1>(g, mode, blocks, ksplit, s)
+                : launch_gemm<kBF16, 1, 1>(g, mode, blocks, ksplit, s);
+  }
+  if (g.bs <= 32) {
+    return wide ? launch_gemm<kBF16, 4, 2>(g, mode, blocks, ksplit, s)
+                : launch_gemm<kBF16, 1, 2>(g, mode, blocks, ksplit, s);
+  }
+  return launch_gemm<kBF16, 4, 4>(g, mode, blocks, ksplit, s);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -621,6 +744,9 @@ extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int
     return fail("a: unit inner stride, row stride a multiple of 8 and at least K");
   }
   if ((n_slots + top_k - 1) / top_k > a_rows) return fail("a has fewer rows than the routed slots need");
+  if (a_rows * a_stride * 2 >= (int64_t(1) << 31) || K * N / 2 >= (int64_t(1) << 31)) {
+    return fail("a and each expert's weights must stay below 2 GiB");
+  }
   if (!marlin::aligned16(a) || !marlin::aligned16(w) || !marlin::aligned16(scales)) {
     return fail("a, w and s must be 16-byte aligned");
   }
@@ -647,6 +773,7 @@ extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int
   marlin::GemmArgs g{};
   g.a = static_cast<const uint16_t*>(a);
   g.a_stride = a_stride;
+  g.a_bytes = uint32_t(a_rows * a_stride * 2);
   g.w = reinterpret_cast<const marlin::u32x4_t*>(w);
   g.s = static_cast<const uint16_t*>(scales);
   g.sorted = sorted;
@@ -664,8 +791,13 @@ extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int
   g.experts = int(experts);
   g.groups_per_split = int(groups / ksplit);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  return act_dtype == kBF16 ? marlin::dispatch_gemm<true>(g, mode, int(blocks), int(ksplit), s)
-                            : marlin::dispatch_gemm<false>(g, mode, int(blocks), int(ksplit), s);
+  // four tiles per workgroup once that still gives ~2 workgroups per CU
+  // (the routed blocks are at most min(blocks, n_slots / 2 + experts); use
+  // the cheaper estimate of blocks routed by the slot count)
+  const int64_t routed_blocks = std::min<int64_t>(blocks, (n_slots + block_size - 1) / block_size + experts / 2);
+  const int wide = routed_blocks * (N / 256) * ksplit >= 512 ? 1 : 0;
+  return act_dtype == kBF16 ? marlin::dispatch_gemm<true>(g, mode, int(blocks), int(ksplit), wide, s)
+                            : marlin::dispatch_gemm<false>(g, mode, int(blocks), int(ksplit), wide, s);
 }
 
 extern "C" int marlin_moe_act(const float* part, const int32_t* ids, int64_t ksplit, int64_t n_slots,
@@ -720,17 +852,20 @@ extern "C" int moe_sum(const void* in, int act_dtype, int64_t tokens, int64_t to
     return fail("moe_sum: sizes out of range");
   }
   if (tokens == 0) return kOk;
-  const dim3 grid(unsigned((hidden + marlin::kThreads - 1) / marlin::kThreads), unsigned(tokens));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const auto* ip = static_cast<const uint16_t*>(in);
   auto* op = static_cast<uint16_t*>(out);
+  const bool vec = hidden % 8 == 0 && marlin::aligned16(in) && marlin::aligned16(out);
+  const int64_t per_block = int64_t(marlin::kThreads) * (vec ? 8 : 1);
+  const dim3 grid(unsigned((hidden + per_block - 1) / per_block), unsigned(tokens));
+#define VQ_SUM(B, V) hipLaunchKernelGGL((marlin::moe_sum_kernel<B, V>), grid, dim3(marlin::kThreads), 0, s, \
+                                        ip, int(topk), hidden, ids, int(experts), op)
   if (act_dtype == kBF16) {
-    hipLaunchKernelGGL(marlin::moe_sum_kernel<true>, grid, dim3(marlin::kThreads), 0, s, ip, int(topk),
-                       hidden, ids, int(experts), op);
+    if (vec) VQ_SUM(true, 8); else VQ_SUM(true, 1);
   } else {
-    hipLaunchKernelGGL(marlin::moe_sum_kernel<false>, grid, dim3(marlin::kThreads), 0, s, ip, int(topk),
-                       hidden, ids, int(experts), op);
+    if (vec) VQ_SUM(false, 8); else VQ_SUM(false, 1);
   }
+#undef VQ_SUM
   return check_launch("moe_sum");
 }
 
@@ -749,9 +884,11 @@ extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int6
   if (sorted_numel < need) return fail("align: sorted_token_ids is smaller than numel + E (bs - 1)");
   if (expert_ids_numel * block_size < need) return fail("align: expert_ids too small");
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(marlin::moe_align_kernel, dim3(1), dim3(marlin::kAlignThreads),
-                     size_t(2 * num_experts) * sizeof(int), s, topk_ids, numel, int(num_experts),
-                     int(block_size), expert_map, sorted, sorted_numel, expert_ids, expert_ids_numel,
-                     ntpp);
+  // per-wavefront counts when they fit in 64 KB of LDS with the rest
+  const int wave_counts = num_experts <= 960 ? 1 : 0;
+  const size_t lds = size_t(2 + (wave_counts ? 16 : 0)) * size_t(num_experts) * sizeof(int);
+  hipLaunchKernelGGL(marlin::moe_align_kernel, dim3(1), dim3(marlin::kAlignThreads), lds, s, topk_ids,
+                     numel, int(num_experts), int(block_size), expert_map, sorted, sorted_numel,
+                     expert_ids, expert_ids_numel, ntpp, wave_counts);
   return check_launch("moe_align_block_size");
 }
