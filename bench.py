@@ -2,24 +2,38 @@
 """Benchmark of the quantized-weight matmul hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
+                    [--no-extras]
 
-Workload (one "step"): one EXL3 dense linear at the decode-GEMV shape, a
-4096 x 14336 matrix at 4 bits per weight (bits_x2 8, mul1 codebook), M = 1
-fp16 activation row ~N(0,1), fp16 output; seeded uniform trellis words,
-suh / svh = +-1 x N(1, 0.05).  Twelve distinct weight copies (353 MB, more
-than the 256 MB Infinity Cache) are used round-robin so every step streams
-its weights from HBM.  The K timed steps run as replays of a HIP graph of
-back-to-back calls, timed with HIP events on the stream they run on.
+Headline workload (one "step"): one EXL3 dense linear at the decode-GEMV
+shape, a 4096 x 14336 matrix at 4 bits per weight (bits_x2 8, mul1
+codebook), M = 1 fp16 activation row ~N(0,1), fp16 output; seeded uniform
+trellis words, suh / svh = +-1 x N(1, 0.05).  Twelve distinct weight copies
+(353 MB, more than the 256 MB Infinity Cache) are used round-robin so every
+step streams its weights from HBM.  The K timed steps run as replays of a
+HIP graph of back-to-back calls, timed with HIP events on the stream they
+run on.
 
 value = algorithmic bytes per step / time per step, in GB/s, where the bytes
 are the packed weights + suh/svh + activations + output
-(K*N*bits/8 + 2(K+N) + 2MK + 2MN).  roofline.achieved is the same figure
-for the dominant kernel (see DESIGN.md for how it relates to the rocprof
-trace), against the 8 TB/s HBM peak.
+(K*N*bits/8 + 2(K+N) + 2MK + 2MN).  roofline.achieved is that figure per
+launch of the one kernel a step runs (the fused GEMV and finish), against
+the 8 TB/s HBM peak; roofline.traffic is the HBM bytes per launch measured
+with rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's readings,
+read from the committed profile summary when it is there.
 
-cpu_baseline: the reference's CPU dequantize-then-matmul path (LUT decode of
-every tile, FP64 block Hadamards, FP64 matmul; oracle/exl3_torch_ref.py) on
-the same matrix shape, timed on this host's cores for about --cpu-seconds.
+The same line also carries:
+  int4_moe   the Marlin-format int4 fused MoE (128 experts, hidden 2048,
+             intermediate 768, top-8, fp16, |N(0,0.02)| group-128 scales,
+             router logits ~N(0,1) -> softmax top-8) at 1, 16, 64 and 256
+             tokens: tokens/s, HBM GB/s over the touched experts' bytes,
+             and MFMA utilisation against the 2.5 PFLOP/s fp16 peak;
+  exl3_prefill  the 8192 x 28672 4-bit linear at M = 2048: TFLOP/s;
+  exl3_moe   the 3-bit EXL3 MoE (256 routed experts + 1 shared, hidden
+             7168, intermediate 2048, top-8 from Zipf(1.1)-skewed logits)
+             at 64 decode tokens: tokens/s and HBM GB/s;
+and the CPU baselines: the reference's CPU dequantize-then-matmul paths
+(oracle/exl3_torch_ref.py, oracle/marlin_torch_ref.py) on this host's
+cores, each on a bounded sample of its workload.
 
 Prints ONE JSON line.
 """
@@ -28,7 +42,9 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
+import re
 import statistics
 import sys
 import time
@@ -40,9 +56,11 @@ for _p in (ROOT, os.path.join(ROOT, "vllm-cmp170hx_amd")):
 
 METRIC = "EXL3 M=1 GEMV HBM GB/s (% peak); int4 MoE tokens/s + MFMA util at 256 tok"
 HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
 K_IN, N_OUT, BITS_X2, CODEBOOK, ROWS = 4096, 14336, 8, 2, 1
 COPIES = 12
 GRAPH_CALLS = 120
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "exl3_gemv_4096x14336_4bit_m1_traffic.md")
 
 
 def gemv_bytes(k: int, n: int, bits_x2: int, rows: int) -> int:
@@ -61,6 +79,38 @@ def make_matrix(torch, gen, device, k, n, bits_x2):
     return trellis, scales(k), scales(n)
 
 
+def time_graph(torch, calls, per_graph, warmup, steps):
+    """(ms per call, timed calls, warm-up calls): calls(i) captured
+    per_graph times in a HIP graph, replayed; HIP events on the replay
+    stream bracket the timed replays."""
+    for i in range(min(per_graph, 4)):  # eager warm-up (loads the library, first launches)
+        calls(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(per_graph):
+                calls(i)
+    torch.cuda.synchronize()
+    warm_reps = max(1, -(-warmup // per_graph))
+    reps = max(1, -(-steps // per_graph))
+    with torch.cuda.stream(stream):
+        for _ in range(warm_reps):
+            graph.replay()
+        stream.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+        end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (reps * per_graph), reps * per_graph, warm_reps * per_graph
+
+
 def gpu_gemv(args, torch):
     from vllm_mi355x.kernels.exl3 import ops
 
@@ -77,41 +127,197 @@ def gpu_gemv(args, torch):
         t, suh, svh = mats[i % COPIES]
         ops.linear_out(x, t, suh, svh, BITS_X2, CODEBOOK, K_IN, N_OUT, out, ws)
 
-    for i in range(COPIES):  # eager warm-up (loads the library, first launches)
-        call(i)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    stream = torch.cuda.Stream()
-    with torch.cuda.stream(stream):
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(GRAPH_CALLS):
-                call(i)
-    torch.cuda.synchronize()
-    warm_reps = max(1, -(-args.warmup // GRAPH_CALLS))
-    reps = max(1, -(-args.steps // GRAPH_CALLS))
-    with torch.cuda.stream(stream):
-        for _ in range(warm_reps):
-            graph.replay()
-        stream.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        end.record(stream)
-        end.synchronize()
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    steps = reps * GRAPH_CALLS
-    return total_ms / steps, steps, warm_reps * GRAPH_CALLS
+    ms, steps, warm = time_graph(torch, call, GRAPH_CALLS, args.warmup, args.steps)
+    del mats
+    return ms, steps, warm
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed FETCH_SIZE / WRITE_SIZE
+    summary (copy-calibrated), or None."""
+    try:
+        text = open(TRAFFIC_SUMMARY).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, flags=re.M)
+    return int(m.group(1)) if m else None
+
+
+# ---- int4 Marlin MoE ------------------------------------------------------------------
+
+MOE_E, MOE_H, MOE_N, MOE_TOPK = 128, 2048, 768, 8
+
+
+def marlin_expert_bytes(h: int, n: int) -> int:
+    return h * 2 * n // 2 + n * h // 2 + 2 * (h // 128 * 2 * n + n // 128 * h)
+
+
+def marlin_layer(torch, gen, device):
+    info = torch.iinfo(torch.int32)
+    w1 = torch.randint(info.min, info.max, (MOE_E, MOE_H // 16, 4 * MOE_N), generator=gen,
+                       device=device, dtype=torch.int32)
+    w2 = torch.randint(info.min, info.max, (MOE_E, MOE_N // 16, 2 * MOE_H), generator=gen,
+                       device=device, dtype=torch.int32)
+    s1 = (torch.randn(MOE_E, MOE_H // 128, 2 * MOE_N, generator=gen, device=device) * 0.02).abs().half()
+    s2 = (torch.randn(MOE_E, MOE_N // 128, MOE_H, generator=gen, device=device) * 0.02).abs().half()
+    return w1, w2, s1, s2
+
+
+def softmax_topk(torch, logits, k):
+    p = torch.softmax(logits.float(), -1)
+    w, ids = torch.topk(p, k, -1)
+    return (w / w.sum(-1, keepdim=True)).float().contiguous(), ids.to(torch.int32).contiguous()
+
+
+def gpu_marlin_moe(torch, tokens=(1, 16, 64, 256)):
+    from vllm_mi355x.kernels.marlin_moe import extension, fused
+
+    extension.require_extension()
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device)
+    gen.manual_seed(4)
+    layers = [marlin_layer(torch, gen, device) for _ in range(2)]
+    per_expert = marlin_expert_bytes(MOE_H, MOE_N)
+    results = {}
+    for T in tokens:
+        x = torch.randn(T, MOE_H, generator=gen, device=device).half()
+        tw, ti = softmax_topk(torch, torch.randn(T, MOE_E, generator=gen, device=device), MOE_TOPK)
+        out = torch.empty_like(x)
+        ws = {}
+
+        def call(i):
+            w1, w2, s1, s2 = layers[i % 2]
+            fused.fused_marlin_moe(x, w1, w2, s1, s2, tw, ti, workspace=ws, output=out)
+
+        ms, _, _ = time_graph(torch, call, 20, 40, 200)
+        touched = int(torch.unique(ti).numel())
+        nbytes = touched * per_expert + 2 * 2 * T * MOE_H
+        flops = 2 * T * MOE_TOPK * (MOE_H * 2 * MOE_N + MOE_N * MOE_H)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        tflops = flops / (ms * 1e-3) / 1e12
+        results[str(T)] = {
+            "us_per_forward": round(ms * 1e3, 2), "tokens_per_s": round(T / (ms * 1e-3)),
+            "experts_touched": touched, "hbm_gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "tflops": round(tflops, 2),
+            "mfma_util": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4),
+        }
+    del layers
+    return results
+
+
+def cpu_marlin_moe(seconds: float, torch):
+    """The reference's CPU path (unpack, FP64 dequant of every routed
+    expert, FP64 matmuls with the fp16 rounding points) on 4 tokens of the
+    same layer shape."""
+    from oracle.marlin_torch_ref import moe_fp64
+
+    g = torch.Generator().manual_seed(5)
+    info = torch.iinfo(torch.int32)
+    T = 4
+    x = torch.randn(T, MOE_H, generator=g).half()
+    tw, ti = softmax_topk(torch, torch.randn(T, MOE_E, generator=g), MOE_TOPK)
+    used = torch.unique(ti)
+    remap = torch.full((MOE_E,), -1, dtype=torch.int64)
+    remap[used] = torch.arange(used.numel())
+    local = remap[ti.long()]
+    E = used.numel()
+    w1 = torch.randint(info.min, info.max, (E, MOE_H // 16, 4 * MOE_N), generator=g, dtype=torch.int32)
+    w2 = torch.randint(info.min, info.max, (E, MOE_N // 16, 2 * MOE_H), generator=g, dtype=torch.int32)
+    s1 = (torch.randn(E, MOE_H // 128, 2 * MOE_N, generator=g) * 0.02).abs().half()
+    s2 = (torch.randn(E, MOE_N // 128, MOE_H, generator=g) * 0.02).abs().half()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        moe_fp64(x, local, tw, w1, w2, s1, s2)
+        times.append(time.perf_counter() - t0)
+    per_call = statistics.median(times)
+    return {
+        "value": round(T / per_call, 2), "unit": "tokens/s", "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} calls (median {per_call:.2f} s) of {T} tokens ({E} routed experts) "
+                   "of the 128-expert 2048/768 top-8 int4 MoE via the reference's CPU path "
+                   "restated in torch (unpack + FP64 dequant of every routed expert, FP64 matmuls "
+                   "with the fp16 rounding points)"),
+    }
+
+
+# ---- EXL3 prefill and MoE ---------------------------------------------------------------
+
+def gpu_exl3_prefill(torch, rows=2048, k=8192, n=28672):
+    from vllm_mi355x.kernels.exl3 import ops
+
+    ops.ensure_extension()
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device)
+    gen.manual_seed(7)
+    t, suh, svh = make_matrix(torch, gen, device, k, n, 8)
+    x = torch.randn(rows, k, device=device, generator=gen).half()
+    out = torch.empty(rows, n, dtype=torch.float16, device=device)
+    ws = torch.empty(ops.linear_workspace_size(rows, k, n), dtype=torch.float32, device=device)
+
+    def call(i):
+        ops.linear_out(x, t, suh, svh, 8, CODEBOOK, k, n, out, ws)
+
+    ms, _, _ = time_graph(torch, call, 4, 4, 12)
+    tflops = 2 * rows * k * n / (ms * 1e-3) / 1e12
+    return {"workload": f"{k}x{n} 4-bit mul1, M={rows}, fp16", "ms": round(ms, 3),
+            "tflops": round(tflops, 1), "mfma_util": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4)}
+
+
+def gpu_exl3_moe(torch, tokens=64, experts=256, hidden=7168, inter=2048, topk=8, bits_x2=6):
+    from vllm_mi355x.kernels.exl3 import ops
+
+    ops.ensure_extension()
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device)
+    gen.manual_seed(9)
+    local = experts + 1  # routed experts + the shared expert (local id `experts`)
+    keep, ptrs, meta = [], [], []
+    for _ in range(local):
+        p, m = [], []
+        for kk, nn in ((hidden, inter), (hidden, inter), (inter, hidden)):
+            t, suh, svh = make_matrix(torch, gen, device, kk, nn, bits_x2)
+            keep += [t, suh, svh]
+            p.append([t.data_ptr(), suh.data_ptr(), svh.data_ptr()])
+            m.append([kk, nn, bits_x2, 2])
+        ptrs.append(p)
+        meta.append(m)
+    ptrs = torch.tensor(ptrs, dtype=torch.int64, device=device)
+    meta = torch.tensor(meta, dtype=torch.int64, device=device)
+    # Zipf(1.1) expert popularity over a seeded permutation, softmax top-8,
+    # plus the shared expert with weight 1 in slot 8
+    ranks = torch.randperm(experts, generator=torch.Generator().manual_seed(10)).float() + 1.0
+    bias = (-1.1 * torch.log(ranks)).to(device)
+    logits = torch.randn(tokens, experts, generator=gen, device=device) + bias
+    tw, ti = softmax_topk(torch, logits, topk)
+    ids = torch.cat([ti, torch.full((tokens, 1), experts, dtype=torch.int32, device=device)], 1)
+    weights = torch.cat([tw, torch.ones(tokens, 1, device=device)], 1).contiguous()
+    emap = torch.arange(local, dtype=torch.int32, device=device)
+    x = torch.randn(tokens, hidden, generator=gen, device=device).half()
+    out = torch.empty_like(x)
+    ws = torch.empty(ops.moe_workspace_size_v2(tokens, hidden, inter, topk + 1, local),
+                     dtype=torch.float32, device=device)
+
+    def call(i):
+        ops.moe_out_v2(x, ids.contiguous(), weights, ptrs, meta, emap, inter, bits_x2, out, ws)
+
+    ms, _, _ = time_graph(torch, call, 10, 10, 50)
+    touched = int(torch.unique(ids).numel())
+    per_expert = 3 * hidden * inter * bits_x2 // 16 + 2 * 2 * (hidden + inter) + 2 * (hidden + inter)
+    nbytes = touched * per_expert + 2 * 2 * tokens * hidden
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del keep
+    return {"workload": (f"{experts}+1 experts, {hidden}/{inter}, {bits_x2 / 2:g}-bit mul1, top-{topk} "
+                         f"Zipf(1.1), {tokens} tokens, fp16"),
+            "us_per_forward": round(ms * 1e3, 1), "tokens_per_s": round(tokens / (ms * 1e-3)),
+            "experts_touched": touched, "hbm_gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def cpu_baseline(seconds: float, torch):
     from oracle.exl3_torch_ref import DenseDecoder, linear_fp64
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(99)
     trellis = torch.randint(-(2 ** 15), 2 ** 15, (K_IN // 16, N_OUT // 16, 8 * BITS_X2),
                             dtype=torch.int16, generator=g)
@@ -146,16 +352,29 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=120)
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--no-extras", action="store_true",
+                        help="only the headline GEMV (profiling runs)")
+    parser.add_argument("--copy-mb", type=int, default=0,
+                        help="also run 10 plain device copies of this many MiB (the counter "
+                             "calibration of FETCH_SIZE / WRITE_SIZE)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(the hot path is a single-GPU kernel; see DESIGN.md for how it would shard)",
+              "(the hot path is a single-GPU kernel; multi-GPU sharding is not built here)",
               file=sys.stderr)
         return 2
 
     import torch
 
+    torch.set_num_threads(os.cpu_count() or 1)
     ms, steps, warm = gpu_gemv(args, torch)
+    if args.copy_mb:
+        src = torch.ones(args.copy_mb << 18, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     nbytes = gemv_bytes(K_IN, N_OUT, BITS_X2, ROWS)
     gbs = nbytes / (ms * 1e-3) / 1e9
     result = {
@@ -183,11 +402,26 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
     }
+    if not args.no_extras:
+        moe = gpu_marlin_moe(torch)
+        at256 = moe["256"]
+        result["int4_moe"] = {
+            "workload": "Marlin int4 fused MoE, 128 experts, hidden 2048, inter 768, top-8, fp16",
+            "tokens_per_s_at_256": at256["tokens_per_s"],
+            "mfma_util_at_256": at256["mfma_util"],
+            "hbm_frac_at_256": at256["hbm_frac"],
+            "bound_at_256": "hbm",
+            "by_tokens": moe,
+        }
+        result["exl3_prefill"] = gpu_exl3_prefill(torch)
+        result["exl3_moe"] = gpu_exl3_moe(torch)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, torch)
+        if not args.no_extras:
+            result["int4_moe"]["cpu_baseline"] = cpu_marlin_moe(args.cpu_seconds, torch)
     print(json.dumps(result))
     return 0
 

@@ -281,3 +281,30 @@ def test_align_with_expert_map_and_invalid_ids():
     s, eids, ntpp = M.align(ids, E, 8, expert_map=emap)
     es, eeids, entpp = spec_align(ids, E, 8, expert_map=emap)
     assert ntpp[0] == entpp and np.array_equal(s, es) and np.array_equal(eids, eeids)
+
+
+def test_torch_cpu_path_matches_the_oracle_layout():
+    """oracle/marlin_torch_ref.py (the bench's CPU baseline) dequantizes to
+    the unrounded (q - 8) s of the pinned layout, and its MoE is the FP64
+    restatement above with unrounded weights."""
+    import torch
+    from oracle import marlin_torch_ref as R
+    rng = np.random.default_rng(21)
+    E, K, N, topk, T = 3, 256, 128, 2, 4
+    layer = make_layer(rng, E, K, N, M.BF16)
+    w13, s13, w2, s2 = layer
+    q = M.unpack(w13[1], K, 2 * N).astype(np.float64) - 8.0
+    sc = to_f32(s13[1], M.BF16)[:, M.scale_positions(2 * N)].astype(np.float64)
+    expect = q * np.repeat(sc, 128, axis=0)
+    s13_t = torch.from_numpy(s13.view(np.int16)).view(torch.bfloat16)
+    got = R.dequant_fp64(torch.from_numpy(w13[1]), s13_t[1], K, 2 * N).numpy()
+    assert np.array_equal(got, expect)
+    x = from_f32(rng.standard_normal((T, K)), M.BF16)
+    ids = np.array([[0, 2], [1, 0], [2, 1], [0, 1]], np.int32)
+    w = rng.random((T, topk)).astype(np.float32)
+    s2_t = torch.from_numpy(s2.view(np.int16)).view(torch.bfloat16)
+    x_t = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    got = R.moe_fp64(x_t, torch.from_numpy(ids), torch.from_numpy(w), torch.from_numpy(w13),
+                     torch.from_numpy(w2), s13_t, s2_t, clamp=10.0).numpy()
+    want = spec_moe(x, M.BF16, ids, w, layer, 10.0, rounded_weights=False)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)

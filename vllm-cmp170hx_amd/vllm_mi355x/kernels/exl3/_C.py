@@ -51,7 +51,53 @@ SCHEMAS = {
     "moe_workspace_size_v2": (
         "moe_workspace_size_v2(int max_rows, int hidden_size, int intermediate_size, "
         "int topk, int local_experts) -> int"),
+    # PLE rows (out of this build's scope): registered so the reference's
+    # loader finds every operator it checks; calling them raises.
+    "ple_decode_out": (
+        "ple_decode_out(Tensor packed_rows, Tensor global_ids, Tensor head_bias, "
+        "Tensor head_offsets, Tensor head_vocab_sizes, int owner_lo, "
+        "int owner_hi, int bits, Tensor(a!) out) -> ()"),
+    "ple_read_rows": (
+        "ple_read_rows(int fd, Tensor ids, Tensor(a!) dest, int count, "
+        "int base, int row_bytes, int owner_lo, int owner_hi, "
+        "Tensor head_offsets, Tensor head_vocab_sizes, int retries, "
+        "int max_threads) -> Tensor"),
+    "linear_prefill_applies": (
+        "linear_prefill_applies(int rows, int padded_in, int padded_out, int bits_x2, "
+        "int codebook) -> bool"),
+    "set_prefill_schedule": "set_prefill_schedule(int mode) -> ()",
+    "set_gemm_shape_override": "set_gemm_shape_override(int shape) -> ()",
+    "moe_v2_draft_force_rows": "moe_v2_draft_force_rows(int rows) -> ()",
 }
+
+# The reference's variants with the same contracts (module.cpp:13-58 and the
+# fragments of dense_prefill_tc.cu:619-631, moe_v2.cu:2234-2250,
+# moe_prefill_v2.cu:1162-1175, moe_prefill_try.cu:1381-1399,
+# moe_v2_try.cu:1542-1559): each is served by one of the operators above.
+_LINEAR_ALIASES = ("linear_out_prefill",)
+_MOE_ALIASES = ("moe_out_mixed", "moe_out_prefill")               # moe_out's signature
+_MOE_V2_ALIASES = ("moe_out_v2_fold", "moe_out_prefill_v2", "moe_out_prefill_try")
+_MOE_V2_MIXED = ("moe_out_v2_mixed", "moe_out_prefill_try_mixed")  # any format per expert
+_MOE_V2_TRY = ("moe_out_v2_try", "moe_out_v2_try_mixed")          # swiglu_limit required
+_SIZE_ALIASES = ("moe_workspace_size_prefill", "moe_workspace_size_prefill_v2",
+                 "moe_workspace_size_prefill_try", "moe_workspace_size_v2_try")
+
+
+def _alias_schema(base: str, name: str) -> str:
+    return SCHEMAS[base].replace(f"{base}(", f"{name}(", 1)
+
+
+for _n in _LINEAR_ALIASES:
+    SCHEMAS[_n] = _alias_schema("linear_out", _n)
+for _n in _MOE_ALIASES:
+    SCHEMAS[_n] = _alias_schema("moe_out", _n)
+for _n in _MOE_V2_ALIASES + _MOE_V2_MIXED:
+    SCHEMAS[_n] = _alias_schema("moe_out_v2", _n)
+for _n in _MOE_V2_TRY:
+    SCHEMAS[_n] = _alias_schema("moe_out_v2", _n).replace("float swiglu_limit=0.0",
+                                                          "float swiglu_limit")
+for _n in _SIZE_ALIASES:
+    SCHEMAS[_n] = _alias_schema("moe_workspace_size", _n)
 
 _library = None
 
@@ -190,6 +236,27 @@ def moe_workspace_size_impl(max_rows, hidden_size, intermediate_size, topk, loca
     return int(size)
 
 
+def moe_out_v2_mixed_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+                          intermediate_size, bits_x2, out, workspace, swiglu_limit=0.0) -> None:
+    """The _mixed variants: every expert's own format, decoded at run time."""
+    _moe_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map, intermediate_size,
+              0, out, workspace, swiglu_limit)
+
+
+def ple_unavailable(*args, **kwargs):
+    raise NotImplementedError("PLE row decoding is not part of the gfx950 quantized-matmul library")
+
+
+def linear_prefill_applies_impl(rows, padded_in, padded_out, bits_x2, codebook) -> bool:
+    """The decode-to-LDS MFMA GEMM serves every format above 8 rows."""
+    return int(rows) > 8
+
+
+def _no_op(*args) -> None:
+    """Tuning switches of the reference's sm_80 kernels; one kernel family
+    serves every shape here."""
+
+
 def build_info() -> dict:
     """The handshake the reference's loader compares (module.cpp:91-99);
     ROCm has no CUDA runtime, so cuda_version is 0 and hip_version is set."""
@@ -222,4 +289,19 @@ def register() -> None:
     lib.impl("moe_workspace_size", moe_workspace_size_impl, "CompositeImplicitAutograd")
     lib.impl("moe_workspace_size_v2", moe_workspace_size_impl, "CompositeImplicitAutograd")
     lib.impl("linear_splitk_splits", linear_splitk_splits_impl, "CompositeImplicitAutograd")
+    for name in _LINEAR_ALIASES:
+        lib.impl(name, linear_out_impl, "CUDA")
+    for name in _MOE_ALIASES:
+        lib.impl(name, moe_out_impl, "CUDA")
+    for name in _MOE_V2_ALIASES + _MOE_V2_TRY:
+        lib.impl(name, moe_out_v2_impl, "CUDA")
+    for name in _MOE_V2_MIXED:
+        lib.impl(name, moe_out_v2_mixed_impl, "CUDA")
+    for name in _SIZE_ALIASES:
+        lib.impl(name, moe_workspace_size_impl, "CompositeImplicitAutograd")
+    lib.impl("ple_decode_out", ple_unavailable, "CUDA")
+    lib.impl("ple_read_rows", ple_unavailable, "CompositeImplicitAutograd")
+    lib.impl("linear_prefill_applies", linear_prefill_applies_impl, "CompositeImplicitAutograd")
+    for name in ("set_prefill_schedule", "set_gemm_shape_override", "moe_v2_draft_force_rows"):
+        lib.impl(name, _no_op, "CompositeImplicitAutograd")
     _library = lib

@@ -25,9 +25,12 @@ LINEAR_SCRATCH_ELEMENTS = 8 << 20
 # FP32 stores it (reference ops.py:114, plus FP16 for FP16 models).
 LINEAR_OUT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
-_OPERATORS = ("linear_out", "linear_out_splitk", "linear_workspace_size",
-              "linear_splitk_splits", "exl3_decode", "moe_out", "moe_out_v2",
-              "moe_workspace_size", "moe_workspace_size_v2")
+# The operators the reference's loader requires (ops.py:193-207), plus this
+# library's decode.
+_OPERATORS = ("linear_out", "linear_out_splitk", "moe_out", "moe_out_v2", "moe_out_prefill",
+              "ple_decode_out", "ple_read_rows", "linear_workspace_size",
+              "linear_splitk_splits", "moe_workspace_size", "moe_workspace_size_v2",
+              "moe_workspace_size_prefill", "exl3_decode")
 
 
 def _linear_fake(x, trellis, suh, svh, bits_x2, codebook, logical_in, logical_out, out,
@@ -77,8 +80,13 @@ def ensure_extension() -> None:
             f"python vllm-cmp170hx_amd/build.py. Detail: {exc}") from exc
     for name in ("linear_out", "linear_out_splitk"):
         torch.library.register_fake(f"_exl3_C::{name}")(_linear_fake)
-    torch.library.register_fake("_exl3_C::moe_out")(_moe_fake)
-    torch.library.register_fake("_exl3_C::moe_out_v2")(_moe_v2_fake)
+    for name in ("moe_out", "moe_out_prefill", "moe_out_mixed"):
+        torch.library.register_fake(f"_exl3_C::{name}")(_moe_fake)
+    for name in ("moe_out_v2", "moe_out_v2_fold", "moe_out_v2_mixed", "moe_out_prefill_v2",
+                 "moe_out_prefill_try", "moe_out_prefill_try_mixed", "moe_out_v2_try",
+                 "moe_out_v2_try_mixed"):
+        torch.library.register_fake(f"_exl3_C::{name}")(_moe_v2_fake)
+    torch.library.register_fake("_exl3_C::linear_out_prefill")(_linear_fake)
     _loaded = True
 
 
