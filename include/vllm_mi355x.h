@@ -135,6 +135,16 @@ int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hidden, const
 int exl3_set_gemv_finish(int mode);
 
 /*
+ * Test and tuning switch, process-wide: 128-input blocks per workgroup of
+ * the small-M kernel (0 = automatic, 1, 2, 4 or 8; more blocks = fewer K
+ * splits; a value that does not divide padded_in / 128 is ignored for that
+ * call).  Changes the FP32 summation grouping, not the weights.  No
+ * counterpart in the reference (its nearest is set_gemm_shape_override,
+ * csrc/exl3/gemm.cu:400-409).
+ */
+int exl3_set_gemv_blocks(int blocks);
+
+/*
  * Decodes every tile of a trellis into its exact FP16 weights,
  * out[k][n] (k < 16 * tiles_k, n < 16 * tiles_n, row-major, FP16 bits).
  * The inspection form of the decode exl3_linear_out fuses; it has no

@@ -60,21 +60,67 @@ __device__ __forceinline__ void store_act(void* p, int dtype, int64_t i, float v
 
 constexpr float kH128Scale = 0.08838834764831845f;
 
+// v from lane (lane ^ d) of the wavefront, for d = 1, 2, ..., 32, without
+// the address arithmetic of a generic shuffle: DPP quad permutes (d = 1, 2),
+// a row shift left / right split by DPP bank mask (d = 4), a row rotate
+// (d = 8), ds_swizzle's xor mode within 32 lanes (d = 16) and one
+// ds_bpermute (d = 32).  Every lane must be active.
+template <int d>
+__device__ __forceinline__ float xor_lanes(float v, int lane) {
+  const int x = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (d == 1) {
+    r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);          // quad_perm [1,0,3,2]
+  } else if constexpr (d == 2) {
+    r = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);          // quad_perm [2,3,0,1]
+  } else if constexpr (d == 4) {
+    r = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);   // row_shl:4, lanes 0-3, 8-11
+    r = __builtin_amdgcn_update_dpp(r, x, 0x114, 0xF, 0xA, false);   // row_shr:4, lanes 4-7, 12-15
+  } else if constexpr (d == 8) {
+    r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);         // row_ror:8
+  } else if constexpr (d == 16) {
+    r = __builtin_amdgcn_ds_swizzle(x, 0x401F);                      // and 0x1f, xor 0x10
+  } else {
+    static_assert(d == 32, "xor distance");
+    r = __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, x);
+  }
+  return __builtin_bit_cast(float, r);
+}
+
+// Max over the wavefront (every lane gets it).
+__device__ __forceinline__ float wave_max(float v, int lane) {
+  v = fmaxf(v, xor_lanes<32>(v, lane));
+  v = fmaxf(v, xor_lanes<16>(v, lane));
+  v = fmaxf(v, xor_lanes<8>(v, lane));
+  v = fmaxf(v, xor_lanes<4>(v, lane));
+  v = fmaxf(v, xor_lanes<2>(v, lane));
+  v = fmaxf(v, xor_lanes<1>(v, lane));
+  return v;
+}
+
 // H128 of one 128-value block held by a wavefront: lane l holds elements l
 // (v0) and l + 64 (v1).  Butterfly distances 1, 2, ..., 64 in increasing
 // order; the lower element becomes lo + hi and the upper one lo - hi (FP32
 // round to nearest), then both are scaled by 1/sqrt(128).  The same
 // operations in the same order as the reference (reference.cu:107-122,
-// codec.cuh:186-209), so the transform is bit-identical to it.
+// codec.cuh:186-209), so the transform is bit-identical to it.  (The upper
+// lane's partner - v is computed as partner + (-v): the same rounding.)
+template <int d>
+__device__ __forceinline__ void h128_stage(float& v0, float& v1, int lane) {
+  const float o0 = xor_lanes<d>(v0, lane);
+  const float o1 = xor_lanes<d>(v1, lane);
+  const bool upper = (lane & d) != 0;
+  v0 = o0 + (upper ? -v0 : v0);
+  v1 = o1 + (upper ? -v1 : v1);
+}
+
 __device__ __forceinline__ void h128_wave(float& v0, float& v1, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const float o0 = __shfl_xor(v0, d);
-    const float o1 = __shfl_xor(v1, d);
-    const bool upper = (lane & d) != 0;
-    v0 = upper ? o0 - v0 : v0 + o0;
-    v1 = upper ? o1 - v1 : v1 + o1;
-  }
+  h128_stage<1>(v0, v1, lane);
+  h128_stage<2>(v0, v1, lane);
+  h128_stage<4>(v0, v1, lane);
+  h128_stage<8>(v0, v1, lane);
+  h128_stage<16>(v0, v1, lane);
+  h128_stage<32>(v0, v1, lane);
   const float lo = v0 + v1;
   const float hi = v0 - v1;
   v0 = lo * kH128Scale;

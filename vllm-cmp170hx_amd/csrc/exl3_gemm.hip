@@ -71,8 +71,7 @@ __global__ __launch_bounds__(256) void prefill_input(const void* __restrict__ x,
     form(b, v0, v1);
     mx = fmaxf(mx, fmaxf(fabsf(v0), fabsf(v1)));
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+  mx = vq::wave_max(mx, lane);
   if (lane == 0) atomicMax(&row_max, __builtin_bit_cast(uint32_t, mx));
   __syncthreads();
   const int e = scale_exponent(row_max);

@@ -18,10 +18,12 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // Every (bits_x2, codebook) the format admits (reference: csrc/exl3/gemm.cu:
 // 17-20, kernels/exl3/utils.py:283-285): even rates 1..8 bits for both
 // codebooks, and 1.5 / 2.5 / 3.5 bits for mul1.
+#ifndef VQ_EXL3_FORMATS
 #define VQ_EXL3_FORMATS(X)                                                       \
   X(2, 1) X(4, 1) X(6, 1) X(8, 1) X(10, 1) X(12, 1) X(14, 1) X(16, 1)           \
   X(2, 2) X(3, 2) X(4, 2) X(5, 2) X(6, 2) X(7, 2) X(8, 2) X(10, 2) X(12, 2)    \
   X(14, 2) X(16, 2)
+#endif
 
 inline bool known_format(int64_t bits_x2, int64_t codebook) {
 #define VQ_KNOWN(B, C) if (bits_x2 == B && codebook == C) return true;

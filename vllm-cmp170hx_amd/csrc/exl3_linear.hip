@@ -55,12 +55,22 @@ constexpr int kMaxGemvRows = 8;
 
 // Per-rate geometry of the small-M kernel.
 //
-// Up to 4 bits per weight (bits_x2 <= 8) a wavefront's two tiles of one tile
-// row are at most 64 dwords: each lane loads one of them with one coalesced
-// global_load_dword (every trellis byte is fetched once, in whole cache
-// lines), and each decoding lane then gathers the ring words of its encoder
-// lane from the loading lanes with ds_bpermute.  Wider rates load each lane's
-// window words directly.
+// A wavefront's two tiles of one tile row (its "chunk") are 32 * bits_x2
+// contiguous bytes.  Three ways to bring them in:
+//  * kLoadLds (16-byte aligned trellis, the fast path): buffer_load_dwordx4
+//    ... lds copies whole chunks straight into a per-wavefront LDS ring, one
+//    kilobyte (kStepsPerLoad steps of two tile rows) per instruction, with
+//    the tile row in the scalar offset.  Decoding lanes then read their ring
+//    words with ds_read_b32 at immediate offsets.  No VGPR staging, so deep
+//    prefetch costs no registers.
+//  * kLoadDword (4-byte aligned): up to 4 bits per weight each lane loads
+//    one dword of the chunk (coalesced) and decoding lanes gather their ring
+//    words with ds_bpermute; wider rates load each lane's window words.
+//  * kLoadHalf (2-byte aligned): as kLoadDword, two halfword loads a word.
+constexpr int kLoadHalf = 0;
+constexpr int kLoadDword = 1;
+constexpr int kLoadLds = 2;
+
 template <int kBitsX2>
 struct Gemv {
   static constexpr bool kCoalesced = kBitsX2 <= 8;
@@ -69,6 +79,12 @@ struct Gemv {
   static constexpr int kRaw = kCoalesced ? 1 : 2 * kWords;
   // steps of loads each wavefront keeps in flight
   static constexpr int kDepth = 32 / (2 * kRaw);
+  // LDS stream: bytes of one chunk, lanes loading one chunk (16 bytes each),
+  // steps (two tile rows) per 1 KB load, loads kept in flight
+  static constexpr int kChunk = 32 * kBitsX2;
+  static constexpr int kChunkLanes = kChunk / 16;
+  static constexpr int kStepsPerLoad = kBitsX2 <= 4 ? 4 : (kBitsX2 <= 8 ? 2 : 1);
+  static constexpr int kStepsInFlight = 8;
 };
 
 // Byte offsets (within a tile) of the words encoder lane L needs.
@@ -126,7 +142,6 @@ struct GemvArgs {
   int x_dtype;
   int out_dtype;
   int rows;              // 1..8
-  int steps_total;       // padded_in / 32
   int splits;            // K splits (padded_in / 128)
 };
 
@@ -138,6 +153,17 @@ struct GemvArgs {
 constexpr int kCounterBanks = 64;
 constexpr int kCounterSlots = 2048;
 __device__ uint32_t g_gemv_counters[kCounterBanks * kCounterSlots];
+
+// Four consecutive partial sums at byte offset `offset` of buffer `r`,
+// written through to the device-coherent level (cache policy sc1, that of an
+// agent-scope store), so a workgroup on another XCD reads them after the
+// arrival counter says they are complete.  A builtin rather than inline
+// assembly: the compiler must see the 16-byte store to keep the VALU off its
+// data registers for the cycle after it issues.
+constexpr int kCachePolicySc1 = 16;
+__device__ __forceinline__ void store_agent_x4(__amdgpu_buffer_rsrc_t r, int offset, f32x4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, offset, 0, kCachePolicySc1);
+}
 
 // A partial sum: agent-scope (bypassing caches that may hold another
 // call's data) in the fused finish, plain in the separate output kernel.
@@ -239,40 +265,74 @@ __device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int 
   }
 }
 
-// One workgroup = 4 wavefronts = 128 output columns (one H128 block) x up to
-// kBlocks 128-input blocks (4 steps of 32 inputs each).  Wavefront w owns
-// the column pair 4 * blockIdx.x + w (two tile columns, 32 outputs) over the
-// whole K range and streams its trellis through a ring of kDepth steps of
-// loads in flight.
+// s_waitcnt with only vmcnt <= n (the other counters unconstrained), and a
+// compiler barrier: LDS reads of data an LDS-DMA load wrote must not move
+// above it.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt lgkmcnt(0) only: every LDS read issued so far has returned.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+  asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// One workgroup = 4 wavefronts = 128 output columns (one H128 block) x
+// kBlocks 128-input blocks (4 steps of 32 inputs each; the host picks kBlocks
+// dividing the input blocks, so every workgroup's range is whole).  Wavefront
+// w owns the column pair 4 * blockIdx.x + w (two tile columns, 32 outputs)
+// over the range and streams its trellis chunks (kLoad: see Gemv).
 //
 // kRows (1, 2, 4 or 8) is the row count the kernel is built for; a call with
 // fewer rows (a.rows) computes its last row in the padding rows, which are
 // never stored.
-template <int kBitsX2, int kCodebook, bool kAligned, int kRows, int kBlocks>
+template <int kBitsX2, int kCodebook, int kLoad, int kRows, int kBlocks>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   using G = Gemv<kBitsX2>;
   using R = Ring<kBitsX2>;
+  constexpr bool kLds = kLoad == kLoadLds;
+  constexpr bool kAligned = kLoad != kLoadHalf;
   constexpr int kSteps = 4 * kBlocks;
   constexpr int kDepth = G::kDepth < kSteps ? G::kDepth : kSteps;
   constexpr int kCols = 2 * kRows;                        // B columns: hi, lo per row
   constexpr int kActHalves = kSteps * 4 * kCols * 8;      // B operands of the range
   constexpr int kTasks = kBlocks * kRows;                 // (block, row) forming tasks
   constexpr int kFormTasks = (kTasks + 3) / 4;            // per wavefront
-  // activations in B-operand order, then 8 zero halves: the B operand of
-  // the unused columns.  Reused by the fused finish for its row sums.
-  __shared__ __attribute__((aligned(16))) _Float16 act[kActHalves + 8 > 2 * 128 * kRows * 2 ? kActHalves + 8 : 2 * 128 * kRows * 2];
+  // LDS stream: loads of the range, loads in flight per wavefront
+  constexpr int kP = G::kStepsPerLoad;
+  constexpr int kLoads = kSteps / kP;
+  constexpr int kRingWant = G::kStepsInFlight / kP < 4 ? G::kStepsInFlight / kP : 4;
+  constexpr int kRingLoads = kLds ? (kRingWant < kLoads ? kRingWant : kLoads) : 1;
+  // Rotated loading order of the 4-bit chunk (dword loads, see below).
+  constexpr bool kRotate = kBitsX2 == 8 && !kLds;
+  static_assert(kSteps % kP == 0, "whole loads per range");
+  // activations in B-operand order.  Reused by the fused finish for its row
+  // sums.
+  __shared__ __attribute__((aligned(16))) _Float16 act[kActHalves > 2 * 128 * kRows * 2 ? kActHalves : 2 * 128 * kRows * 2];
   __shared__ int block_exp[kBlocks][kRows];
+  // LDS stream: kRingLoads slots of 1 KB (kP steps) per wavefront, one
+  // array per slot: the compiler's wait for an LDS-DMA load before a read
+  // of its data then names that load, not every load in flight.
+  constexpr int kSlotWords = kLds ? 4 * 256 : 4;
+  __shared__ __attribute__((aligned(16))) uint32_t ring0[kSlotWords];
+  __shared__ __attribute__((aligned(16))) uint32_t ring1[kRingLoads > 1 ? kSlotWords : 4];
+  __shared__ __attribute__((aligned(16))) uint32_t ring2[kRingLoads > 2 ? kSlotWords : 4];
+  __shared__ __attribute__((aligned(16))) uint32_t ring3[kRingLoads > 3 ? kSlotWords : 4];
+  static_assert(kRingLoads <= 4, "four ring slots");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4;
   const int m = lane & 15;
   const int L = 4 * (m & 7) + g;
-  const int blocks_total = a.steps_total / 4;
   const int block0 = blockIdx.y * kBlocks;
-  const int nblocks = min(kBlocks, blocks_total - block0);
-  const int nsteps = 4 * nblocks;
   const int64_t k0 = int64_t(block0) * 128;
 
   // a. activation loads first (they must not queue behind the trellis).
@@ -286,7 +346,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 #pragma unroll
   for (int f = 0; f < kFormTasks; ++f) {
     const int t = wave + 4 * f;
-    const int b = min(t / kRows, nblocks - 1);
+    const int b = min(t / kRows, kBlocks - 1);
     const int64_t row = int64_t(min(t % kRows, a.rows - 1)) * a.logical_in;
     const int64_t k_0 = k0 + 128 * b + lane;
     const int64_t k_1 = k_0 + 64;
@@ -299,48 +359,101 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   }
 #pragma unroll
   for (int f = 0; f < kFormTasks; ++f) {
-    const int b = min((wave + 4 * f) / kRows, nblocks - 1);
+    const int b = min((wave + 4 * f) / kRows, kBlocks - 1);
     const int64_t k_0 = k0 + 128 * b + lane;
     if (!(k_0 < a.logical_in)) { sv[f][0] = 0u; xv[f][0] = 0u; }
     if (!(k_0 + 64 < a.logical_in)) { sv[f][1] = 0u; xv[f][1] = 0u; }
   }
 
-  // b. the first kDepth steps of trellis loads.  raw[j][h] holds tile row
-  //    2j + h of this wavefront's two tiles (coalesced: dword `lane` of the
-  //    2-tile chunk; direct: this lane's window words, tile m >> 3).
+  // b. the first trellis loads.  The wavefront's chunk of tile row 0 is the
+  //    base of a buffer resource, the tile row a scalar offset.
   int off[G::kWords];
   lane_word_offsets<kBitsX2>(L, off);
-  const int64_t row_bytes = a.tiles_n * R::kTileBytes;
+  const int row_bytes = int(a.tiles_n) * R::kTileBytes;
   const uint8_t* chunk = a.trellis + 2 * (4 * int64_t(blockIdx.x) + wave) * R::kTileBytes +
                          8 * int64_t(block0) * row_bytes;
-  const int raw_off = lane < 8 * kBitsX2 ? 4 * lane : 0;  // lanes past the chunk reload dword 0
+  const __amdgpu_buffer_rsrc_t trellis_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(chunk), 0, (8 * kBlocks - 1) * row_bytes + 2 * R::kTileBytes, 0x00020000);
   const int tile_off = (m >> 3) * R::kTileBytes;
-  uint32_t raw[kSteps][2][G::kRaw];
+
+  //    LDS stream: load i (steps kP*i ..) fills ring slot i % kRingLoads of
+  //    this wavefront: lane l copies 16 bytes, part l % kChunkLanes of tile
+  //    row l / kChunkLanes of the load (lanes past the load's rows copy part
+  //    0 of its first row again, into the slot's unread tail).
+  auto slot_of_load = [&](int i) -> uint32_t* {
+    switch (i % kRingLoads) {
+      case 0: return ring0 + wave * 256;
+      case 1: return ring1 + wave * 256;
+      case 2: return ring2 + wave * 256;
+      default: return ring3 + wave * 256;
+    }
+  };
+  const int dma_off = lane < 2 * kP * G::kChunkLanes
+                          ? (lane / G::kChunkLanes) * row_bytes + 16 * (lane % G::kChunkLanes)
+                          : 0;
+  auto load_lds = [&](int i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(trellis_rsrc, (lds_ptr_t)slot_of_load(i), 16, dma_off,
+                                             i * 2 * kP * row_bytes, 0, 0);
+  };
+
+  //    Dword / halfword loads: raw[j][h] holds tile row 2j + h of this
+  //    wavefront's two tiles (coalesced: one dword of the chunk; direct: this
+  //    lane's window words, tile m >> 3).  4-bit chunks load rotated: lane l
+  //    holds word ((l & 31) - 2t) & 31 of tile t = l >> 5, so the two words
+  //    each decoding lane gathers below come, across each half-wavefront,
+  //    from 32 distinct lanes mod 32 (no ds_bpermute bank conflict between
+  //    the two tiles).
+  const int raw_off = kRotate ? 4 * (32 * (lane >> 5) + (((lane & 31) - 2 * (lane >> 5)) & 31))
+                              : (lane < 8 * kBitsX2 ? 4 * lane : 0);  // lanes past the chunk reload dword 0
+  uint32_t raw[kLds ? 1 : kSteps][2][G::kRaw];
   auto load_step = [&](int j) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint8_t* row = chunk + (2 * j + h) * row_bytes;
+      const int row = (2 * j + h) * row_bytes;
       if constexpr (G::kCoalesced) {
-        raw[j][h][0] = tile_word<kAligned>(row, raw_off);
+        if constexpr (kAligned) {
+          raw[j][h][0] = __builtin_amdgcn_raw_buffer_load_b32(trellis_rsrc, raw_off, row, 0);
+        } else {
+          raw[j][h][0] = tile_word<false>(chunk + row, raw_off);
+        }
       } else {
 #pragma unroll
-        for (int i = 0; i < G::kWords; ++i) raw[j][h][i] = tile_word<kAligned>(row + tile_off, off[i]);
+        for (int i = 0; i < G::kWords; ++i) {
+          if constexpr (kAligned) {
+            raw[j][h][i] = __builtin_amdgcn_raw_buffer_load_b32(trellis_rsrc, tile_off + off[i], row, 0);
+          } else {
+            raw[j][h][i] = tile_word<false>(chunk + row + tile_off, off[i]);
+          }
+        }
       }
     }
   };
+  // (the activation loads above are issued first)
+  asm volatile("" ::: "memory");
+  if constexpr (kLds) {
 #pragma unroll
-  for (int j = 0; j < kDepth; ++j) {
-    if (j < nsteps) load_step(j);
+    for (int i = 0; i < kRingLoads; ++i) load_lds(i);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j) load_step(j);
   }
-  // coalesced: ds_bpermute byte addresses of the lanes holding this lane's words
+  // dword loads: ds_bpermute byte addresses of the lanes holding this lane's
+  // words; LDS stream: this lane's word addresses within a slot's tile row
   int src[G::kWords];
 #pragma unroll
-  for (int i = 0; i < G::kWords; ++i) src[i] = 4 * ((m >> 3) * 4 * kBitsX2 + off[i] / 4);
+  for (int i = 0; i < G::kWords; ++i) {
+    const int t = m >> 3;
+    const int w = off[i] / 4;
+    if constexpr (kLds) {
+      src[i] = (tile_off + off[i]) / 4;
+    } else {
+      src[i] = kRotate ? 4 * (32 * t + ((w + 2 * t) & 31)) : 4 * (t * 4 * kBitsX2 + w);
+    }
+  }
 
   // c. forming: t = H128(x * suh) of a (block, row), split at a power-of-two
   //    scale into FP16 high / low parts, written straight into B-operand
   //    order: act = [step][g][B column 2r + (0 hi | 1 lo)][8 halves].
-  if (tid < 8) act[kActHalves + tid] = _Float16(0.0f);
   {
     // half index of input k (within a block) at B column 0
     auto slot_of = [&](int k) {
@@ -358,13 +471,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
       const int t = wave + 4 * f;
       const int b = t / kRows;
       const int r = t % kRows;
-      if (t < kTasks && b < nblocks) {
+      if (t < kTasks) {
         float v0 = u16_act(uint16_t(xv[f][0]), a.x_dtype) * vq::f16_to_f32(uint16_t(sv[f][0]));
         float v1 = u16_act(uint16_t(xv[f][1]), a.x_dtype) * vq::f16_to_f32(uint16_t(sv[f][1]));
         vq::h128_wave(v0, v1, lane);
-        float mx = fmaxf(fabsf(v0), fabsf(v1));
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+        const float mx = vq::wave_max(fmaxf(fabsf(v0), fabsf(v1)), lane);
         const int e = scale_exponent(__builtin_bit_cast(uint32_t, mx));
         if (lane == 0) block_exp[b][r] = e;
         const float t0 = ldexpf(v0, e);
@@ -382,8 +493,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   // d. stream: decode step j while later steps are in flight.  Each block's
   //    products accumulate in acc1/acc2 from zero and are folded, unscaled,
   //    into tot1/tot2 (high + low parts: B columns 2r, 2r + 1 sit in
-  //    adjacent lanes) at the block's end, blocks in order.
-  uint32_t wv[kSteps][2][G::kWords];
+  //    adjacent lanes) at the block's end, blocks in order.  Lanes m >= kCols
+  //    read B column m % kCols again: their MFMA columns are never used.
+  uint32_t wv[kLds ? 1 : kSteps][2][G::kWords];
   auto gather = [&](int j) {
 #pragma unroll
     for (int i = 0; i < G::kWords; ++i) {
@@ -396,39 +508,94 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
       }
     }
   };
-  const char* lds = reinterpret_cast<const char*>(act);
+  const half8_t* bops = reinterpret_cast<const half8_t*>(act) + g * kCols + (m % kCols);
   const int r_own = (m >> 1) < kRows ? (m >> 1) : 0;
   f32x4_t acc1 = {}, acc2 = {};
   float tot1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float tot2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  gather(0);
+  half8_t bop = {};
+  if constexpr (!kLds) gather(0);
 #pragma unroll
   for (int j = 0; j < kSteps; ++j) {
-    if (j < nsteps) {
-      if (j + 1 < kSteps && j + 1 < nsteps) gather(j + 1);
-      if (j + kDepth < kSteps && j + kDepth < nsteps) load_step(j + kDepth);
-      uint32_t q0[4], q1[4];
-      decode_words<kBitsX2, kCodebook>(L, wv[j][0], q0);
-      decode_words<kBitsX2, kCodebook>(L, wv[j][1], q1);
-      // the activations are complete once every wavefront is past here (the
-      // first decode overlaps the wait)
-      if (j == 0) __syncthreads();
-      const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
-      const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
-      const half8_t bop = *reinterpret_cast<const half8_t*>(
-          lds + (m < kCols ? ((j * 4 + g) * kCols + m) * 16 : kActHalves * 2));
-      const f32x4_t zero = {};
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), bop,
-                                                    (j & 3) == 0 ? zero : acc1, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), bop,
-                                                    (j & 3) == 0 ? zero : acc2, 0, 0, 0);
-      if ((j & 3) == 3) {
-        const int e = block_exp[j >> 2][r_own];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          tot1[i] += ldexpf(acc1[i] + __shfl_xor(acc1[i], 1), -e);
-          tot2[i] += ldexpf(acc2[i] + __shfl_xor(acc2[i], 1), -e);
+    uint32_t w0[G::kWords], w1[G::kWords];
+    if constexpr (kLds) {
+      const int i = j / kP;
+      if (j % kP == 0) {
+        // load i has landed: at most the loads issued after it are pending
+        if (i + kRingLoads - 1 < kLoads) {
+          wait_vmcnt<kRingLoads - 1>();
+        } else {
+          // the tail: no loads were issued after the last kRingLoads
+          switch (kLoads - 1 - i) {
+            case 0: wait_vmcnt<0>(); break;
+            case 1: wait_vmcnt<1>(); break;
+            case 2: wait_vmcnt<2>(); break;
+            case 3: wait_vmcnt<3>(); break;
+            case 4: wait_vmcnt<4>(); break;
+            case 5: wait_vmcnt<5>(); break;
+            case 6: wait_vmcnt<6>(); break;
+            default: wait_vmcnt<7>(); break;
+          }
         }
+      }
+      const uint32_t* slot = slot_of_load(i) + (2 * (j % kP)) * (G::kChunk / 4);
+#pragma unroll
+      for (int q = 0; q < G::kWords; ++q) {
+        w0[q] = slot[src[q]];
+        w1[q] = slot[G::kChunk / 4 + src[q]];
+      }
+    } else {
+      if (j + 1 < kSteps) gather(j + 1);
+      if (j + kDepth < kSteps) load_step(j + kDepth);
+#pragma unroll
+      for (int q = 0; q < G::kWords; ++q) {
+        w0[q] = wv[j][0][q];
+        w1[q] = wv[j][1][q];
+      }
+    }
+    uint32_t q0[4], q1[4];
+    decode_words<kBitsX2, kCodebook>(L, w0, q0);
+    decode_words<kBitsX2, kCodebook>(L, w1, q1);
+    // the activations are complete once every wavefront is past here (the
+    // first decode overlaps the wait).  LDS stream: a bare s_barrier after
+    // this wavefront's LDS writes; __syncthreads would also wait for every
+    // trellis load in flight.
+    if (j == 0) {
+      if constexpr (kLds) {
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      } else {
+        __syncthreads();
+      }
+    }
+    const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
+    const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
+    // only the lanes of used B columns read (LDS bandwidth): the others keep
+    // a stale operand, whose MFMA columns are never looked at
+    if (m < kCols) {
+      asm volatile("" ::: "memory");
+      bop = bops[j * 4 * kCols];
+    }
+    const f32x4_t zero = {};
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), bop,
+                                                  (j & 3) == 0 ? zero : acc1, 0, 0, 0);
+    acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), bop,
+                                                  (j & 3) == 0 ? zero : acc2, 0, 0, 0);
+    if ((j & 3) == 3) {
+      const int e = block_exp[j >> 2][r_own];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        tot1[i] += ldexpf(acc1[i] + vq::xor_lanes<1>(acc1[i], lane), -e);
+        tot2[i] += ldexpf(acc2[i] + vq::xor_lanes<1>(acc2[i], lane), -e);
+      }
+    }
+    // LDS stream: the slot's last step was read (its reads returned during
+    // the decode): refill it with load i + kRingLoads
+    if constexpr (kLds) {
+      if (j % kP == kP - 1 && j / kP + kRingLoads < kLoads) {
+        wait_lgkmcnt0();
+        load_lds(j / kP + kRingLoads);
       }
     }
   }
@@ -437,16 +604,19 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   //    both MFMAs.  Agent-scope stores are written through to the
   //    device-coherent level, so the fused finish (on any XCD) reads them
   //    without a cache writeback of this workgroup.
-  float* dst = a.partial + int64_t(blockIdx.y) * a.rows * a.np + 32 * (4 * int64_t(blockIdx.x) + wave);
+  //    Lane (g, 2r)'s four rows 4g..4g+3 are columns 4 (g & 1) + 16 (g >> 1)
+  //    + 0..3 of this wavefront's 32 (tot1) and the same + 8 (tot2): two
+  //    16-byte stores, whole runs rather than scattered words.
+  //    The buffer starts at this workgroup's 128 columns of split blockIdx.y
+  //    and ends with row a.rows - 1 of them.
+  float* dst = a.partial + int64_t(blockIdx.y) * a.rows * a.np + 128 * int64_t(blockIdx.x);
+  const __amdgpu_buffer_rsrc_t part_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(dst, 0, int(4 * ((a.rows - 1) * a.np + 128)), 0x00020000);
   if (m < kCols && (m & 1) == 0 && (m >> 1) < a.rows) {
-    const int r = m >> 1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * g + i;
-      const int col = (row & 7) + 16 * (row >> 3);
-      __hip_atomic_store(dst + int64_t(r) * a.np + col, tot1[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(dst + int64_t(r) * a.np + col + 8, tot2[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    const int col = 32 * wave + 4 * (g & 1) + 16 * (g >> 1);
+    const int offset = 4 * (int((m >> 1) * a.np) + col);
+    store_agent_x4(part_rsrc, offset, f32x4_t{tot1[0], tot1[1], tot1[2], tot1[3]});
+    store_agent_x4(part_rsrc, offset + 32, f32x4_t{tot2[0], tot2[1], tot2[2], tot2[3]});
   }
 
   // f. fused finish: the last workgroup of this 128-column block to arrive
@@ -488,8 +658,9 @@ __global__ __launch_bounds__(kThreads) void gemv_output(const float* __restrict_
 // ---- dispatch ----------------------------------------------------------------
 
 template <int kBitsX2, int kCodebook>
-int launch_format(bool aligned, const GemvArgs* gemv, int gemv_blocks, dim3 grid, size_t lds, hipStream_t stream,
-                  const uint8_t* trellis, int64_t tiles_k, int64_t tiles_n, uint16_t* decoded) {
+int launch_format(bool aligned, int load, const GemvArgs* gemv, int gemv_blocks, dim3 grid, size_t lds,
+                  hipStream_t stream, const uint8_t* trellis, int64_t tiles_k, int64_t tiles_n,
+                  uint16_t* decoded) {
   if (gemv) {
 #define VQ_GEMV(A, NR, NB)                                                                    \
   hipLaunchKernelGGL((gemv_kernel<kBitsX2, kCodebook, A, NR, NB>), grid, dim3(kThreads), 0, stream, *gemv)
@@ -497,11 +668,15 @@ int launch_format(bool aligned, const GemvArgs* gemv, int gemv_blocks, dim3 grid
   if (r <= 1) VQ_GEMV(A, 1, NB); else if (r <= 2) VQ_GEMV(A, 2, NB);        \
   else if (r <= 4) VQ_GEMV(A, 4, NB); else VQ_GEMV(A, 8, NB);
     const int r = gemv->rows;
-    const bool one = gemv_blocks == 1;
-    if (aligned) {
-      if (one) { VQ_GEMV_ROWS(true, 1) } else { VQ_GEMV_ROWS(true, 4) }
+    if (load == kLoadLds) {
+      if (gemv_blocks == 1) { VQ_GEMV_ROWS(kLoadLds, 1) }
+      else if (gemv_blocks == 2) { VQ_GEMV_ROWS(kLoadLds, 2) }
+      else if (gemv_blocks == 4) { VQ_GEMV_ROWS(kLoadLds, 4) }
+      else { VQ_GEMV_ROWS(kLoadLds, 8) }
+    } else if (load == kLoadDword) {
+      VQ_GEMV_ROWS(kLoadDword, 1)
     } else {
-      if (one) { VQ_GEMV_ROWS(false, 1) } else { VQ_GEMV_ROWS(false, 4) }
+      VQ_GEMV_ROWS(kLoadHalf, 1)
     }
 #undef VQ_GEMV_ROWS
 #undef VQ_GEMV
@@ -519,12 +694,13 @@ int launch_format(bool aligned, const GemvArgs* gemv, int gemv_blocks, dim3 grid
   return vq::check_launch("exl3 decode_kernel");
 }
 
-int dispatch(int64_t bits_x2, int64_t codebook, bool aligned, const GemvArgs* gemv, int gemv_blocks,
-             dim3 grid, size_t lds, hipStream_t stream, const uint8_t* trellis, int64_t tiles_k,
-             int64_t tiles_n, uint16_t* decoded) {
+int dispatch(int64_t bits_x2, int64_t codebook, bool aligned, int load, const GemvArgs* gemv,
+             int gemv_blocks, dim3 grid, size_t lds, hipStream_t stream, const uint8_t* trellis,
+             int64_t tiles_k, int64_t tiles_n, uint16_t* decoded) {
 #define VQ_CASE(B, C)                                                                   \
   if (bits_x2 == B && codebook == C)                                                    \
-    return launch_format<B, C>(aligned, gemv, gemv_blocks, grid, lds, stream, trellis, tiles_k, tiles_n, decoded);
+    return launch_format<B, C>(aligned, load, gemv, gemv_blocks, grid, lds, stream, trellis, tiles_k, \
+                               tiles_n, decoded);
   VQ_EXL3_FORMATS(VQ_CASE)
 #undef VQ_CASE
   return vq::fail("Unsupported EXL3 rate/codebook combination");
@@ -571,12 +747,19 @@ int counter_bank(hipStream_t stream) {
 // Most K splits the small-M kernel uses: one per 128-input block.
 int64_t gemv_splits(int64_t padded_in) { return padded_in / 128; }
 
-// 128-input blocks per workgroup: 1 while the fused finish stays short
-// (rows * splits <= 32) and the grid stays under ~4096 workgroups, else 4
-// (longer trellis streams per wavefront, fewer partial sums).
+// 128-input blocks per workgroup, always a divisor of padded_in / 128: 1
+// while the fused finish stays short (rows * splits <= 32) and the grid stays
+// under ~4096 workgroups, else the largest of 4, 2 that divides (longer
+// trellis streams per wavefront, fewer partial sums).  A forced value that
+// does not divide falls back to the automatic choice.
+std::atomic<int> g_blocks_override{0};
+
 int gemv_blocks(int64_t rows, int64_t padded_in, int64_t padded_out) {
   const int64_t k_blocks = padded_in / 128;
-  return rows * k_blocks <= 32 && (padded_out / 128) * k_blocks <= 4096 ? 1 : 4;
+  const int forced = g_blocks_override.load();
+  if (forced > 0 && k_blocks % forced == 0) return forced;
+  if (rows * k_blocks <= 32 && (padded_out / 128) * k_blocks <= 4096) return 1;
+  return k_blocks % 4 == 0 ? 4 : (k_blocks % 2 == 0 ? 2 : 1);
 }
 
 // Finish of the small-M path: -1 automatic (fused while a counter bank is
@@ -611,7 +794,7 @@ extern "C" int exl3_decode(const void* trellis, int64_t tiles_k, int64_t tiles_n
     return vq::fail("Unsupported EXL3 rate/codebook combination");
   }
   const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
-  return exl3::dispatch(bits_x2, codebook, aligned, nullptr, 0, dim3(), 0,
+  return exl3::dispatch(bits_x2, codebook, aligned, 0, nullptr, 0, dim3(), 0,
                         static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(trellis),
                         tiles_k, tiles_n, static_cast<uint16_t*>(out));
 }
@@ -676,12 +859,21 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
                                 static_cast<const uint16_t*>(svh), int(bits_x2), int(codebook),
                                 logical_in, logical_out, out, out_dtype, workspace, s);
   }
-  const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
-  const int steps_total = int(padded_in / 32);
-  const int blocks = exl3::gemv_blocks(rows < exl3::kMaxGemvRows ? rows : exl3::kMaxGemvRows,
-                                       padded_in, padded_out);
-  const int64_t splits = (padded_in / 128 + blocks - 1) / blocks;
+  // trellis loads: LDS stream from a 16-byte aligned base, else the dword or
+  // halfword path (one 128-input block per workgroup)
+  const uintptr_t base = reinterpret_cast<uintptr_t>(trellis);
+  const int load = (base & 15) == 0 ? exl3::kLoadLds : ((base & 3) == 0 ? exl3::kLoadDword : exl3::kLoadHalf);
+  const int blocks = load == exl3::kLoadLds
+                         ? exl3::gemv_blocks(rows < exl3::kMaxGemvRows ? rows : exl3::kMaxGemvRows,
+                                             padded_in, padded_out)
+                         : 1;
+  const int64_t splits = padded_in / 128 / blocks;
   if (splits > 65535) return fail("EXL3 linear K is too large");
+  // 32-bit buffer offsets: a workgroup's trellis rows and the partial sums
+  // of one split
+  if (8 * blocks * tiles_n * 16 * bits_x2 > INT_MAX || 4 * exl3::kMaxGemvRows * padded_out > INT_MAX) {
+    return fail("EXL3 linear N is too large for the small-M kernel");
+  }
   float* partial = workspace;
   const int64_t col_blocks = padded_out / 128;
   const int mode = exl3::g_finish_mode.load();
@@ -703,10 +895,10 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
     a.x_dtype = x_dtype;
     a.out_dtype = out_dtype;
     a.rows = chunk;
-    a.steps_total = steps_total;
     a.splits = int(splits);
     const dim3 grid{unsigned(col_blocks), unsigned(splits), 1u};
-    if (int rc = exl3::dispatch(bits_x2, codebook, aligned, &a, blocks, grid, 0, s, nullptr, 0, 0, nullptr)) {
+    if (int rc = exl3::dispatch(bits_x2, codebook, load != exl3::kLoadHalf, load, &a, blocks, grid, 0, s,
+                                nullptr, 0, 0, nullptr)) {
       return rc;
     }
     if (bank < 0) {
@@ -718,6 +910,14 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
     }
   }
   return kOk;
+}
+
+extern "C" int exl3_set_gemv_blocks(int blocks) {
+  if (blocks != 0 && blocks != 1 && blocks != 2 && blocks != 4 && blocks != 8) {
+    return vq::fail("EXL3 GEMV blocks per workgroup must be 0 (automatic), 1, 2, 4 or 8");
+  }
+  exl3::g_blocks_override.store(blocks);
+  return vq::kOk;
 }
 
 extern "C" int exl3_set_gemv_finish(int mode) {

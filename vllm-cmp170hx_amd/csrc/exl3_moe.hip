@@ -177,8 +177,7 @@ __device__ __forceinline__ int64_t b_order(int64_t k) {
 __device__ __forceinline__ void store_block(_Float16* dst, int64_t kp, int64_t block, float v0,
                                             float v1, int* exp_slot, int lane) {
   float mx = fmaxf(fabsf(v0), fabsf(v1));
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+  mx = vq::wave_max(mx, lane);
   const int e = scale_exponent(__builtin_bit_cast(uint32_t, mx));
   if (lane == 0) *exp_slot = e;
   const float t0 = ldexpf(v0, e);
@@ -451,8 +450,8 @@ __global__ __launch_bounds__(256) void moe_gemv(Routing routing, int projection,
           const int e = bexp[buf][r_own];
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            tot1[k] += ldexpf(acc1[k] + __shfl_xor(acc1[k], 1), -e);
-            tot2[k] += ldexpf(acc2[k] + __shfl_xor(acc2[k], 1), -e);
+            tot1[k] += ldexpf(acc1[k] + vq::xor_lanes<1>(acc1[k], lane), -e);
+            tot2[k] += ldexpf(acc2[k] + vq::xor_lanes<1>(acc2[k], lane), -e);
           }
           if (kb + 1 < kblocks) {
             *reinterpret_cast<u32x4_t*>(&bop[buf ^ 1][st_step][st_g][st_col][0]) = sv;
