@@ -145,6 +145,16 @@ int exl3_set_gemv_finish(int mode);
 int exl3_set_gemv_blocks(int blocks);
 
 /*
+ * Test and tuning switch, process-wide: groups of 4 wavefronts per
+ * workgroup of the small-M kernel (0 = automatic, 1 or 4).  A group count of
+ * 4 applies when the input blocks divide into whole 4 * blocks ranges (else
+ * 1 is used).  Changes the FP32 summation grouping, not the weights.  No
+ * counterpart in the reference (its nearest is set_gemm_shape_override,
+ * csrc/exl3/gemm.cu:400-409).
+ */
+int exl3_set_gemv_groups(int groups);
+
+/*
  * Decodes every tile of a trellis into its exact FP16 weights,
  * out[k][n] (k < 16 * tiles_k, n < 16 * tiles_n, row-major, FP16 bits).
  * The inspection form of the decode exl3_linear_out fuses; it has no

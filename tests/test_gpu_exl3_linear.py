@@ -226,6 +226,54 @@ def test_linear_fused_and_separate_finish_agree(ops, device, shape, rows):
         _assert_fp32_close(_out_np(results[0]), want, "finish modes")
 
 
+@pytest.mark.parametrize("blocks,groups", [(1, 1), (2, 1), (4, 1), (8, 1), (1, 4), (2, 4), (4, 4)])
+@pytest.mark.parametrize("bits_x2,codebook", [(8, 2), (4, 1), (3, 2), (2, 2), (10, 2), (16, 1)])
+@pytest.mark.parametrize("rows", [1, 3, 8])
+def test_linear_workgroup_shapes_match_oracle(ops, device, blocks, groups, bits_x2, codebook, rows):
+    """Every (blocks per group, groups per workgroup) shape of the small-M
+    kernel, forced through the tuning switches: same bar as the automatic
+    choice (a shape the rate cannot use falls back, and must still agree)."""
+    from vllm_mi355x import _native
+    print(f"linear shape blocks={blocks} groups={groups} bits_x2={bits_x2} rows={rows}", flush=True)
+    rng = np.random.default_rng(100 * blocks + 10 * groups + bits_x2 + rows)
+    trellis, suh, svh = random_matrix(rng, 2048, 384, bits_x2, scales="test")
+    logical_in, logical_out = 2040, 380
+    x, code = random_acts(rng, rows, logical_in, "fp16")
+    lib = _native.load()
+    try:
+        _native.check(lib.exl3_set_gemv_blocks(blocks))
+        _native.check(lib.exl3_set_gemv_groups(groups))
+        got = _run_linear(ops, device, trellis, suh, svh, x, code, bits_x2, codebook, logical_out,
+                          torch.float32)
+    finally:
+        _native.check(lib.exl3_set_gemv_blocks(0))
+        _native.check(lib.exl3_set_gemv_groups(0))
+    want = O.linear_out(x, code, trellis, suh, svh, bits_x2, codebook, logical_out, O.FP32)
+    _assert_fp32_close(_out_np(got), want, f"blocks={blocks} groups={groups} bits_x2={bits_x2}")
+
+
+@pytest.mark.parametrize("offset_bytes", [2, 4, 8])
+@pytest.mark.parametrize("bits_x2,codebook", [(8, 2), (3, 2), (12, 1)])
+def test_linear_unaligned_trellis_matches_oracle(ops, device, offset_bytes, bits_x2, codebook):
+    """Trellis bases that are not 16-byte aligned take the dword (4, 8) or
+    halfword (2) load paths."""
+    print(f"linear unaligned offset={offset_bytes} bits_x2={bits_x2}", flush=True)
+    rng = np.random.default_rng(500 + offset_bytes + bits_x2)
+    trellis, suh, svh = random_matrix(rng, 512, 256, bits_x2, scales="test")
+    x, code = random_acts(rng, 2, 512, "bf16")
+    flat = torch.empty(trellis.size + 8, dtype=torch.int16, device=device)
+    shift = offset_bytes // 2
+    view = flat[shift:shift + trellis.size].view(trellis.shape)
+    view.copy_(_dev(trellis, device))
+    out = torch.empty(2, 256, dtype=torch.float32, device=device)
+    ws = torch.empty(ops.linear_workspace_size(2, 512, 256), dtype=torch.float32, device=device)
+    ops.linear_out(_to_torch_act(x, code, device), view, _dev(suh, device), _dev(svh, device), bits_x2,
+                   codebook, 512, 256, out, ws)
+    torch.cuda.synchronize()
+    want = O.linear_out(x, code, trellis, suh, svh, bits_x2, codebook, 256, O.FP32)
+    _assert_fp32_close(out.cpu().numpy(), want, f"offset={offset_bytes}")
+
+
 @pytest.mark.parametrize("rows", [9, 64, 300, 513])
 @pytest.mark.parametrize("bits_x2,codebook", [(8, 2), (4, 1), (6, 2), (3, 2)])
 def test_prefill_matches_oracle(ops, device, rows, bits_x2, codebook):

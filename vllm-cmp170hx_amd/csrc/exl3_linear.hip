@@ -150,9 +150,12 @@ struct GemvArgs {
 // kCounterBanks banks of kCounterSlots (one slot per 128-column block), one
 // bank per stream, so calls that overlap on different streams never share a
 // slot.
-constexpr int kCounterBanks = 64;
-constexpr int kCounterSlots = 2048;
-__device__ uint32_t g_gemv_counters[kCounterBanks * kCounterSlots];
+constexpr int kCounterBanks = 16;
+constexpr int kCounterSlots = 1024;
+// One counter per 128-byte line: atomics to one line serialize, so column
+// blocks must not share lines.
+constexpr int kCounterStride = 32;
+__device__ uint32_t g_gemv_counters[kCounterBanks * kCounterSlots * kCounterStride];
 
 // Four consecutive partial sums at byte offset `offset` of buffer `r`,
 // written through to the device-coherent level (cache policy sc1, that of an
@@ -177,8 +180,8 @@ __device__ __forceinline__ float load_partial(const float* p) {
 }
 
 // Row r of one 128-column output block (the separate output kernel): lane l
-// sums columns l and l + 64 over the K splits (loads eight at a time in
-// flight), then H128, times svh, rounded to the output dtype.
+// sums columns l and l + 64 over the K splits (32 loads in flight), then
+// H128, times svh, rounded to the output dtype.
 template <bool kCoherent>
 __device__ __forceinline__ void finish_row_block(const float* __restrict__ partial, int splits,
                                                  int rows, int64_t np, int64_t r, int64_t base,
@@ -194,31 +197,24 @@ __device__ __forceinline__ void finish_row_block(const float* __restrict__ parti
   // even splits, then odd splits, each in order, then even + odd: the same
   // additions as the fused finish
   float e0 = 0.0f, e1 = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  int s = 0;
-  for (; s + 8 <= splits; s += 8) {
-    float a0[8], a1[8];
+  for (int s = 0; s < splits; s += 16) {
+    float a0[16], a1[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      a0[u] = load_partial<kCoherent>(p + (s + u) * stride + c0);
-      a1[u] = load_partial<kCoherent>(p + (s + u) * stride + c1);
+    for (int u = 0; u < 16; ++u) {
+      const bool in = s + u < splits;
+      a0[u] = in ? load_partial<kCoherent>(p + int64_t(s + u) * stride + c0) : 0.0f;
+      a1[u] = in ? load_partial<kCoherent>(p + int64_t(s + u) * stride + c1) : 0.0f;
     }
 #pragma unroll
-    for (int u = 0; u < 8; u += 2) {
-      e0 += a0[u];
-      e1 += a1[u];
-      o0 += a0[u + 1];
-      o1 += a1[u + 1];
-    }
-  }
-  for (; s < splits; ++s) {
-    const float x0 = load_partial<kCoherent>(p + s * stride + c0);
-    const float x1 = load_partial<kCoherent>(p + s * stride + c1);
-    if (s & 1) {
-      o0 += x0;
-      o1 += x1;
-    } else {
-      e0 += x0;
-      e1 += x1;
+    for (int u = 0; u < 16; u += 2) {
+      if (s + u < splits) {
+        e0 += a0[u];
+        e1 += a1[u];
+      }
+      if (s + u + 1 < splits) {
+        o0 += a0[u + 1];
+        o1 += a1[u + 1];
+      }
     }
   }
   float v0 = e0 + o0, v1 = e1 + o1;
@@ -227,33 +223,44 @@ __device__ __forceinline__ void finish_row_block(const float* __restrict__ parti
   if (c1 < logical_out) vq::store_act(out, out_dtype, r * logical_out + c1, v1 * vq::f16_to_f32(uint16_t(scale1)));
 }
 
-// Fused finish of one 128-column block by the whole workgroup: thread t
-// sums column t & 127 over the splits of parity t >> 7 (agent-scope loads,
-// eight in flight, split order), the two parity sums are added (even +
-// odd) through LDS, then wavefront w applies H128 and svh to rows w, w + 4.
-__device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int tid) {
+// Fused finish of one 128-column block by the first 256 threads of the
+// workgroup (the others only pass its barrier): thread t sums column t & 127
+// over the splits of parity t >> 7 (agent-scope loads, eight in flight, split
+// order), the two parity sums are added (even + odd) through LDS, then
+// wavefront w applies H128 and svh to rows w, w + 4.
+__device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int tid, int cblk) {
   const int col = tid & 127;
   const int part = tid >> 7;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t base = 128 * int64_t(blockIdx.x);
-  const int64_t stride = int64_t(a.rows) * a.np;
-  for (int r = 0; r < a.rows; ++r) {
-    const float* p = a.partial + int64_t(r) * a.np + base + col;
+  const int64_t base = 128 * int64_t(cblk);
+  // buffer over this column block's partials of every split (the split in
+  // the scalar offset): one VGPR per load in flight
+  const int stride_bytes = 4 * a.rows * int(a.np);
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      a.partial + base, 0, (a.splits - 1) * stride_bytes + 4 * ((a.rows - 1) * int(a.np) + 128), 0x00020000);
+  for (int r = 0; r < a.rows && tid < 256; ++r) {
+    const int voff = 4 * (r * int(a.np) + col);
     float v = 0.0f;
-    int s = part;
-    for (; s + 14 < a.splits; s += 16) {
-      float t[8];
+    // 16 loads in flight (32 splits) per round, split order
+    for (int s = part; s < a.splits; s += 32) {
+      float t[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) t[u] = load_partial<true>(p + (s + 2 * u) * stride);
+      for (int u = 0; u < 16; ++u) {
+        t[u] = s + 2 * u < a.splits
+                   ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                   rsrc, voff, (s + 2 * u) * stride_bytes, kCachePolicySc1))
+                   : 0.0f;
+      }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v += t[u];
+      for (int u = 0; u < 16; ++u) {
+        if (s + 2 * u < a.splits) v += t[u];
+      }
     }
-    for (; s < a.splits; s += 2) v += load_partial<true>(p + s * stride);
     red[(part * a.rows + r) * 128 + col] = v;
   }
   __syncthreads();
-  for (int r = wave; r < a.rows; r += 4) {
+  for (int r = wave; r < a.rows && wave < 4; r += 4) {
     float v0 = red[r * 128 + lane] + red[(a.rows + r) * 128 + lane];
     float v1 = red[r * 128 + lane + 64] + red[(a.rows + r) * 128 + lane + 64];
     vq::h128_wave(v0, v1, lane);
@@ -283,17 +290,23 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// One workgroup = 4 wavefronts = 128 output columns (one H128 block) x
-// kBlocks 128-input blocks (4 steps of 32 inputs each; the host picks kBlocks
-// dividing the input blocks, so every workgroup's range is whole).  Wavefront
-// w owns the column pair 4 * blockIdx.x + w (two tile columns, 32 outputs)
-// over the range and streams its trellis chunks (kLoad: see Gemv).
+// One workgroup = kGroups groups of 4 wavefronts = 128 output columns (one
+// H128 block) x kGroups * kBlocks 128-input blocks.  Group q takes the
+// kBlocks blocks (4 steps of 32 inputs each) from q * kBlocks on; the host
+// picks kGroups * kBlocks dividing the input blocks, so every workgroup's
+// range is whole.  Wavefront w of a group owns the column pair
+// 4 * blockIdx.x + w (two tile columns, 32 outputs) over the group's range
+// and streams its trellis chunks (kLoad: see Gemv).  The groups' sums meet in
+// LDS (in group order), so a workgroup writes one partial sum per column.
+//
+// The grid is (column block, K split): consecutive workgroups read adjacent
+// kilobytes of the same tile rows (DRAM page locality).
 //
 // kRows (1, 2, 4 or 8) is the row count the kernel is built for; a call with
 // fewer rows (a.rows) computes its last row in the padding rows, which are
 // never stored.
-template <int kBitsX2, int kCodebook, int kLoad, int kRows, int kBlocks>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+template <int kBitsX2, int kCodebook, int kLoad, int kRows, int kBlocks, int kGroups>
+__global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
   using G = Gemv<kBitsX2>;
   using R = Ring<kBitsX2>;
   constexpr bool kLds = kLoad == kLoadLds;
@@ -312,14 +325,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   // Rotated loading order of the 4-bit chunk (dword loads, see below).
   constexpr bool kRotate = kBitsX2 == 8 && !kLds;
   static_assert(kSteps % kP == 0, "whole loads per range");
-  // activations in B-operand order.  Reused by the fused finish for its row
-  // sums.
-  __shared__ __attribute__((aligned(16))) _Float16 act[kActHalves > 2 * 128 * kRows * 2 ? kActHalves : 2 * 128 * kRows * 2];
-  __shared__ int block_exp[kBlocks][kRows];
+  static_assert(kGroups == 1 || (kLds && kRingLoads >= 2), "groups meet in two ring slots");
+  // activations in B-operand order, per group.  Reused by the fused finish
+  // for its row sums.
+  constexpr int kActAll = kGroups * kActHalves;
+  __shared__ __attribute__((aligned(16))) _Float16 act[kActAll > 2 * 128 * kRows * 2 ? kActAll : 2 * 128 * kRows * 2];
+  __shared__ int block_exp[kGroups][kBlocks][kRows];
   // LDS stream: kRingLoads slots of 1 KB (kP steps) per wavefront, one
   // array per slot: the compiler's wait for an LDS-DMA load before a read
   // of its data then names that load, not every load in flight.
-  constexpr int kSlotWords = kLds ? 4 * 256 : 4;
+  constexpr int kSlotWords = kLds ? 4 * kGroups * 256 : 4;
   __shared__ __attribute__((aligned(16))) uint32_t ring0[kSlotWords];
   __shared__ __attribute__((aligned(16))) uint32_t ring1[kRingLoads > 1 ? kSlotWords : 4];
   __shared__ __attribute__((aligned(16))) uint32_t ring2[kRingLoads > 2 ? kSlotWords : 4];
@@ -328,11 +343,15 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // in the workgroup
+  const int grp = wave >> 2;
+  const int wc = wave & 3;                                       // column pair in the block
   const int g = lane >> 4;
   const int m = lane & 15;
   const int L = 4 * (m & 7) + g;
-  const int block0 = blockIdx.y * kBlocks;
+  const int cblk = blockIdx.x;
+  const int split = blockIdx.y;
+  const int block0 = (split * kGroups + grp) * kBlocks;
   const int64_t k0 = int64_t(block0) * 128;
 
   // a. activation loads first (they must not queue behind the trellis).
@@ -345,7 +364,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   uint32_t xv[kFormTasks][2], sv[kFormTasks][2];
 #pragma unroll
   for (int f = 0; f < kFormTasks; ++f) {
-    const int t = wave + 4 * f;
+    const int t = wc + 4 * f;
     const int b = min(t / kRows, kBlocks - 1);
     const int64_t row = int64_t(min(t % kRows, a.rows - 1)) * a.logical_in;
     const int64_t k_0 = k0 + 128 * b + lane;
@@ -359,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   }
 #pragma unroll
   for (int f = 0; f < kFormTasks; ++f) {
-    const int b = min((wave + 4 * f) / kRows, kBlocks - 1);
+    const int b = min((wc + 4 * f) / kRows, kBlocks - 1);
     const int64_t k_0 = k0 + 128 * b + lane;
     if (!(k_0 < a.logical_in)) { sv[f][0] = 0u; xv[f][0] = 0u; }
     if (!(k_0 + 64 < a.logical_in)) { sv[f][1] = 0u; xv[f][1] = 0u; }
@@ -370,7 +389,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   int off[G::kWords];
   lane_word_offsets<kBitsX2>(L, off);
   const int row_bytes = int(a.tiles_n) * R::kTileBytes;
-  const uint8_t* chunk = a.trellis + 2 * (4 * int64_t(blockIdx.x) + wave) * R::kTileBytes +
+  const uint8_t* chunk = a.trellis + 2 * (4 * int64_t(cblk) + wc) * R::kTileBytes +
                          8 * int64_t(block0) * row_bytes;
   const __amdgpu_buffer_rsrc_t trellis_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(chunk), 0, (8 * kBlocks - 1) * row_bytes + 2 * R::kTileBytes, 0x00020000);
@@ -466,9 +485,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     };
     const int h0 = slot_of(lane);
     const int h1 = slot_of(lane + 64);
+    _Float16* gact = act + grp * kActHalves;
 #pragma unroll
     for (int f = 0; f < kFormTasks; ++f) {
-      const int t = wave + 4 * f;
+      const int t = wc + 4 * f;
       const int b = t / kRows;
       const int r = t % kRows;
       if (t < kTasks) {
@@ -477,15 +497,15 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         vq::h128_wave(v0, v1, lane);
         const float mx = vq::wave_max(fmaxf(fabsf(v0), fabsf(v1)), lane);
         const int e = scale_exponent(__builtin_bit_cast(uint32_t, mx));
-        if (lane == 0) block_exp[b][r] = e;
+        if (lane == 0) block_exp[grp][b][r] = e;
         const float t0 = ldexpf(v0, e);
         const float t1 = ldexpf(v1, e);
         const _Float16 hi0 = _Float16(t0), hi1 = _Float16(t1);
         const int base = b * 4 * 4 * kCols * 8 + (2 * r) * 8;
-        act[base + h0] = hi0;
-        act[base + h0 + 8] = _Float16(t0 - float(hi0));
-        act[base + h1] = hi1;
-        act[base + h1 + 8] = _Float16(t1 - float(hi1));
+        gact[base + h0] = hi0;
+        gact[base + h0 + 8] = _Float16(t0 - float(hi0));
+        gact[base + h1] = hi1;
+        gact[base + h1 + 8] = _Float16(t1 - float(hi1));
       }
     }
   }
@@ -508,7 +528,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
       }
     }
   };
-  const half8_t* bops = reinterpret_cast<const half8_t*>(act) + g * kCols + (m % kCols);
+  const half8_t* bops = reinterpret_cast<const half8_t*>(act + grp * kActHalves) + g * kCols + (m % kCols);
   const int r_own = (m >> 1) < kRows ? (m >> 1) : 0;
   f32x4_t acc1 = {}, acc2 = {};
   float tot1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -583,7 +603,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), bop,
                                                   (j & 3) == 0 ? zero : acc2, 0, 0, 0);
     if ((j & 3) == 3) {
-      const int e = block_exp[j >> 2][r_own];
+      const int e = block_exp[grp][j >> 2][r_own];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         tot1[i] += ldexpf(acc1[i] + vq::xor_lanes<1>(acc1[i], lane), -e);
@@ -607,13 +627,38 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   //    Lane (g, 2r)'s four rows 4g..4g+3 are columns 4 (g & 1) + 16 (g >> 1)
   //    + 0..3 of this wavefront's 32 (tot1) and the same + 8 (tot2): two
   //    16-byte stores, whole runs rather than scattered words.
-  //    The buffer starts at this workgroup's 128 columns of split blockIdx.y
+  //    The buffer starts at this workgroup's 128 columns of its split
   //    and ends with row a.rows - 1 of them.
-  float* dst = a.partial + int64_t(blockIdx.y) * a.rows * a.np + 128 * int64_t(blockIdx.x);
+  //    Groups 1.. first hand their sums to group 0 through this wavefront's
+  //    own regions of ring slots 0 and 1 (its loads have all landed and been
+  //    read); group 0 adds them in group order.
+  if constexpr (kGroups > 1) {
+    if (grp > 0) {
+      wait_lgkmcnt0();
+      *reinterpret_cast<f32x4_t*>(ring0 + wave * 256 + 4 * lane) = f32x4_t{tot1[0], tot1[1], tot1[2], tot1[3]};
+      *reinterpret_cast<f32x4_t*>(ring1 + wave * 256 + 4 * lane) = f32x4_t{tot2[0], tot2[1], tot2[2], tot2[3]};
+    }
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (grp == 0) {
+#pragma unroll
+      for (int q = 1; q < kGroups; ++q) {
+        const f32x4_t o1 = *reinterpret_cast<const f32x4_t*>(ring0 + (4 * q + wc) * 256 + 4 * lane);
+        const f32x4_t o2 = *reinterpret_cast<const f32x4_t*>(ring1 + (4 * q + wc) * 256 + 4 * lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          tot1[i] += o1[i];
+          tot2[i] += o2[i];
+        }
+      }
+    }
+  }
+  float* dst = a.partial + int64_t(split) * a.rows * a.np + 128 * int64_t(cblk);
   const __amdgpu_buffer_rsrc_t part_rsrc =
       __builtin_amdgcn_make_buffer_rsrc(dst, 0, int(4 * ((a.rows - 1) * a.np + 128)), 0x00020000);
-  if (m < kCols && (m & 1) == 0 && (m >> 1) < a.rows) {
-    const int col = 32 * wave + 4 * (g & 1) + 16 * (g >> 1);
+  if (grp == 0 && m < kCols && (m & 1) == 0 && (m >> 1) < a.rows) {
+    const int col = 32 * wc + 4 * (g & 1) + 16 * (g >> 1);
     const int offset = 4 * (int((m >> 1) * a.np) + col);
     store_agent_x4(part_rsrc, offset, f32x4_t{tot1[0], tot1[1], tot1[2], tot1[3]});
     store_agent_x4(part_rsrc, offset + 32, f32x4_t{tot2[0], tot2[1], tot2[2], tot2[3]});
@@ -622,7 +667,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   // f. fused finish: the last workgroup of this 128-column block to arrive
   //    sums every split's partials and writes the outputs.
   if (a.counter_bank >= 0) {
-    uint32_t* counter = g_gemv_counters + a.counter_bank * kCounterSlots + blockIdx.x;
+    uint32_t* counter = g_gemv_counters + (a.counter_bank * kCounterSlots + cblk) * kCounterStride;
     __shared__ int is_last;
     // every store of this wavefront has completed (vmcnt counts stores on
     // gfx9), then every wavefront of the workgroup is past that point
@@ -635,7 +680,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
     if (is_last) {
-      finish_block(a, reinterpret_cast<float*>(act), tid);
+      finish_block(a, reinterpret_cast<float*>(act), tid, cblk);
       if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -657,30 +702,51 @@ __global__ __launch_bounds__(kThreads) void gemv_output(const float* __restrict_
 
 // ---- dispatch ----------------------------------------------------------------
 
+// Steps (two tile rows) per LDS-stream load, as Gemv<kBitsX2>::kStepsPerLoad.
+inline int steps_per_load(int64_t bits_x2) { return bits_x2 <= 4 ? 4 : (bits_x2 <= 8 ? 2 : 1); }
+
+// A workgroup of kGroups groups needs two loads per group range (the groups
+// meet in two ring slots).
+inline bool can_group(int64_t bits_x2, int blocks) { return steps_per_load(bits_x2) < 4 * blocks; }
+
+template <int kBitsX2, int kCodebook, int kLoad, int kBlocks, int kGroups>
+int launch_gemv(const GemvArgs& a, dim3 grid, hipStream_t stream) {
+  if constexpr (kGroups > 1 && !(Gemv<kBitsX2>::kStepsPerLoad < 4 * kBlocks)) {
+    return vq::fail("EXL3 GEMV: grouped workgroups need two loads per group");
+  } else {
+    const dim3 block(kThreads * kGroups);
+    if (a.rows <= 1) {
+      hipLaunchKernelGGL((gemv_kernel<kBitsX2, kCodebook, kLoad, 1, kBlocks, kGroups>), grid, block, 0, stream, a);
+    } else if (a.rows <= 2) {
+      hipLaunchKernelGGL((gemv_kernel<kBitsX2, kCodebook, kLoad, 2, kBlocks, kGroups>), grid, block, 0, stream, a);
+    } else if (a.rows <= 4) {
+      hipLaunchKernelGGL((gemv_kernel<kBitsX2, kCodebook, kLoad, 4, kBlocks, kGroups>), grid, block, 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((gemv_kernel<kBitsX2, kCodebook, kLoad, 8, kBlocks, kGroups>), grid, block, 0, stream, a);
+    }
+    return vq::check_launch("exl3 gemv_kernel");
+  }
+}
+
 template <int kBitsX2, int kCodebook>
-int launch_format(bool aligned, int load, const GemvArgs* gemv, int gemv_blocks, dim3 grid, size_t lds,
-                  hipStream_t stream, const uint8_t* trellis, int64_t tiles_k, int64_t tiles_n,
+int launch_format(bool aligned, int load, const GemvArgs* gemv, int gemv_blocks, int gemv_groups, dim3 grid,
+                  size_t lds, hipStream_t stream, const uint8_t* trellis, int64_t tiles_k, int64_t tiles_n,
                   uint16_t* decoded) {
   if (gemv) {
-#define VQ_GEMV(A, NR, NB)                                                                    \
-  hipLaunchKernelGGL((gemv_kernel<kBitsX2, kCodebook, A, NR, NB>), grid, dim3(kThreads), 0, stream, *gemv)
-#define VQ_GEMV_ROWS(A, NB)                                                  \
-  if (r <= 1) VQ_GEMV(A, 1, NB); else if (r <= 2) VQ_GEMV(A, 2, NB);        \
-  else if (r <= 4) VQ_GEMV(A, 4, NB); else VQ_GEMV(A, 8, NB);
-    const int r = gemv->rows;
-    if (load == kLoadLds) {
-      if (gemv_blocks == 1) { VQ_GEMV_ROWS(kLoadLds, 1) }
-      else if (gemv_blocks == 2) { VQ_GEMV_ROWS(kLoadLds, 2) }
-      else if (gemv_blocks == 4) { VQ_GEMV_ROWS(kLoadLds, 4) }
-      else { VQ_GEMV_ROWS(kLoadLds, 8) }
-    } else if (load == kLoadDword) {
-      VQ_GEMV_ROWS(kLoadDword, 1)
-    } else {
-      VQ_GEMV_ROWS(kLoadHalf, 1)
+    const GemvArgs& a = *gemv;
+    if (load == kLoadLds && gemv_groups == 4) {
+      if (gemv_blocks == 1) return launch_gemv<kBitsX2, kCodebook, kLoadLds, 1, 4>(a, grid, stream);
+      if (gemv_blocks == 2) return launch_gemv<kBitsX2, kCodebook, kLoadLds, 2, 4>(a, grid, stream);
+      return launch_gemv<kBitsX2, kCodebook, kLoadLds, 4, 4>(a, grid, stream);
     }
-#undef VQ_GEMV_ROWS
-#undef VQ_GEMV
-    return vq::check_launch("exl3 gemv_kernel");
+    if (load == kLoadLds) {
+      if (gemv_blocks == 1) return launch_gemv<kBitsX2, kCodebook, kLoadLds, 1, 1>(a, grid, stream);
+      if (gemv_blocks == 2) return launch_gemv<kBitsX2, kCodebook, kLoadLds, 2, 1>(a, grid, stream);
+      if (gemv_blocks == 4) return launch_gemv<kBitsX2, kCodebook, kLoadLds, 4, 1>(a, grid, stream);
+      return launch_gemv<kBitsX2, kCodebook, kLoadLds, 8, 1>(a, grid, stream);
+    }
+    if (load == kLoadDword) return launch_gemv<kBitsX2, kCodebook, kLoadDword, 1, 1>(a, grid, stream);
+    return launch_gemv<kBitsX2, kCodebook, kLoadHalf, 1, 1>(a, grid, stream);
   }
   const int64_t threads = tiles_k * tiles_n * 32;
   const dim3 dgrid(unsigned((threads + kThreads - 1) / kThreads));
@@ -695,12 +761,12 @@ int launch_format(bool aligned, int load, const GemvArgs* gemv, int gemv_blocks,
 }
 
 int dispatch(int64_t bits_x2, int64_t codebook, bool aligned, int load, const GemvArgs* gemv,
-             int gemv_blocks, dim3 grid, size_t lds, hipStream_t stream, const uint8_t* trellis,
-             int64_t tiles_k, int64_t tiles_n, uint16_t* decoded) {
+             int gemv_blocks, int gemv_groups, dim3 grid, size_t lds, hipStream_t stream,
+             const uint8_t* trellis, int64_t tiles_k, int64_t tiles_n, uint16_t* decoded) {
 #define VQ_CASE(B, C)                                                                   \
   if (bits_x2 == B && codebook == C)                                                    \
-    return launch_format<B, C>(aligned, load, gemv, gemv_blocks, grid, lds, stream, trellis, tiles_k, \
-                               tiles_n, decoded);
+    return launch_format<B, C>(aligned, load, gemv, gemv_blocks, gemv_groups, grid, lds, stream, trellis, \
+                               tiles_k, tiles_n, decoded);
   VQ_EXL3_FORMATS(VQ_CASE)
 #undef VQ_CASE
   return vq::fail("Unsupported EXL3 rate/codebook combination");
@@ -747,19 +813,40 @@ int counter_bank(hipStream_t stream) {
 // Most K splits the small-M kernel uses: one per 128-input block.
 int64_t gemv_splits(int64_t padded_in) { return padded_in / 128; }
 
-// 128-input blocks per workgroup, always a divisor of padded_in / 128: 1
-// while the fused finish stays short (rows * splits <= 32) and the grid stays
-// under ~4096 workgroups, else the largest of 4, 2 that divides (longer
-// trellis streams per wavefront, fewer partial sums).  A forced value that
-// does not divide falls back to the automatic choice.
+// 128-input blocks per workgroup, always a divisor of padded_in / 128: the
+// fewest (1, 2, 4 or 8) that keep the grid within ~7 wavefronts per SIMD
+// (all resident at once: one round, no second-round start-up) and the K
+// splits within 32 (the fused finish reads every split's partial sums).  A
+// forced value that does not divide falls back to the automatic choice.
 std::atomic<int> g_blocks_override{0};
 
 int gemv_blocks(int64_t rows, int64_t padded_in, int64_t padded_out) {
+  (void)rows;
   const int64_t k_blocks = padded_in / 128;
   const int forced = g_blocks_override.load();
   if (forced > 0 && k_blocks % forced == 0) return forced;
-  if (rows * k_blocks <= 32 && (padded_out / 128) * k_blocks <= 4096) return 1;
-  return k_blocks % 4 == 0 ? 4 : (k_blocks % 2 == 0 ? 2 : 1);
+  const int64_t col_waves = padded_out / 128 * 4;
+  int best = 1;
+  for (int b : {1, 2, 4, 8}) {
+    if (k_blocks % b != 0) continue;
+    best = b;
+    if (col_waves * (k_blocks / b) <= 7168 && k_blocks / b <= 32) break;
+  }
+  return best;
+}
+
+// Groups of 4 wavefronts per workgroup (1 or 4), each on its own kBlocks
+// blocks: 4 when the split covers whole 4 * blocks ranges and the rate
+// allows it (LDS stream only; see can_group), else 1.
+std::atomic<int> g_groups_override{0};
+
+int gemv_groups(int64_t rows, int64_t padded_in, int64_t bits_x2, int blocks) {
+  const int64_t k_blocks = padded_in / 128;
+  const int forced = g_groups_override.load();
+  const bool ok = k_blocks % (4 * blocks) == 0 && can_group(bits_x2, blocks) && blocks <= 4;
+  if (forced == 1) return 1;
+  if (forced == 4) return ok ? 4 : 1;
+  return 1;
 }
 
 // Finish of the small-M path: -1 automatic (fused while a counter bank is
@@ -794,7 +881,7 @@ extern "C" int exl3_decode(const void* trellis, int64_t tiles_k, int64_t tiles_n
     return vq::fail("Unsupported EXL3 rate/codebook combination");
   }
   const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
-  return exl3::dispatch(bits_x2, codebook, aligned, 0, nullptr, 0, dim3(), 0,
+  return exl3::dispatch(bits_x2, codebook, aligned, 0, nullptr, 0, 1, dim3(), 0,
                         static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(trellis),
                         tiles_k, tiles_n, static_cast<uint16_t*>(out));
 }
@@ -863,15 +950,15 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
   // halfword path (one 128-input block per workgroup)
   const uintptr_t base = reinterpret_cast<uintptr_t>(trellis);
   const int load = (base & 15) == 0 ? exl3::kLoadLds : ((base & 3) == 0 ? exl3::kLoadDword : exl3::kLoadHalf);
-  const int blocks = load == exl3::kLoadLds
-                         ? exl3::gemv_blocks(rows < exl3::kMaxGemvRows ? rows : exl3::kMaxGemvRows,
-                                             padded_in, padded_out)
-                         : 1;
-  const int64_t splits = padded_in / 128 / blocks;
+  const int64_t small_rows = rows < exl3::kMaxGemvRows ? rows : exl3::kMaxGemvRows;
+  const int blocks = load == exl3::kLoadLds ? exl3::gemv_blocks(small_rows, padded_in, padded_out) : 1;
+  const int groups = load == exl3::kLoadLds ? exl3::gemv_groups(small_rows, padded_in, bits_x2, blocks) : 1;
+  const int64_t splits = padded_in / 128 / (blocks * groups);
   if (splits > 65535) return fail("EXL3 linear K is too large");
   // 32-bit buffer offsets: a workgroup's trellis rows and the partial sums
   // of one split
-  if (8 * blocks * tiles_n * 16 * bits_x2 > INT_MAX || 4 * exl3::kMaxGemvRows * padded_out > INT_MAX) {
+  if (8 * blocks * tiles_n * 16 * bits_x2 > INT_MAX ||
+      4 * exl3::kMaxGemvRows * padded_out * exl3::gemv_splits(padded_in) > INT_MAX) {
     return fail("EXL3 linear N is too large for the small-M kernel");
   }
   float* partial = workspace;
@@ -897,8 +984,8 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
     a.rows = chunk;
     a.splits = int(splits);
     const dim3 grid{unsigned(col_blocks), unsigned(splits), 1u};
-    if (int rc = exl3::dispatch(bits_x2, codebook, load != exl3::kLoadHalf, load, &a, blocks, grid, 0, s,
-                                nullptr, 0, 0, nullptr)) {
+    if (int rc = exl3::dispatch(bits_x2, codebook, load != exl3::kLoadHalf, load, &a, blocks, groups, grid,
+                                0, s, nullptr, 0, 0, nullptr)) {
       return rc;
     }
     if (bank < 0) {
@@ -917,6 +1004,14 @@ extern "C" int exl3_set_gemv_blocks(int blocks) {
     return vq::fail("EXL3 GEMV blocks per workgroup must be 0 (automatic), 1, 2, 4 or 8");
   }
   exl3::g_blocks_override.store(blocks);
+  return vq::kOk;
+}
+
+extern "C" int exl3_set_gemv_groups(int groups) {
+  if (groups != 0 && groups != 1 && groups != 4) {
+    return vq::fail("EXL3 GEMV groups per workgroup must be 0 (automatic), 1 or 4");
+  }
+  exl3::g_groups_override.store(groups);
   return vq::kOk;
 }
 

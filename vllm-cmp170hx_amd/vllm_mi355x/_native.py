@@ -38,6 +38,7 @@ SIGNATURES = {
     "exl3_decode": (c_int, [c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp]),
     "exl3_set_gemv_finish": (c_int, [c_int]),
     "exl3_set_gemv_blocks": (c_int, [c_int]),
+    "exl3_set_gemv_groups": (c_int, [c_int]),
     "exl3_moe_workspace_size": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64]),
     "exl3_moe_out": (c_int, [
         c_vp, c_int, c_i64, c_i64,            # x, x_dtype, rows, hidden
