@@ -176,6 +176,7 @@ int exl3_decode(const void* trellis, int64_t tiles_k, int64_t tiles_n, int64_t t
 #define VQ_MARLIN_PARTIAL 0 /* FP32 k-split partials part[ks][slot][N] */
 #define VQ_MARLIN_STORE 1   /* out[slot][n] = RN(sum) */
 #define VQ_MARLIN_TOPK 2    /* out[slot][n] = RN(RN(sum) * RN(topk_w[slot])) */
+#define VQ_MARLIN_SWIGLU 3  /* marlin_moe_gemm_direct only: h = SwiGLU(gate, up) */
 
 /*
  * Grouped expert GEMM over aligned blocks: for every block b < ntpp[0] /
@@ -199,6 +200,37 @@ int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stri
                     int64_t K, int64_t N, int64_t block_size, int mode, int64_t ksplit,
                     float* part, int64_t part_numel, void* out, int64_t out_stride,
                     int64_t out_rows, void* stream);
+
+/*
+ * marlin_moe_gemm (same arguments, checks and sums, bitwise) on k-permuted
+ * activations: a's rows hold, in every 32-k step, element 8q + 2s + t = k
+ * 8s + 2q + t (marlin_permute_act); weights stream through LDS and each
+ * lane loads its matrix operand directly, with no staging barrier.  Four
+ * 64-column tiles per workgroup, ksplit 1 for STORE / TOPK / SWIGLU.  Mode
+ * SWIGLU (ksplit 1, N % 256 == 0): N = 2 Nh columns of gate | up, out =
+ * h[slot] (rows of out_stride elements, out_stride % 32 == 0) in the
+ * permuted layout, h = RN(RN(SiLU(min(G, L))) * clamp(U, -L, L)) of the
+ * activation-dtype roundings G, U of the sums (marlin_moe_act's arithmetic).
+ * No counterpart in the reference: the fused path's layout of
+ * decode_gemm_orig / decode_act_orig (csrc/ampere_marlin/decode_orig.cu:
+ * 272-305, 361-390).
+ */
+int marlin_moe_gemm_direct(const void* a_perm, int act_dtype, int64_t a_rows, int64_t a_stride,
+                           const int32_t* w, const void* scales, int64_t experts,
+                           const int32_t* sorted, int64_t sorted_numel, const int32_t* expert_ids,
+                           int64_t expert_ids_numel, const int32_t* ntpp, const float* topk_w,
+                           int64_t top_k, int64_t n_slots, int64_t K, int64_t N,
+                           int64_t block_size, int mode, int64_t ksplit, float limit, float* part,
+                           int64_t part_numel, void* out, int64_t out_stride, int64_t out_rows,
+                           void* stream);
+
+/*
+ * out[r][p(k)] = a[r][k] for r < rows, k < cols (cols % 32 == 0), p the
+ * permutation marlin_moe_gemm_direct reads (inside each 32-k step, k = 8s +
+ * 2q + t goes to 8q + 2s + t).  No counterpart in the reference.
+ */
+int marlin_permute_act(const void* a, int act_dtype, int64_t rows, int64_t cols, int64_t a_stride,
+                       void* out, int64_t out_stride, void* stream);
 
 /*
  * SwiGLU of the w13 partials: G / U = RN(sum over ks in order of

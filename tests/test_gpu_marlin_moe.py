@@ -248,6 +248,87 @@ def test_fused_expert_map(mm, device):
     assert_close(host_bits(out), expected, M.BF16, "expert map")
 
 
+# ---- the direct path (k-permuted activations, LDS weight ring, fused SwiGLU) ----------------
+
+def permuted_k(k):
+    w = k & 31
+    return (k & ~31) + 8 * ((w >> 1) & 3) + 2 * (w >> 3) + (w & 1)
+
+
+def test_permute_act_layout(mm, device):
+    from vllm_mi355x.kernels.marlin_moe import _C
+    rng = np.random.default_rng(21)
+    x = torch.from_numpy(rng.integers(-2 ** 15, 2 ** 15, (7, 96), dtype=np.int64).astype(np.int16))
+    x = x.to(device).view(torch.bfloat16)
+    out = torch.zeros_like(x)
+    _C.permute_act(x, out)
+    torch.cuda.synchronize()
+    perm = np.array([permuted_k(k) for k in range(96)])
+    assert sorted(perm.tolist()) == list(range(96))
+    want = np.zeros((7, 96), np.int16)
+    want[:, perm] = x.view(torch.int16).cpu().numpy()
+    assert np.array_equal(out.view(torch.int16).cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype,limit", [(M.BF16, 10.0), (M.FP16, None), (M.BF16, 0.02)])
+@pytest.mark.parametrize("T,bs", [(1, 8), (5, 16), (33, 32), (40, 8)])
+def test_direct_path_matches_oracle(mm, device, dtype, limit, T, bs):
+    print(f"direct dtype={dtype} limit={limit} T={T} bs={bs}", flush=True)
+    rng = np.random.default_rng(T * 13 + dtype)
+    E, K, N, topk = 8, 256, 128, 4
+    layer = Layer(rng, E, K, N, dtype, device)
+    ids, w = routing(rng, T, E, topk, skew=1.1)
+    x = from_f32(rng.standard_normal((T, K)), dtype)
+    out = mm[0].fused_marlin_moe(dev_act(x, dtype, device), layer.w1, layer.w2, layer.s1, layer.s2,
+                                 dev(w, device), dev(ids, device), clamp_limit=limit,
+                                 block_size=bs, path="direct")
+    torch.cuda.synchronize()
+    expected = M.moe(x, dtype, ids, w, *layer.host, limit=math.inf if limit is None else limit)
+    assert_close(host_bits(out), expected, dtype, f"direct T={T} bs={bs}")
+
+
+@pytest.mark.parametrize("dtype,bs", [(M.FP16, 32), (M.BF16, 16)])
+def test_direct_and_staged_paths_bitwise_at_c4_shape(mm, device, dtype, bs):
+    """128 experts, hidden 2048, intermediate 768, top-8, 256 tokens: the
+    staged path runs four tiles per workgroup here, the same per-tile MFMA
+    sequence as the direct path, so the fused outputs are equal bit for bit
+    (the direct path's fused SwiGLU does marlin_moe_act's arithmetic); and
+    the direct STORE / PARTIAL modes equal the staged ones."""
+    from vllm_mi355x.kernels.marlin_moe import _C
+    print(f"direct vs staged dtype={dtype} bs={bs}", flush=True)
+    rng = np.random.default_rng(22 + bs)
+    E, K, N, topk, T = 128, 2048, 768, 8, 256
+    layer = Layer(rng, E, K, N, dtype, device)
+    ids, w = routing(rng, T, E, topk)
+    x = dev_act(from_f32(rng.standard_normal((T, K)), dtype), dtype, device)
+    args = (x, layer.w1, layer.w2, layer.s1, layer.s2, dev(w, device), dev(ids, device))
+    staged = mm[0].fused_marlin_moe(*args, block_size=bs, ksplit=1, path="staged", clamp_limit=7.0)
+    direct = mm[0].fused_marlin_moe(*args, block_size=bs, path="direct", clamp_limit=7.0)
+    torch.cuda.synchronize()
+    assert torch.equal(staged.view(torch.int16), direct.view(torch.int16))
+    # single GEMMs: w2 shape, STORE and PARTIAL
+    slots = T * topk
+    sorted_ids, expert_ids, ntpp = mm[1].align(dev(ids, device), E, bs)
+    h = dev_act(from_f32(rng.standard_normal((slots, N)), dtype), dtype, device)
+    hp = torch.empty_like(h)
+    _C.permute_act(h, hp)
+    o1 = torch.zeros(slots, K, dtype=h.dtype, device=device)
+    o2 = torch.zeros_like(o1)
+    _C.gemm(h, layer.w2, layer.s2, sorted_ids, expert_ids, ntpp, None, 1, slots, N, K, bs,
+            _C.MODE_STORE, 1, out=o1)
+    _C.gemm_direct(hp, layer.w2, layer.s2, sorted_ids, expert_ids, ntpp, None, 1, slots, N, K, bs,
+                   _C.MODE_STORE, 1, out=o2)
+    p1 = torch.zeros(slots * K, dtype=torch.float32, device=device)
+    p2 = torch.zeros_like(p1)
+    _C.gemm(h, layer.w2, layer.s2, sorted_ids, expert_ids, ntpp, None, 1, slots, N, K, bs,
+            _C.MODE_PARTIAL, 1, part=p1)
+    _C.gemm_direct(hp, layer.w2, layer.s2, sorted_ids, expert_ids, ntpp, None, 1, slots, N, K, bs,
+                   _C.MODE_PARTIAL, 1, part=p2)
+    torch.cuda.synchronize()
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    assert torch.equal(p1, p2)
+
+
 # ---- the reference's operator sequence ----------------------------------------------------
 
 def test_decode_ops_sequence_matches_fused(mm, device):

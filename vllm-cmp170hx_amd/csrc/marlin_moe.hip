@@ -50,7 +50,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kThreads = 256;
 constexpr int kMaxBlock = 64;  // tokens per aligned block (upstream block sizes 8..64)
 
-enum Mode : int { kPartial = 0, kStore = 1, kTopk = 2 };
+enum Mode : int { kPartial = 0, kStore = 1, kTopk = 2, kSwiglu = 3 };
 
 struct GemmArgs {
   const uint16_t* a;      // activations, row r at a + r * a_stride
@@ -66,6 +66,7 @@ struct GemmArgs {
   uint16_t* out;          // kStore / kTopk: row slot at out + slot * out_stride
   int64_t out_stride;
   int top_k, n_slots, K, N, bs, experts, groups_per_split;
+  float limit;            // kSwiglu: SwiGLU clamp (+inf: none)
 };
 
 // Raw buffer resource over [base, base + bytes): 32-bit offsets, and loads
@@ -442,6 +443,251 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
   }
 }
 
+
+// ---- grouped GEMM on k-permuted activations (the fused path) -------------------
+
+// Position, inside its 32-k step, of activation k in the permuted layout the
+// direct GEMM reads: element 8 q + 2 s + t of a step holds k = 8 s + 2 q + t,
+// so lane (q, token) finds its whole B operand (k {2q, 2q+1, 2q+8, 2q+9,
+// 16+2q, 17+2q, 24+2q, 25+2q}, the A operand's order) in 16 contiguous bytes.
+__host__ __device__ __forceinline__ int permuted_k(int k) {
+  const int w = k & 31;
+  return (k & ~31) + 8 * ((w >> 1) & 3) + 2 * (w >> 3) + (w & 1);
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// As marlin_gemm with four 64-column tiles per workgroup (one per
+// wavefront, all of the workgroup's K range), but:
+//  * weights stream through a per-wavefront LDS ring of three 128-k groups
+//    (buffer_load_dwordx4 ... lds: no VGPR staging), two groups ahead;
+//  * each lane loads its B operands straight from k-permuted activations
+//    (one 16-byte load per step and 16-token sub-block, one group ahead), so
+//    there is no activation staging and no workgroup barrier in the loop;
+//  * kSwiglu: wavefronts 0, 1 take gate tiles 2p, 2p + 1 and wavefronts 2, 3
+//    the matching up tiles (N / 128 + 2p ...): the up sums meet the gate sums
+//    in LDS and h = RN(RN(SiLU(min(G, L))) * clamp(U, -L, L)) is written in
+//    the permuted layout (the w2 GEMM's input), G / U the activation-dtype
+//    roundings of the FP32 sums (marlin_act_kernel's arithmetic).
+// The MFMA sequence per tile is marlin_gemm's, so the sums are bitwise the
+// same.
+template <bool kBF16, int kSub, int kMode>
+__global__ __launch_bounds__(kThreads) void marlin_gemm_direct(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) u32x4_t ring0[4 * 4 * 64];
+  __shared__ __attribute__((aligned(16))) u32x4_t ring1[4 * 4 * 64];
+  __shared__ __attribute__((aligned(16))) u32x4_t ring2[4 * 4 * 64];
+  __shared__ int s_slot[kMaxBlock];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4;
+  const int col = lane & 15;
+  int tile;
+  if constexpr (kMode == kSwiglu) {
+    const int p = blockIdx.x;
+    tile = wave < 2 ? 2 * p + wave : (g.N >> 7) + 2 * p + (wave - 2);
+  } else {
+    tile = int(blockIdx.x) * 4 + wave;
+  }
+  const bool tile_ok = tile < (g.N >> 6);
+  const int b = blockIdx.y;
+  const int ks = blockIdx.z;
+  if (int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
+  const int e = g.eids[b];
+  if (e < 0 || e >= g.experts) return;
+  if (tid < kMaxBlock) {
+    int slot = -1;
+    if (tid < g.bs) {
+      const int sid = g.sorted[int64_t(b) * g.bs + tid];
+      if (sid >= 0 && sid < g.n_slots) slot = sid;
+    }
+    s_slot[tid] = slot;
+  }
+  __syncthreads();
+  const uint64_t valid = __ballot(s_slot[lane] >= 0);
+  if (valid == 0) return;
+  const int nvalid = 64 - __builtin_clzll(valid);
+  const int nsub = (nvalid + 15) >> 4;
+
+  const int gps = g.groups_per_split;
+  const int g0 = ks * gps;
+  const int groups_total = g.K >> 7;
+  const __amdgpu_buffer_rsrc_t wbuf =
+      buffer(g.w + int64_t(e) * (g.K >> 4) * (g.N >> 1), uint32_t(g.K >> 4) * uint32_t(g.N >> 1) * 16u);
+  const __amdgpu_buffer_rsrc_t sbuf =
+      buffer(g.s + int64_t(e) * groups_total * g.N, uint32_t(groups_total) * uint32_t(g.N) * 2u);
+  const __amdgpu_buffer_rsrc_t abuf = buffer(g.a, g.a_bytes);
+  const uint32_t wstep = uint32_t(g.N) * 16u;
+  const int t = tile_ok ? tile : 0;  // a missing tile streams tile 0 and stores nothing
+  uint32_t woff[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) woff[st] = fragment_offset(g.N, t, lane) + st * wstep;
+  const uint32_t soff = uint32_t(t * 64 + 8 * (lane & 7)) * 2u;
+  uint32_t boff[kSub];
+#pragma unroll
+  for (int sb = 0; sb < kSub; ++sb) {
+    const int slot = s_slot[16 * sb + col];
+    boff[sb] = slot >= 0 ? uint32_t((int64_t(slot / g.top_k) * g.a_stride + 8 * q) * 2) : 0x80000000u;
+  }
+
+  auto ring_at = [&](int k) -> u32x4_t* {
+    return (k == 0 ? ring0 : (k == 1 ? ring1 : ring2)) + wave * 256;
+  };
+  u32x4_t ring_s[3];
+  auto load_group = [&](int k, int grp) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wbuf, (lds_ptr_t)(ring_at(k) + st * 64), 16, woff[st],
+                                               int(uint32_t(grp) * 4u * wstep), 0, 0);
+    }
+    ring_s[k] = load16(sbuf, soff, uint32_t(grp) * uint32_t(g.N) * 2u);
+  };
+
+  NibbleMasks masks;
+  masks.lo = 0x000f000fu;
+  masks.hi = 0x00f000f0u;
+  masks.magic = 0x64006400u;
+
+  auto run = [&](auto ns_tag) {
+    constexpr int kNs = decltype(ns_tag)::value;
+    f32x4_t acc[4][kNs];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int sb = 0; sb < kNs; ++sb) acc[j][sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // B operands of the current group's steps; step st of the next group is
+    // loaded into breg[st] as soon as step st of this one has been read
+    u32x4_t breg[4][kNs];
+    auto load_b = [&](int st, int grp) {
+#pragma unroll
+      for (int sb = 0; sb < kNs; ++sb) breg[st][sb] = load16(abuf, boff[sb], uint32_t(grp * 128 + 32 * st) * 2u);
+    };
+    load_group(0, g0);
+    if (gps > 1) load_group(1, g0 + 1);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) load_b(st, g0);
+
+    auto body = [&](int i, auto slot_tag) {
+      constexpr int kSlot = decltype(slot_tag)::value;
+      const int grp = g0 + i;
+      if (i + 2 < gps) load_group((kSlot + 2) % 3, grp + 2);
+      Scales<kBF16> sc;
+      sc.set(ring_s[kSlot], lane);
+      const u32x4_t* ring = ring_at(kSlot);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const u32x4_t v = ring[st * 64 + lane];
+        u32x4_t bop[kNs];
+#pragma unroll
+        for (int sb = 0; sb < kNs; ++sb) bop[sb] = breg[st][sb];
+        if (i + 1 < gps) load_b(st, grp + 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x4_t a = sc.operand(combine(v[j], lane), j, masks);
+#pragma unroll
+          for (int sb = 0; sb < kNs; ++sb) acc[j][sb] = mfma<kBF16>(a, bop[sb], acc[j][sb]);
+        }
+      }
+    };
+    for (int i = 0; i < gps; i += 3) {
+      body(i, std::integral_constant<int, 0>{});
+      if (i + 1 < gps) body(i + 1, std::integral_constant<int, 1>{});
+      if (i + 2 < gps) body(i + 2, std::integral_constant<int, 2>{});
+    }
+
+    if constexpr (kMode == kSwiglu) {
+      // up wavefronts hand their sums to the gate wavefront of the same tile
+      // column through ring slots 0 (sub-blocks 0, 1) and 1 (2, 3): every
+      // wavefront's ring reads are done
+      __syncthreads();
+      auto xch = [&](int w, int j, int sb) {
+        return reinterpret_cast<f32x4_t*>(sb < 2 ? ring0 : ring1) + ((w * 4 + j) * 2 + (sb & 1)) * 64 + lane;
+      };
+      if (wave >= 2) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int sb = 0; sb < kNs; ++sb) *xch(wave - 2, j, sb) = acc[j][sb];
+      }
+      __syncthreads();
+      if (wave >= 2 || !tile_ok) return;
+#pragma unroll
+      for (int sb = 0; sb < kNs; ++sb) {
+        const int slot = s_slot[16 * sb + col];
+        if (slot < 0) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4_t u = *xch(wave, j, sb);
+          const f32x4_t gsum = acc[j][sb];
+          uint16_t hv[4];
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            const float gv = fminf(round_act<kBF16>(gsum[x]), g.limit);
+            const float uv = fmaxf(fminf(round_act<kBF16>(u[x]), g.limit), -g.limit);
+            const float sl = round_act<kBF16>(gv / (1.0f + expf(-gv)));
+            hv[x] = to_act<kBF16>(sl * uv);
+          }
+          // columns n .. n + 3 (n = 4q mod 8 inside their 32-k step): two
+          // adjacent pairs in the permuted layout
+          const int n = tile * 64 + 16 * j + 4 * q;
+          uint16_t* row = g.out + int64_t(slot) * g.out_stride;
+          *reinterpret_cast<uint32_t*>(row + permuted_k(n)) = uint32_t(hv[0]) | (uint32_t(hv[1]) << 16);
+          *reinterpret_cast<uint32_t*>(row + permuted_k(n + 2)) = uint32_t(hv[2]) | (uint32_t(hv[3]) << 16);
+        }
+      }
+      return;
+    }
+    if (!tile_ok) return;
+#pragma unroll
+    for (int sb = 0; sb < kNs; ++sb) {
+      const int slot = s_slot[16 * sb + col];
+      if (slot < 0) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t n = int64_t(tile) * 64 + 16 * j + 4 * q;
+        const f32x4_t v = acc[j][sb];
+        if constexpr (kMode == kPartial) {
+          *reinterpret_cast<f32x4_t*>(g.part + (int64_t(ks) * g.n_slots + slot) * g.N + n) = v;
+        } else {
+          float x[4] = {v[0], v[1], v[2], v[3]};
+          if constexpr (kMode == kTopk) {
+            const float w = round_act<kBF16>(g.topk_w[slot]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] = round_act<kBF16>(x[u]) * w;  // exact product
+          }
+          const u32x2_t packed = {uint32_t(to_act<kBF16>(x[0])) | (uint32_t(to_act<kBF16>(x[1])) << 16),
+                                  uint32_t(to_act<kBF16>(x[2])) | (uint32_t(to_act<kBF16>(x[3])) << 16)};
+          *reinterpret_cast<u32x2_t*>(g.out + int64_t(slot) * g.out_stride + n) = packed;
+        }
+      }
+    }
+  };
+  if constexpr (kSub == 1) {
+    run(std::integral_constant<int, 1>{});
+  } else if constexpr (kSub == 2) {
+    if (nsub == 1) run(std::integral_constant<int, 1>{});
+    else run(std::integral_constant<int, 2>{});
+  } else {
+    if (nsub <= 2) run(std::integral_constant<int, 2>{});
+    else run(std::integral_constant<int, 4>{});
+  }
+}
+
+// out[r][permuted_k(k)] = a[r][k]: rows of `cols` elements (cols % 32 == 0).
+__global__ __launch_bounds__(kThreads) void marlin_permute_kernel(const uint16_t* a, int64_t a_stride,
+                                                                 int64_t rows, int cols, uint16_t* out,
+                                                                 int64_t out_stride) {
+  // one thread per (row, 32-k step, pair of halves)
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t pairs = int64_t(cols) / 2;
+  if (i >= rows * pairs) return;
+  const int64_t r = i / pairs;
+  const int k = int(i - r * pairs) * 2;
+  const uint32_t v = *reinterpret_cast<const uint32_t*>(a + r * a_stride + k);
+  *reinterpret_cast<uint32_t*>(out + r * out_stride + permuted_k(k)) = v;
+}
+
 // ---- dequant of one matrix (the GEMM's own operand path, for exact checks) ----
 
 // W [K][N] in the activation dtype: one wavefront per (step, tile), the same
@@ -700,6 +946,26 @@ int launch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t
   return vq::check_launch("marlin_gemm");
 }
 
+template <bool kBF16, int kSub>
+int launch_direct(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t s) {
+  const unsigned gx = mode == kSwiglu ? unsigned(g.N / 128 / 2) : unsigned((g.N / 64 + 3) / 4);
+  const dim3 grid(gx, unsigned(blocks), unsigned(ksplit));
+  switch (mode) {
+    case kPartial: hipLaunchKernelGGL((marlin_gemm_direct<kBF16, kSub, kPartial>), grid, dim3(kThreads), 0, s, g); break;
+    case kStore: hipLaunchKernelGGL((marlin_gemm_direct<kBF16, kSub, kStore>), grid, dim3(kThreads), 0, s, g); break;
+    case kTopk: hipLaunchKernelGGL((marlin_gemm_direct<kBF16, kSub, kTopk>), grid, dim3(kThreads), 0, s, g); break;
+    default: hipLaunchKernelGGL((marlin_gemm_direct<kBF16, kSub, kSwiglu>), grid, dim3(kThreads), 0, s, g); break;
+  }
+  return vq::check_launch("marlin_gemm_direct");
+}
+
+template <bool kBF16>
+int dispatch_direct(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t s) {
+  if (g.bs <= 16) return launch_direct<kBF16, 1>(g, mode, blocks, ksplit, s);
+  if (g.bs <= 32) return launch_direct<kBF16, 2>(g, mode, blocks, ksplit, s);
+  return launch_direct<kBF16, 4>(g, mode, blocks, ksplit, s);
+}
+
 // One 64-column tile per workgroup with its four wavefronts splitting K (few
 // blocks: many workgroups), or four tiles per workgroup sharing the staged
 // activations (enough blocks to fill the GPU: a quarter of the activation
@@ -722,19 +988,24 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 }  // namespace
 }  // namespace marlin
 
-extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
-                               const int32_t* w, const void* scales, int64_t experts,
-                               const int32_t* sorted, int64_t sorted_numel, const int32_t* expert_ids,
-                               int64_t expert_ids_numel, const int32_t* ntpp, const float* topk_w,
-                               int64_t top_k, int64_t n_slots, int64_t K, int64_t N,
-                               int64_t block_size, int mode, int64_t ksplit, float* part,
-                               int64_t part_numel, void* out, int64_t out_stride, int64_t out_rows,
-                               void* stream) {
+namespace marlin {
+namespace {
+
+// Argument checks shared by the staged and the direct GEMM (the reference's
+// checks where it has them), then the kernel arguments; `blocks` = the
+// aligned blocks to launch (0: nothing to do).
+int prepare_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride, const int32_t* w,
+                 const void* scales, int64_t experts, const int32_t* sorted, int64_t sorted_numel,
+                 const int32_t* expert_ids, int64_t expert_ids_numel, const int32_t* ntpp,
+                 const float* topk_w, int64_t top_k, int64_t n_slots, int64_t K, int64_t N,
+                 int64_t block_size, int mode, int64_t ksplit, float limit, float* part,
+                 int64_t part_numel, void* out, int64_t out_stride, int64_t out_rows, GemmArgs& g,
+                 int64_t& blocks) {
   using namespace vq;
   if (act_dtype != kBF16 && act_dtype != kFP16) return fail("a: bf16 or fp16 activations");
   if (K <= 0 || N <= 0 || K % 128 != 0 || N % 64 != 0) return fail("K % 128, N % 64");
   if (K > INT_MAX / 2 || N > INT_MAX / 2) return fail("K and N must fit int32");
-  if (block_size < 8 || block_size > marlin::kMaxBlock || block_size % 8 != 0) {
+  if (block_size < 8 || block_size > kMaxBlock || block_size % 8 != 0) {
     return fail("moe block size must be a multiple of 8 up to 64");
   }
   if (top_k <= 0 || n_slots < 0 || n_slots > INT_MAX || experts <= 0 || experts > INT_MAX) {
@@ -747,34 +1018,40 @@ extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int
   if (a_rows * a_stride * 2 >= (int64_t(1) << 31) || K * N / 2 >= (int64_t(1) << 31)) {
     return fail("a and each expert's weights must stay below 2 GiB");
   }
-  if (!marlin::aligned16(a) || !marlin::aligned16(w) || !marlin::aligned16(scales)) {
+  if (!aligned16(a) || !aligned16(w) || !aligned16(scales)) {
     return fail("a, w and s must be 16-byte aligned");
   }
   // every routed block holds at least one slot, and routed blocks come first
-  const int64_t blocks =
-      std::min(std::min<int64_t>(sorted_numel / block_size, expert_ids_numel), n_slots);
+  blocks = std::min(std::min<int64_t>(sorted_numel / block_size, expert_ids_numel), n_slots);
   if (blocks > 65535) return fail("too many aligned blocks");
   const int64_t groups = K / 128;
   if (ksplit <= 0 || groups % ksplit != 0 || ksplit > 65535) {
     return fail("ksplit must divide K / 128");
   }
-  if (mode == marlin::kPartial) {
+  if (mode == kPartial) {
     if (!part || part_numel < ksplit * n_slots * N) return fail("w13 partial buffer");
-    if (!marlin::aligned16(part)) return fail("w13 partial buffer must be 16-byte aligned");
-  } else if (mode == marlin::kStore || mode == marlin::kTopk) {
+    if (!aligned16(part)) return fail("w13 partial buffer must be 16-byte aligned");
+  } else if (mode == kStore || mode == kTopk) {
     if (ksplit != 1) return fail("a stored output takes one k-slice");
     if (!out || out_stride < N || out_stride % 4 != 0 || out_rows < n_slots) return fail("output too small");
     if ((reinterpret_cast<uintptr_t>(out) & 7) != 0) return fail("output must be 8-byte aligned");
-    if (mode == marlin::kTopk && !topk_w) return fail("topk weights required");
+    if (mode == kTopk && !topk_w) return fail("topk weights required");
+  } else if (mode == kSwiglu) {
+    if (ksplit != 1) return fail("a stored output takes one k-slice");
+    if (N % 256 != 0) return fail("SwiGLU: the gate and up halves must be whole 128-column pairs");
+    if (!out || out_stride < N / 2 || out_stride % 32 != 0 || out_rows < n_slots) {
+      return fail("h output too small (row stride a multiple of 32)");
+    }
+    if ((reinterpret_cast<uintptr_t>(out) & 7) != 0) return fail("output must be 8-byte aligned");
+    if (std::isnan(limit)) return fail("act: limit must not be NaN");
   } else {
     return fail("unknown marlin_moe_gemm mode");
   }
-  if (n_slots == 0 || blocks == 0) return kOk;
-  marlin::GemmArgs g{};
+  g = GemmArgs{};
   g.a = static_cast<const uint16_t*>(a);
   g.a_stride = a_stride;
   g.a_bytes = uint32_t(a_rows * a_stride * 2);
-  g.w = reinterpret_cast<const marlin::u32x4_t*>(w);
+  g.w = reinterpret_cast<const u32x4_t*>(w);
   g.s = static_cast<const uint16_t*>(scales);
   g.sorted = sorted;
   g.eids = expert_ids;
@@ -790,14 +1067,81 @@ extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int
   g.bs = int(block_size);
   g.experts = int(experts);
   g.groups_per_split = int(groups / ksplit);
+  g.limit = limit;
+  if (n_slots == 0) blocks = 0;
+  return kOk;
+}
+
+}  // namespace
+}  // namespace marlin
+
+extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
+                               const int32_t* w, const void* scales, int64_t experts,
+                               const int32_t* sorted, int64_t sorted_numel, const int32_t* expert_ids,
+                               int64_t expert_ids_numel, const int32_t* ntpp, const float* topk_w,
+                               int64_t top_k, int64_t n_slots, int64_t K, int64_t N,
+                               int64_t block_size, int mode, int64_t ksplit, float* part,
+                               int64_t part_numel, void* out, int64_t out_stride, int64_t out_rows,
+                               void* stream) {
+  if (mode == marlin::kSwiglu) return vq::fail("unknown marlin_moe_gemm mode");
+  marlin::GemmArgs g;
+  int64_t blocks = 0;
+  if (int rc = marlin::prepare_gemm(a, act_dtype, a_rows, a_stride, w, scales, experts, sorted, sorted_numel,
+                                    expert_ids, expert_ids_numel, ntpp, topk_w, top_k, n_slots, K, N,
+                                    block_size, mode, ksplit, INFINITY, part, part_numel, out, out_stride,
+                                    out_rows, g, blocks)) {
+    return rc;
+  }
+  if (blocks == 0) return vq::kOk;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   // four tiles per workgroup once that still gives ~2 workgroups per CU
   // (the routed blocks are at most min(blocks, n_slots / 2 + experts); use
   // the cheaper estimate of blocks routed by the slot count)
   const int64_t routed_blocks = std::min<int64_t>(blocks, (n_slots + block_size - 1) / block_size + experts / 2);
   const int wide = routed_blocks * (N / 256) * ksplit >= 512 ? 1 : 0;
-  return act_dtype == kBF16 ? marlin::dispatch_gemm<true>(g, mode, int(blocks), int(ksplit), wide, s)
-                            : marlin::dispatch_gemm<false>(g, mode, int(blocks), int(ksplit), wide, s);
+  return act_dtype == vq::kBF16 ? marlin::dispatch_gemm<true>(g, mode, int(blocks), int(ksplit), wide, s)
+                                : marlin::dispatch_gemm<false>(g, mode, int(blocks), int(ksplit), wide, s);
+}
+
+extern "C" int marlin_moe_gemm_direct(const void* a_perm, int act_dtype, int64_t a_rows, int64_t a_stride,
+                                      const int32_t* w, const void* scales, int64_t experts,
+                                      const int32_t* sorted, int64_t sorted_numel,
+                                      const int32_t* expert_ids, int64_t expert_ids_numel,
+                                      const int32_t* ntpp, const float* topk_w, int64_t top_k,
+                                      int64_t n_slots, int64_t K, int64_t N, int64_t block_size, int mode,
+                                      int64_t ksplit, float limit, float* part, int64_t part_numel,
+                                      void* out, int64_t out_stride, int64_t out_rows, void* stream) {
+  marlin::GemmArgs g;
+  int64_t blocks = 0;
+  if (int rc = marlin::prepare_gemm(a_perm, act_dtype, a_rows, a_stride, w, scales, experts, sorted,
+                                    sorted_numel, expert_ids, expert_ids_numel, ntpp, topk_w, top_k, n_slots,
+                                    K, N, block_size, mode, ksplit, limit, part, part_numel, out, out_stride,
+                                    out_rows, g, blocks)) {
+    return rc;
+  }
+  if (blocks == 0) return vq::kOk;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  return act_dtype == vq::kBF16 ? marlin::dispatch_direct<true>(g, mode, int(blocks), int(ksplit), s)
+                                : marlin::dispatch_direct<false>(g, mode, int(blocks), int(ksplit), s);
+}
+
+extern "C" int marlin_permute_act(const void* a, int act_dtype, int64_t rows, int64_t cols, int64_t a_stride,
+                                  void* out, int64_t out_stride, void* stream) {
+  using namespace vq;
+  if (act_dtype != kBF16 && act_dtype != kFP16) return fail("a: bf16 or fp16 activations");
+  if (rows < 0 || cols <= 0 || cols % 32 != 0 || cols > INT_MAX) return fail("permute: cols % 32");
+  if (a_stride < cols || out_stride < cols || a_stride % 2 != 0 || out_stride % 2 != 0) {
+    return fail("permute: even row strides of at least cols");
+  }
+  if ((reinterpret_cast<uintptr_t>(a) & 3) != 0 || (reinterpret_cast<uintptr_t>(out) & 3) != 0) {
+    return fail("permute: 4-byte aligned rows");
+  }
+  if (rows == 0) return kOk;
+  const int64_t pairs = rows * (cols / 2);
+  hipLaunchKernelGGL(marlin::marlin_permute_kernel, dim3(unsigned((pairs + marlin::kThreads - 1) / marlin::kThreads)),
+                     dim3(marlin::kThreads), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(a),
+                     a_stride, rows, int(cols), static_cast<uint16_t*>(out), out_stride);
+  return check_launch("marlin_permute");
 }
 
 extern "C" int marlin_moe_act(const float* part, const int32_t* ids, int64_t ksplit, int64_t n_slots,

@@ -58,6 +58,17 @@ SIGNATURES = {
         c_vp, c_i64, c_vp, c_i64, c_i64,      # part, part_numel, out, out_stride, out_rows
         c_vp,                                 # stream
     ]),
+    "marlin_moe_gemm_direct": (c_int, [
+        c_vp, c_int, c_i64, c_i64,            # a_perm, act_dtype, a_rows, a_stride
+        c_vp, c_vp, c_i64,                    # w, scales, experts
+        c_vp, c_i64, c_vp, c_i64, c_vp,       # sorted, numel, expert_ids, numel, ntpp
+        c_vp, c_i64, c_i64,                   # topk_w, top_k, n_slots
+        c_i64, c_i64, c_i64, c_int, c_i64,    # K, N, block_size, mode, ksplit
+        ctypes.c_float,                       # limit
+        c_vp, c_i64, c_vp, c_i64, c_i64,      # part, part_numel, out, out_stride, out_rows
+        c_vp,                                 # stream
+    ]),
+    "marlin_permute_act": (c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp]),
     "marlin_moe_act": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, ctypes.c_float, c_vp, c_int,
                                c_vp]),
     "marlin_dequant": (c_int, [c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_vp]),

@@ -12,13 +12,15 @@ for type only.  The work counters ``ctr`` are left as they are (zero).
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from ... import _native
 
 _DTYPE_CODES = {torch.bfloat16: _native.BF16, torch.float16: _native.FP16}
 
-MODE_PARTIAL, MODE_STORE, MODE_TOPK = 0, 1, 2
+MODE_PARTIAL, MODE_STORE, MODE_TOPK, MODE_SWIGLU = 0, 1, 2, 3
 
 # build_info keys (ampere_marlin/module.cpp:9-15): abi_version 1, prefill
 # schedule version 2 (extension.py:47).
@@ -102,6 +104,55 @@ def gemm(a, w, s, sorted_ids, expert_ids, ntpp, topk_w, top_k, n_slots, K, N, bl
             0 if part is None else part.data_ptr(), 0 if part is None else part.numel(),
             0 if out is None else out.data_ptr(), 0 if out is None else out.stride(0),
             0 if out is None else out.size(0), _stream(a.device))
+    _native.check(status)
+
+
+def gemm_direct(a_perm, w, s, sorted_ids, expert_ids, ntpp, topk_w, top_k, n_slots, K, N,
+                block_size, mode, ksplit=1, limit=math.inf, part=None, out=None) -> None:
+    """marlin_moe_gemm_direct on torch tensors: gemm's contract on k-permuted
+    activations (permute_act), plus mode MODE_SWIGLU (out = h, permuted)."""
+    _require(a_perm.dtype in _DTYPE_CODES and a_perm.dim() == 2 and a_perm.stride(1) == 1,
+             "a: bf16 or fp16, unit inner stride")
+    _require(s.dtype == a_perm.dtype and w.dtype == torch.int32 and w.is_contiguous()
+             and s.is_contiguous(), "weights contiguous, scales of the activation dtype")
+    _require(w.dim() == 3 and w.size(1) * 16 == K and w.size(2) == 2 * N, "w: int32 [E, K/16, 2N]")
+    _require(s.dim() == 3 and s.size(0) == w.size(0) and s.size(1) * 128 == K and s.size(2) == N,
+             "s: [E, K/128, N]")
+    for t, name in ((w, "w"), (s, "s"), (sorted_ids, "sorted"), (expert_ids, "eids"),
+                    (ntpp, "ntpp")):
+        _on(t, a_perm.device, name)
+    if topk_w is not None:
+        _require(topk_w.dtype == torch.float32 and topk_w.is_contiguous(), "topk weights fp32")
+    if out is not None:
+        _require(out.dtype == a_perm.dtype and out.dim() == 2 and out.stride(1) == 1,
+                 "out: activation dtype, unit inner stride")
+    if part is not None:
+        _require(part.dtype == torch.float32 and part.is_contiguous(), "w13 partial buffer")
+    lib = _native.load()
+    with torch.cuda.device(a_perm.device):
+        status = lib.marlin_moe_gemm_direct(
+            a_perm.data_ptr(), _DTYPE_CODES[a_perm.dtype], a_perm.size(0), a_perm.stride(0),
+            w.data_ptr(), s.data_ptr(), w.size(0), sorted_ids.data_ptr(), sorted_ids.numel(),
+            expert_ids.data_ptr(), expert_ids.numel(), ntpp.data_ptr(),
+            0 if topk_w is None else topk_w.data_ptr(), int(top_k), int(n_slots), int(K), int(N),
+            int(block_size), int(mode), int(ksplit), float(limit),
+            0 if part is None else part.data_ptr(), 0 if part is None else part.numel(),
+            0 if out is None else out.data_ptr(), 0 if out is None else out.stride(0),
+            0 if out is None else out.size(0), _stream(a_perm.device))
+    _native.check(status)
+
+
+def permute_act(a, out) -> None:
+    """marlin_permute_act: out[r][p(k)] = a[r][k], the k order gemm_direct reads."""
+    _require(a.dtype in _DTYPE_CODES and out.dtype == a.dtype and a.dim() == 2 and out.dim() == 2
+             and a.stride(1) == 1 and out.stride(1) == 1 and out.shape == a.shape,
+             "a, out: same shape and dtype, unit inner stride")
+    _on(out, a.device, "out")
+    lib = _native.load()
+    with torch.cuda.device(a.device):
+        status = lib.marlin_permute_act(a.data_ptr(), _DTYPE_CODES[a.dtype], a.size(0), a.size(1),
+                                        a.stride(0), out.data_ptr(), out.stride(0),
+                                        _stream(a.device))
     _native.check(status)
 
 

@@ -50,11 +50,34 @@ def choose_w13_ksplit(blocks: int, n13: int, k: int, bs: int, target: int = 768)
 
 
 def workspace_shapes(tokens: int, topk: int, hidden: int, inter: int, experts: int,
-                     block_size: int, ksplit: int) -> dict:
+                     block_size: int, ksplit: int, direct: bool = False) -> dict:
     slots = tokens * topk
     size, blocks = align_sizes(slots, experts, block_size)
-    return {"sorted": (size,), "expert_ids": (blocks,), "ntpp": (1,),
-            "part": (ksplit * slots * 2 * inter,), "h": (slots, inter), "c3": (slots, hidden)}
+    shapes = {"sorted": (size,), "expert_ids": (blocks,), "ntpp": (1,), "h": (slots, inter),
+              "c3": (slots, hidden)}
+    if direct:
+        shapes["xp"] = (tokens, hidden)
+    else:
+        shapes["part"] = (ksplit * slots * 2 * inter,)
+    return shapes
+
+
+# workgroups the direct w13 must have to be chosen (tuned on MI355X)
+_DIRECT_MIN_WORKGROUPS = 384
+
+
+def direct_applies(tokens: int, topk: int, hidden: int, inter: int, experts: int,
+                   block_size: int) -> bool:
+    """The direct path (k-permuted activations, weights through an LDS ring,
+    SwiGLU fused into w13) needs blocks of at most 32 tokens, whole 256-column
+    gate / up pairs, and enough routed blocks for its four-tile workgroups
+    to fill the GPU (the expected touched experts times the w13 workgroups
+    per block)."""
+    if block_size > 32 or (2 * inter) % 256 != 0 or hidden % 32 != 0:
+        return False
+    slots = tokens * topk
+    touched = experts * (1.0 - (1.0 - 1.0 / max(experts, 1)) ** slots)
+    return touched * (2 * inter // 256) >= _DIRECT_MIN_WORKGROUPS
 
 
 def marlin_dequant(w: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
@@ -76,11 +99,16 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
                      topk_ids: torch.Tensor, clamp_limit: float | None = None,
                      expert_map: torch.Tensor | None = None, block_size: int | None = None,
                      ksplit: int | None = None, workspace: dict | None = None,
-                     output: torch.Tensor | None = None) -> torch.Tensor:
+                     output: torch.Tensor | None = None, path: str | None = None) -> torch.Tensor:
     """out [M, K] = sum over the top-k slots (slot order) of
     RN(RN(w2_e(h)) * RN(router weight)), h = RN(RN(SiLU(min(g, L))) *
     clamp(u, -L, L)), (g | u) = RN(w1_e(x)).  Slots routed outside the local
-    experts (id out of range, or mapped to -1) add nothing."""
+    experts (id out of range, or mapped to -1) add nothing.
+
+    path: None (automatic), "staged" (activations staged in LDS per
+    workgroup, any block size and K split) or "direct" (k-permuted
+    activations, SwiGLU fused into w13; blocks of at most 32 tokens, K split
+    1).  Both give the same sums."""
     M, K = hidden_states.shape
     E = w1.size(0)
     N = w2.size(1) * 16
@@ -106,13 +134,22 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
         inside = (ids >= 0) & (ids < emap.numel())
         local = torch.where(inside, emap[torch.where(inside, ids, 0).long()], -1).contiguous()
     bs = block_size or choose_block_size(M, topk, E)
+    if path is None:
+        direct = ksplit in (None, 1) and direct_applies(M, topk, K, N, E, bs)
+    elif path in ("direct", "staged"):
+        direct = path == "direct"
+        if direct and (ksplit not in (None, 1) or bs > 32 or (2 * N) % 256 != 0 or K % 32 != 0):
+            raise RuntimeError("the direct path takes blocks of <= 32 tokens, K split 1, "
+                               "intermediate % 128 == 0 and hidden % 32 == 0")
+    else:
+        raise RuntimeError(f"unknown path {path!r}")
     blocks_est = min(slots, E)
-    ks = ksplit or choose_w13_ksplit(blocks_est, 2 * N, K, bs)
-    shapes = workspace_shapes(M, topk, K, N, E, bs, ks)
+    ks = 1 if direct else (ksplit or choose_w13_ksplit(blocks_est, 2 * N, K, bs))
+    shapes = workspace_shapes(M, topk, K, N, E, bs, ks, direct)
     ws = workspace if workspace is not None else {}
     buf = {}
     for name, shape in shapes.items():
-        dtype = {"part": torch.float32, "h": hidden_states.dtype,
+        dtype = {"part": torch.float32, "h": hidden_states.dtype, "xp": hidden_states.dtype,
                  "c3": hidden_states.dtype}.get(name, torch.int32)
         t = ws.get(name)
         numel = math.prod(shape)
@@ -123,6 +160,14 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
     kernel_moe_align_block_size(local, E, bs, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
                                 None)
     tw = topk_weights.to(torch.float32).contiguous().view(-1)
+    if direct:
+        _C.permute_act(hidden_states, buf["xp"])
+        _C.gemm_direct(buf["xp"], w1, w1_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
+                       topk, slots, K, 2 * N, bs, _C.MODE_SWIGLU, 1, limit, out=buf["h"])
+        _C.gemm_direct(buf["h"], w2, w2_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], tw, 1,
+                       slots, N, K, bs, _C.MODE_TOPK, 1, out=buf["c3"])
+        moe_sum(buf["c3"].view(M, topk, K), out, local, E)
+        return out
     _C.gemm(hidden_states, w1, w1_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
             topk, slots, K, 2 * N, bs, _C.MODE_PARTIAL, ks, part=buf["part"])
     _C.act(buf["part"], local.view(-1), ks, slots, N, limit, buf["h"])
