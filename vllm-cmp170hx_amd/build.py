@@ -61,6 +61,21 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _check_undefined(library: str) -> None:
+    """A shared library links with undefined symbols, which only fail when it
+    is loaded: reject a kernel launch stub the host compilation did not emit
+    (clang can drop one silently) or any other symbol of this project."""
+    nm = shutil.which("nm")
+    if not nm:
+        return
+    res = subprocess.run([nm, "-u", "-C", library], capture_output=True, text=True)
+    bad = [line.strip() for line in res.stdout.splitlines()
+           if "__device_stub__" in line or any(ns in line for ns in ("exl3::", "marlin::", "vq::"))]
+    if bad:
+        os.remove(library)
+        raise RuntimeError("linked library has undefined project symbols:\n  " + "\n  ".join(bad[:10]))
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> str:
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
@@ -70,6 +85,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"linking failed:\n{res.stdout}\n{res.stderr}")
+    _check_undefined(tmp)
     os.replace(tmp, LIBRARY)
     if verbose:
         print(f"built {LIBRARY}")

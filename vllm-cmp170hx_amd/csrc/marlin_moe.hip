@@ -457,25 +457,50 @@ __host__ __device__ __forceinline__ int permuted_k(int k) {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// As marlin_gemm with four 64-column tiles per workgroup (one per
-// wavefront, all of the workgroup's K range), but:
-//  * weights stream through a per-wavefront LDS ring of three 128-k groups
-//    (buffer_load_dwordx4 ... lds: no VGPR staging), two groups ahead;
+// As marlin_gemm, but:
+//  * each wavefront owns direct_tiles 64-column tiles over the workgroup's
+//    whole K range (with two, every B operand it loads feeds both tiles'
+//    MFMAs);
+//  * weights stream through a per-wavefront LDS ring of direct_slots
+//    half-groups (64 k of its tiles, buffer_load_dwordx4 ... lds: no VGPR
+//    staging);
 //  * each lane loads its B operands straight from k-permuted activations
 //    (one 16-byte load per step and 16-token sub-block, one group ahead), so
 //    there is no activation staging and no workgroup barrier in the loop;
-//  * kSwiglu: wavefronts 0, 1 take gate tiles 2p, 2p + 1 and wavefronts 2, 3
-//    the matching up tiles (N / 128 + 2p ...): the up sums meet the gate sums
+//  * kSwiglu: wavefronts 0, 1 take gate tiles and wavefronts 2, 3 the
+//    matching up tiles (N / 128 further on): the up sums meet the gate sums
 //    in LDS and h = RN(RN(SiLU(min(G, L))) * clamp(U, -L, L)) is written in
 //    the permuted layout (the w2 GEMM's input), G / U the activation-dtype
 //    roundings of the FP32 sums (marlin_act_kernel's arithmetic).
 // The MFMA sequence per tile is marlin_gemm's, so the sums are bitwise the
 // same.
+// Tiles per wavefront and ring slots (half-groups) per wavefront by mode.
+// kSwiglu: one tile per wavefront (a workgroup = two gate tiles and their
+// up tiles), so the GPU holds every workgroup of a 256-token w13 at once
+// and its VALU dequant spreads over more wavefronts; three half-groups
+// ahead.  The other modes: two tiles per wavefront (each B operand feeds
+// both), one half-group ahead.
+template <int kMode>
+struct DirectShape {
+  static constexpr int kTiles = kMode == kSwiglu ? 1 : 2;
+  static constexpr int kSlots = kMode == kSwiglu ? 4 : 2;
+};
+inline int direct_tiles(int mode) { return mode == kSwiglu ? DirectShape<kSwiglu>::kTiles : DirectShape<kTopk>::kTiles; }
+// The kernel's per-tile arrays have this fixed size (loops run to the mode's
+// tile count): arrays whose size depends on the template arguments, captured
+// by the kernel's lambdas, make the host compilation drop the kernel's launch
+// stub.
+constexpr int kMaxDirectTiles = 2;
 template <bool kBF16, int kSub, int kMode>
-__global__ __launch_bounds__(kThreads) void marlin_gemm_direct(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) u32x4_t ring0[4 * 4 * 64];
-  __shared__ __attribute__((aligned(16))) u32x4_t ring1[4 * 4 * 64];
-  __shared__ __attribute__((aligned(16))) u32x4_t ring2[4 * 4 * 64];
+__global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direct(GemmArgs g) {
+  constexpr int kDirectTiles = DirectShape<kMode>::kTiles;
+  constexpr int kSlots = DirectShape<kMode>::kSlots;
+  // ring slot = [wavefront][tile][step of the half-group][64 lanes] x 16 bytes
+  constexpr int kSlotVecs = 4 * kDirectTiles * 2 * 64;
+  __shared__ __attribute__((aligned(16))) u32x4_t ring0[kSlotVecs];
+  __shared__ __attribute__((aligned(16))) u32x4_t ring1[kSlotVecs];
+  __shared__ __attribute__((aligned(16))) u32x4_t ring2[kSlots > 2 ? kSlotVecs : 4];
+  __shared__ __attribute__((aligned(16))) u32x4_t ring3[kSlots > 2 ? kSlotVecs : 4];
   __shared__ int s_slot[kMaxBlock];
 
   const int tid = threadIdx.x;
@@ -483,14 +508,20 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_direct(GemmArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4;
   const int col = lane & 15;
-  int tile;
-  if constexpr (kMode == kSwiglu) {
-    const int p = blockIdx.x;
-    tile = wave < 2 ? 2 * p + wave : (g.N >> 7) + 2 * p + (wave - 2);
-  } else {
-    tile = int(blockIdx.x) * 4 + wave;
+  int tiles[kMaxDirectTiles];
+  bool tile_ok[kMaxDirectTiles];
+#pragma unroll
+  for (int x = 0; x < kDirectTiles; ++x) {
+    if constexpr (kMode == kSwiglu) {
+      const int gate_tiles = g.N >> 7;
+      const int gt = 2 * kDirectTiles * int(blockIdx.x) + kDirectTiles * (wave & 1) + x;  // gate tile
+      tiles[x] = wave < 2 ? gt : gate_tiles + gt;
+      tile_ok[x] = gt < gate_tiles;
+    } else {
+      tiles[x] = 4 * kDirectTiles * int(blockIdx.x) + kDirectTiles * wave + x;
+      tile_ok[x] = tiles[x] < (g.N >> 6);
+    }
   }
-  const bool tile_ok = tile < (g.N >> 6);
   const int b = blockIdx.y;
   const int ks = blockIdx.z;
   if (int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
@@ -513,17 +544,25 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_direct(GemmArgs g) {
   const int gps = g.groups_per_split;
   const int g0 = ks * gps;
   const int groups_total = g.K >> 7;
-  const __amdgpu_buffer_rsrc_t wbuf =
-      buffer(g.w + int64_t(e) * (g.K >> 4) * (g.N >> 1), uint32_t(g.K >> 4) * uint32_t(g.N >> 1) * 16u);
-  const __amdgpu_buffer_rsrc_t sbuf =
-      buffer(g.s + int64_t(e) * groups_total * g.N, uint32_t(groups_total) * uint32_t(g.N) * 2u);
-  const __amdgpu_buffer_rsrc_t abuf = buffer(g.a, g.a_bytes);
   const uint32_t wstep = uint32_t(g.N) * 16u;
-  const int t = tile_ok ? tile : 0;  // a missing tile streams tile 0 and stores nothing
-  uint32_t woff[4];
+  // Buffers over this split's groups only: the loop below issues every load
+  // unconditionally (a load that a branch may skip makes the compiler's
+  // count of loads in flight unknown, and it then waits for all of them),
+  // and the loads of the group after the last fall past the end and return
+  // zeros without touching memory.
+  const __amdgpu_buffer_rsrc_t wbuf =
+      buffer(g.w + (int64_t(e) * (g.K >> 4) + int64_t(g0) * 8) * (g.N >> 1), uint32_t(gps) * 4u * wstep);
+  const __amdgpu_buffer_rsrc_t sbuf =
+      buffer(g.s + (int64_t(e) * groups_total + g0) * g.N, uint32_t(gps) * uint32_t(g.N) * 2u);
+  const __amdgpu_buffer_rsrc_t abuf = buffer(g.a, g.a_bytes);
+  // a missing tile streams tile 0 and stores nothing
+  uint32_t woff[kMaxDirectTiles], soff[kMaxDirectTiles];
 #pragma unroll
-  for (int st = 0; st < 4; ++st) woff[st] = fragment_offset(g.N, t, lane) + st * wstep;
-  const uint32_t soff = uint32_t(t * 64 + 8 * (lane & 7)) * 2u;
+  for (int x = 0; x < kDirectTiles; ++x) {
+    const int t = tile_ok[x] ? tiles[x] : 0;
+    woff[x] = fragment_offset(g.N, t, lane);
+    soff[x] = uint32_t(t * 64 + 8 * (lane & 7)) * 2u;
+  }
   uint32_t boff[kSub];
 #pragma unroll
   for (int sb = 0; sb < kSub; ++sb) {
@@ -531,17 +570,25 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_direct(GemmArgs g) {
     boff[sb] = slot >= 0 ? uint32_t((int64_t(slot / g.top_k) * g.a_stride + 8 * q) * 2) : 0x80000000u;
   }
 
-  auto ring_at = [&](int k) -> u32x4_t* {
-    return (k == 0 ? ring0 : (k == 1 ? ring1 : ring2)) + wave * 256;
+  auto slot_base = [&](int k) -> u32x4_t* {
+    return (k == 0 ? ring0 : (k == 1 ? ring1 : (k == 2 ? ring2 : ring3))) + wave * (kDirectTiles * 2 * 64);
   };
-  u32x4_t ring_s[3];
-  auto load_group = [&](int k, int grp) {
+  // half-group (group i of the split, steps 2 half, 2 half + 1) of both
+  // tiles into ring slot k
+  auto load_half = [&](int k, int i, int half) {
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wbuf, (lds_ptr_t)(ring_at(k) + st * 64), 16, woff[st],
-                                               int(uint32_t(grp) * 4u * wstep), 0, 0);
+    for (int x = 0; x < kDirectTiles; ++x) {
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wbuf, (lds_ptr_t)(slot_base(k) + (2 * x + sl) * 64), 16,
+                                                 woff[x], int(uint32_t(4 * i + 2 * half + sl) * wstep), 0, 0);
+      }
     }
-    ring_s[k] = load16(sbuf, soff, uint32_t(grp) * uint32_t(g.N) * 2u);
+  };
+  u32x4_t s_next[kMaxDirectTiles];
+  auto load_scales = [&](int i) {
+#pragma unroll
+    for (int x = 0; x < kDirectTiles; ++x) s_next[x] = load16(sbuf, soff[x], uint32_t(i) * uint32_t(g.N) * 2u);
   };
 
   NibbleMasks masks;
@@ -551,114 +598,160 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_direct(GemmArgs g) {
 
   auto run = [&](auto ns_tag) {
     constexpr int kNs = decltype(ns_tag)::value;
-    f32x4_t acc[4][kNs];
+    f32x4_t acc[kMaxDirectTiles][4][kNs];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int x = 0; x < kDirectTiles; ++x)
 #pragma unroll
-      for (int sb = 0; sb < kNs; ++sb) acc[j][sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int sb = 0; sb < kNs; ++sb) acc[x][j][sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     // B operands of the current group's steps; step st of the next group is
     // loaded into breg[st] as soon as step st of this one has been read
     u32x4_t breg[4][kNs];
-    auto load_b = [&](int st, int grp) {
+    // (a B offset past the split's last group reads the next k, or past
+    // the buffer: zeros; either way unused)
+    auto load_b = [&](int st, int i) {
 #pragma unroll
-      for (int sb = 0; sb < kNs; ++sb) breg[st][sb] = load16(abuf, boff[sb], uint32_t(grp * 128 + 32 * st) * 2u);
+      for (int sb = 0; sb < kNs; ++sb) breg[st][sb] = load16(abuf, boff[sb], uint32_t((g0 + i) * 128 + 32 * st) * 2u);
     };
-    load_group(0, g0);
-    if (gps > 1) load_group(1, g0 + 1);
+    // Issue order matters too: vmcnt retires loads in order, so a wait for
+    // a B operand also waits for every load issued before it.  Half-group h
+    // (ring slot h % kSlots) starts by issuing the weights of half-group
+    // h + kSlots - 1 into the slot read in half-group h - 1 (and, at a group's
+    // start, the next group's scales); then per step the MFMAs and the B
+    // operands of the same step of the next group (into the registers just
+    // read: no copies).  Every wait then names data that is due, and each
+    // weight load has kSlots - 1 half-groups to land.  The loop runs whole
+    // rounds of kSlots / 2 groups; a group past the split (odd gps) only
+    // issues its loads, which fall past the buffers.
+    auto half_group = [&](int i, int half) { load_half((2 * i + half) % kSlots, i, half); };
 #pragma unroll
-    for (int st = 0; st < 4; ++st) load_b(st, g0);
+    for (int h = 0; h < kSlots - 1; ++h) {
+      half_group(h / 2, h % 2);
+      if (h == 0) {
+        load_scales(0);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) load_b(st, 0);
+      }
+    }
 
-    auto body = [&](int i, auto slot_tag) {
-      constexpr int kSlot = decltype(slot_tag)::value;
-      const int grp = g0 + i;
-      if (i + 2 < gps) load_group((kSlot + 2) % 3, grp + 2);
-      Scales<kBF16> sc;
-      sc.set(ring_s[kSlot], lane);
-      const u32x4_t* ring = ring_at(kSlot);
+    for (int i0 = 0; i0 < gps; i0 += kSlots / 2) {
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const u32x4_t v = ring[st * 64 + lane];
-        u32x4_t bop[kNs];
+      for (int gi = 0; gi < kSlots / 2; ++gi) {
+        const int i = i0 + gi;
+        const bool live = i < gps;
+        Scales<kBF16> sc[kMaxDirectTiles];
 #pragma unroll
-        for (int sb = 0; sb < kNs; ++sb) bop[sb] = breg[st][sb];
-        if (i + 1 < gps) load_b(st, grp + 1);
+        for (int x = 0; x < kDirectTiles; ++x) sc[x].set(s_next[x], lane);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const u32x4_t a = sc.operand(combine(v[j], lane), j, masks);
+        for (int half = 0; half < 2; ++half) {
+          const int h = 2 * gi + half;  // slot
+          const int ahead = 2 * i + half + kSlots - 1;
+          half_group(ahead / 2, ahead % 2);
+          if (half == 0) load_scales(i + 1);
+          asm volatile("" ::: "memory");
 #pragma unroll
-          for (int sb = 0; sb < kNs; ++sb) acc[j][sb] = mfma<kBF16>(a, bop[sb], acc[j][sb]);
+          for (int sl = 0; sl < 2; ++sl) {
+            const int st = 2 * half + sl;
+            if (live) {
+#pragma unroll
+              for (int x = 0; x < kDirectTiles; ++x) {
+                const u32x4_t v = slot_base(h)[(2 * x + sl) * 64 + lane];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                  const u32x4_t a = sc[x].operand(combine(v[j], lane), j, masks);
+#pragma unroll
+                  for (int sb = 0; sb < kNs; ++sb) acc[x][j][sb] = mfma<kBF16>(a, breg[st][sb], acc[x][j][sb]);
+                }
+              }
+            }
+            load_b(st, i + 1);
+            asm volatile("" ::: "memory");
+          }
         }
       }
-    };
-    for (int i = 0; i < gps; i += 3) {
-      body(i, std::integral_constant<int, 0>{});
-      if (i + 1 < gps) body(i + 1, std::integral_constant<int, 1>{});
-      if (i + 2 < gps) body(i + 2, std::integral_constant<int, 2>{});
     }
 
     if constexpr (kMode == kSwiglu) {
-      // up wavefronts hand their sums to the gate wavefront of the same tile
-      // column through ring slots 0 (sub-blocks 0, 1) and 1 (2, 3): every
-      // wavefront's ring reads are done
-      __syncthreads();
-      auto xch = [&](int w, int j, int sb) {
-        return reinterpret_cast<f32x4_t*>(sb < 2 ? ring0 : ring1) + ((w * 4 + j) * 2 + (sb & 1)) * 64 + lane;
+      // up wavefronts 2, 3 hand their sums to gate wavefronts 0, 1 through
+      // ring slots 0, 1 (every wavefront's ring reads are done, and its loads
+      // past the split have landed), two 16-token sub-blocks per round
+      u32x4_t* xbase = wave == 2 || wave == 0 ? ring0 : ring1;
+      auto xch = [&](int x, int j, int sbl) {
+        return reinterpret_cast<f32x4_t*>(xbase) + ((x * 4 + j) * 2 + sbl) * 64 + lane;
       };
-      if (wave >= 2) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+      for (int r0 = 0; r0 < kNs; r0 += 2) {
+        __syncthreads();
+        if (wave >= 2) {
 #pragma unroll
-          for (int sb = 0; sb < kNs; ++sb) *xch(wave - 2, j, sb) = acc[j][sb];
+          for (int x = 0; x < kDirectTiles; ++x)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+              for (int sbl = 0; sbl < 2; ++sbl)
+                if (r0 + sbl < kNs) *xch(x, j, sbl) = acc[x][j][r0 + sbl];
+        }
+        __syncthreads();
+        if (wave < 2) {
+#pragma unroll
+          for (int x = 0; x < kDirectTiles; ++x) {
+            if (!tile_ok[x]) continue;
+#pragma unroll
+            for (int sbl = 0; sbl < 2; ++sbl) {
+              const int sb = r0 + sbl;
+              if (sb >= kNs) continue;
+              const int slot = s_slot[16 * sb + col];
+              if (slot < 0) continue;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const f32x4_t u = *xch(x, j, sbl);
+                const f32x4_t gsum = acc[x][j][sb];
+                uint16_t hv[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                  const float gv = fminf(round_act<kBF16>(gsum[c]), g.limit);
+                  const float uv = fmaxf(fminf(round_act<kBF16>(u[c]), g.limit), -g.limit);
+                  const float sl = round_act<kBF16>(gv / (1.0f + expf(-gv)));
+                  hv[c] = to_act<kBF16>(sl * uv);
+                }
+                // columns n .. n + 3 (n = 4q mod 8 inside their 32-k step): two
+                // adjacent pairs in the permuted layout
+                const int n = tiles[x] * 64 + 16 * j + 4 * q;
+                uint16_t* row = g.out + int64_t(slot) * g.out_stride;
+                *reinterpret_cast<uint32_t*>(row + permuted_k(n)) = uint32_t(hv[0]) | (uint32_t(hv[1]) << 16);
+                *reinterpret_cast<uint32_t*>(row + permuted_k(n + 2)) = uint32_t(hv[2]) | (uint32_t(hv[3]) << 16);
+              }
+            }
+          }
+        }
       }
-      __syncthreads();
-      if (wave >= 2 || !tile_ok) return;
+      return;
+    }
+#pragma unroll
+    for (int x = 0; x < kDirectTiles; ++x) {
+      if (!tile_ok[x]) continue;
 #pragma unroll
       for (int sb = 0; sb < kNs; ++sb) {
         const int slot = s_slot[16 * sb + col];
         if (slot < 0) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const f32x4_t u = *xch(wave, j, sb);
-          const f32x4_t gsum = acc[j][sb];
-          uint16_t hv[4];
+          const int64_t n = int64_t(tiles[x]) * 64 + 16 * j + 4 * q;
+          const f32x4_t v = acc[x][j][sb];
+          if constexpr (kMode == kPartial) {
+            *reinterpret_cast<f32x4_t*>(g.part + (int64_t(ks) * g.n_slots + slot) * g.N + n) = v;
+          } else {
+            float y[4] = {v[0], v[1], v[2], v[3]};
+            if constexpr (kMode == kTopk) {
+              const float w = round_act<kBF16>(g.topk_w[slot]);
 #pragma unroll
-          for (int x = 0; x < 4; ++x) {
-            const float gv = fminf(round_act<kBF16>(gsum[x]), g.limit);
-            const float uv = fmaxf(fminf(round_act<kBF16>(u[x]), g.limit), -g.limit);
-            const float sl = round_act<kBF16>(gv / (1.0f + expf(-gv)));
-            hv[x] = to_act<kBF16>(sl * uv);
+              for (int u = 0; u < 4; ++u) y[u] = round_act<kBF16>(y[u]) * w;  // exact product
+            }
+            const u32x2_t packed = {uint32_t(to_act<kBF16>(y[0])) | (uint32_t(to_act<kBF16>(y[1])) << 16),
+                                    uint32_t(to_act<kBF16>(y[2])) | (uint32_t(to_act<kBF16>(y[3])) << 16)};
+            *reinterpret_cast<u32x2_t*>(g.out + int64_t(slot) * g.out_stride + n) = packed;
           }
-          // columns n .. n + 3 (n = 4q mod 8 inside their 32-k step): two
-          // adjacent pairs in the permuted layout
-          const int n = tile * 64 + 16 * j + 4 * q;
-          uint16_t* row = g.out + int64_t(slot) * g.out_stride;
-          *reinterpret_cast<uint32_t*>(row + permuted_k(n)) = uint32_t(hv[0]) | (uint32_t(hv[1]) << 16);
-          *reinterpret_cast<uint32_t*>(row + permuted_k(n + 2)) = uint32_t(hv[2]) | (uint32_t(hv[3]) << 16);
-        }
-      }
-      return;
-    }
-    if (!tile_ok) return;
-#pragma unroll
-    for (int sb = 0; sb < kNs; ++sb) {
-      const int slot = s_slot[16 * sb + col];
-      if (slot < 0) continue;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t n = int64_t(tile) * 64 + 16 * j + 4 * q;
-        const f32x4_t v = acc[j][sb];
-        if constexpr (kMode == kPartial) {
-          *reinterpret_cast<f32x4_t*>(g.part + (int64_t(ks) * g.n_slots + slot) * g.N + n) = v;
-        } else {
-          float x[4] = {v[0], v[1], v[2], v[3]};
-          if constexpr (kMode == kTopk) {
-            const float w = round_act<kBF16>(g.topk_w[slot]);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) x[u] = round_act<kBF16>(x[u]) * w;  // exact product
-          }
-          const u32x2_t packed = {uint32_t(to_act<kBF16>(x[0])) | (uint32_t(to_act<kBF16>(x[1])) << 16),
-                                  uint32_t(to_act<kBF16>(x[2])) | (uint32_t(to_act<kBF16>(x[3])) << 16)};
-          *reinterpret_cast<u32x2_t*>(g.out + int64_t(slot) * g.out_stride + n) = packed;
         }
       }
     }
@@ -948,7 +1041,10 @@ int launch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t
 
 template <bool kBF16, int kSub>
 int launch_direct(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t s) {
-  const unsigned gx = mode == kSwiglu ? unsigned(g.N / 128 / 2) : unsigned((g.N / 64 + 3) / 4);
+  // 4 direct_tiles(mode) tiles per workgroup (kSwiglu: half of them gate
+  // tiles, half the matching up tiles)
+  const int per = 4 * direct_tiles(mode);
+  const unsigned gx = unsigned((g.N / 64 + per - 1) / per);
   const dim3 grid(gx, unsigned(blocks), unsigned(ksplit));
   switch (mode) {
     case kPartial: hipLaunchKernelGGL((marlin_gemm_direct<kBF16, kSub, kPartial>), grid, dim3(kThreads), 0, s, g); break;
