@@ -205,8 +205,9 @@ int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stri
  * marlin_moe_gemm (same arguments, checks and sums, bitwise) on k-permuted
  * activations: a's rows hold, in every 32-k step, element 8q + 2s + t = k
  * 8s + 2q + t (marlin_permute_act); weights stream through LDS and each
- * lane loads its matrix operand directly, with no staging barrier.  Four
- * 64-column tiles per workgroup, ksplit 1 for STORE / TOPK / SWIGLU.  Mode
+ * lane loads its matrix operand directly, with no staging barrier.  Eight
+ * 64-column tiles per workgroup (SWIGLU: two gate tiles and their up
+ * tiles), ksplit 1 for STORE / TOPK / SWIGLU.  Mode
  * SWIGLU (ksplit 1, N % 256 == 0): N = 2 Nh columns of gate | up, out =
  * h[slot] (rows of out_stride elements, out_stride % 32 == 0) in the
  * permuted layout, h = RN(RN(SiLU(min(G, L))) * clamp(U, -L, L)) of the
@@ -275,6 +276,20 @@ int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t num_exp
                          int64_t block_size, const int32_t* expert_map, int32_t* sorted,
                          int64_t sorted_numel, int32_t* expert_ids, int64_t expert_ids_numel,
                          int32_t* ntpp, void* stream);
+
+/*
+ * moe_align_block_size and marlin_permute_act (the same arguments, checks
+ * and results) in one launch: the permutation runs beside the
+ * single-workgroup alignment.  The output rows must be 16-byte aligned
+ * (out_stride % 8 == 0).  No counterpart in the reference: the direct fused
+ * path's first step (align, then the w13 GEMM's k-permuted input).
+ */
+int marlin_moe_align_permute(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
+                             int64_t block_size, const int32_t* expert_map, int32_t* sorted,
+                             int64_t sorted_numel, int32_t* expert_ids, int64_t expert_ids_numel,
+                             int32_t* ntpp, const void* a, int act_dtype, int64_t rows,
+                             int64_t cols, int64_t a_stride, void* out, int64_t out_stride,
+                             void* stream);
 
 #ifdef __cplusplus
 }

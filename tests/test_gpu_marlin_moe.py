@@ -270,6 +270,33 @@ def test_permute_act_layout(mm, device):
     assert np.array_equal(out.view(torch.int16).cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("T,E,topk,bs,K", [(1, 8, 2, 8, 32), (37, 16, 4, 16, 96), (300, 128, 8, 32, 2048)])
+def test_align_permute_matches_separate_calls(mm, device, T, E, topk, bs, K):
+    # one launch (alignment workgroup + permutation workgroups) == the two calls
+    from vllm_mi355x.kernels.marlin_moe import _C
+    import importlib
+    A = importlib.import_module("vllm_mi355x.kernels.moe.align")  # the module, not its align()
+    print(f"align_permute T={T} E={E} topk={topk} bs={bs} K={K}", flush=True)
+    rng = np.random.default_rng(T + E)
+    ids = torch.from_numpy(rng.integers(-1, E + 1, (T, topk), dtype=np.int64).astype(np.int32)).to(device)
+    x = torch.from_numpy(rng.integers(-2 ** 15, 2 ** 15, (T, K), dtype=np.int64).astype(np.int16))
+    x = x.to(device).view(torch.float16)
+    size, blocks = A.align_sizes(ids.numel(), E, bs)
+    got = [torch.full((size,), -7, dtype=torch.int32, device=device),
+           torch.full((blocks,), -7, dtype=torch.int32, device=device),
+           torch.zeros(1, dtype=torch.int32, device=device)]
+    want = [t.clone() for t in got]
+    xp_got = torch.zeros_like(x)
+    xp_want = torch.zeros_like(x)
+    _C.align_permute(ids, E, bs, *got, x, xp_got)
+    A.kernel_moe_align_block_size(ids, E, bs, *want, None, None)
+    _C.permute_act(x, xp_want)
+    torch.cuda.synchronize()
+    for g, w in zip(got, want):
+        assert torch.equal(g, w)
+    assert torch.equal(xp_got.view(torch.int16), xp_want.view(torch.int16))
+
+
 @pytest.mark.parametrize("dtype,limit", [(M.BF16, 10.0), (M.FP16, None), (M.BF16, 0.02)])
 @pytest.mark.parametrize("T,bs", [(1, 8), (5, 16), (33, 32), (40, 8)])
 def test_direct_path_matches_oracle(mm, device, dtype, limit, T, bs):

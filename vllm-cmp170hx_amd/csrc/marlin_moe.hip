@@ -925,7 +925,7 @@ __device__ __forceinline__ int block_inclusive_scan(int v, int* wave_tot) {
 // lands after its expert's rows of earlier rounds and earlier wavefronts
 // (per-wavefront counts in LDS when 16 x experts fit, else the 16 wavefronts
 // take turns at the per-expert cursors).
-__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+__device__ __forceinline__ void align_block(
     const int32_t* ids, int64_t numel, int experts, int bs, const int32_t* expert_map,
     int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp,
     int wave_counts) {
@@ -1024,6 +1024,40 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     }
     if (dest >= 0 && dest < sorted_size) sorted[dest] = int32_t(i);
   }
+}
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+    const int32_t* ids, int64_t numel, int experts, int bs, const int32_t* expert_map,
+    int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp,
+    int wave_counts) {
+  align_block(ids, numel, experts, bs, expert_map, sorted, sorted_size, eids, blocks, ntpp, wave_counts);
+}
+
+// The alignment (workgroup 0) and the activations' k permutation (the other
+// workgroups) in one launch: the two are independent, and the permutation
+// hides under the single-workgroup alignment.  Permutation thread = (row,
+// 32-k step, q): the 16 bytes at permuted positions 8q .. 8q + 7, i.e.
+// k = 8s + 2q + t for s = 0..3, t = 0, 1 (four 4-byte loads, one store).
+__global__ __launch_bounds__(kAlignThreads) void moe_align_permute_kernel(
+    const int32_t* ids, int64_t numel, int experts, int bs, const int32_t* expert_map,
+    int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp,
+    int wave_counts, const uint16_t* a, int64_t a_stride, int64_t rows, int cols, uint16_t* out,
+    int64_t out_stride) {
+  if (blockIdx.x == 0) {
+    align_block(ids, numel, experts, bs, expert_map, sorted, sorted_size, eids, blocks, ntpp, wave_counts);
+    return;
+  }
+  const int64_t i = int64_t(blockIdx.x - 1) * kAlignThreads + threadIdx.x;
+  const int64_t per_row = int64_t(cols) / 8;
+  if (i >= rows * per_row) return;
+  const int64_t r = i / per_row;
+  const int c = int(i - r * per_row);  // 8-half chunk of the row: step c / 4, q = c % 4
+  const int base = (c >> 2) * 32 + 2 * (c & 3);
+  const uint16_t* src = a + r * a_stride + base;
+  u32x4_t v;
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) v[s4] = *reinterpret_cast<const uint32_t*>(src + 8 * s4);
+  *reinterpret_cast<u32x4_t*>(out + r * out_stride + 8 * int64_t(c)) = v;
 }
 
 // ---- host ----------------------------------------------------------------------------
@@ -1309,11 +1343,14 @@ extern "C" int moe_sum(const void* in, int act_dtype, int64_t tokens, int64_t to
   return check_launch("moe_sum");
 }
 
-extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
-                                    int64_t block_size, const int32_t* expert_map, int32_t* sorted,
-                                    int64_t sorted_numel, int32_t* expert_ids, int64_t expert_ids_numel,
-                                    int32_t* ntpp, void* stream) {
-  using namespace vq;
+namespace marlin {
+namespace {
+
+// moe_align_block_size's argument checks; `lds` and `wave_counts` configure
+// the alignment workgroup.
+int align_checks(int64_t numel, int64_t num_experts, int64_t block_size, int64_t sorted_numel,
+                 int64_t expert_ids_numel, int& wave_counts, size_t& lds) {
+  using vq::fail;
   if (numel < 0 || numel > INT_MAX || block_size <= 0 || block_size > 1024) {
     return fail("align: numel and block size out of range");
   }
@@ -1323,12 +1360,62 @@ extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int6
   const int64_t need = numel < num_experts ? std::min(numel * block_size, worst) : worst;
   if (sorted_numel < need) return fail("align: sorted_token_ids is smaller than numel + E (bs - 1)");
   if (expert_ids_numel * block_size < need) return fail("align: expert_ids too small");
-  const hipStream_t s = static_cast<hipStream_t>(stream);
   // per-wavefront counts when they fit in 64 KB of LDS with the rest
-  const int wave_counts = num_experts <= 960 ? 1 : 0;
-  const size_t lds = size_t(2 + (wave_counts ? 16 : 0)) * size_t(num_experts) * sizeof(int);
+  wave_counts = num_experts <= 960 ? 1 : 0;
+  lds = size_t(2 + (wave_counts ? 16 : 0)) * size_t(num_experts) * sizeof(int);
+  return vq::kOk;
+}
+
+}  // namespace
+}  // namespace marlin
+
+extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
+                                    int64_t block_size, const int32_t* expert_map, int32_t* sorted,
+                                    int64_t sorted_numel, int32_t* expert_ids, int64_t expert_ids_numel,
+                                    int32_t* ntpp, void* stream) {
+  using namespace vq;
+  int wave_counts = 0;
+  size_t lds = 0;
+  if (int rc = marlin::align_checks(numel, num_experts, block_size, sorted_numel, expert_ids_numel,
+                                    wave_counts, lds)) {
+    return rc;
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(marlin::moe_align_kernel, dim3(1), dim3(marlin::kAlignThreads), lds, s, topk_ids,
                      numel, int(num_experts), int(block_size), expert_map, sorted, sorted_numel,
                      expert_ids, expert_ids_numel, ntpp, wave_counts);
   return check_launch("moe_align_block_size");
+}
+
+extern "C" int marlin_moe_align_permute(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
+                                        int64_t block_size, const int32_t* expert_map, int32_t* sorted,
+                                        int64_t sorted_numel, int32_t* expert_ids,
+                                        int64_t expert_ids_numel, int32_t* ntpp, const void* a,
+                                        int act_dtype, int64_t rows, int64_t cols, int64_t a_stride,
+                                        void* out, int64_t out_stride, void* stream) {
+  using namespace vq;
+  int wave_counts = 0;
+  size_t lds = 0;
+  if (int rc = marlin::align_checks(numel, num_experts, block_size, sorted_numel, expert_ids_numel,
+                                    wave_counts, lds)) {
+    return rc;
+  }
+  if (act_dtype != kBF16 && act_dtype != kFP16) return fail("a: bf16 or fp16 activations");
+  if (rows < 0 || cols <= 0 || cols % 32 != 0 || cols > INT_MAX) return fail("permute: cols % 32");
+  if (a_stride < cols || out_stride < cols || a_stride % 2 != 0 || out_stride % 8 != 0) {
+    return fail("permute: row strides of at least cols (even; output a multiple of 8)");
+  }
+  if ((reinterpret_cast<uintptr_t>(a) & 3) != 0 || (reinterpret_cast<uintptr_t>(out) & 15) != 0) {
+    return fail("permute: 4-byte aligned input and 16-byte aligned output rows");
+  }
+  const int64_t chunks = rows * (cols / 8);
+  const int64_t permute_groups = (chunks + marlin::kAlignThreads - 1) / marlin::kAlignThreads;
+  if (permute_groups + 1 > INT_MAX) return fail("permute: too many rows");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(marlin::moe_align_permute_kernel, dim3(unsigned(1 + permute_groups)),
+                     dim3(marlin::kAlignThreads), lds, s, topk_ids, numel, int(num_experts),
+                     int(block_size), expert_map, sorted, sorted_numel, expert_ids, expert_ids_numel, ntpp,
+                     wave_counts, static_cast<const uint16_t*>(a), a_stride, rows, int(cols),
+                     static_cast<uint16_t*>(out), out_stride);
+  return check_launch("marlin_moe_align_permute");
 }

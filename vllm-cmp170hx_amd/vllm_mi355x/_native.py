@@ -69,6 +69,12 @@ SIGNATURES = {
         c_vp,                                 # stream
     ]),
     "marlin_permute_act": (c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp]),
+    "marlin_moe_align_permute": (c_int, [
+        c_vp, c_i64, c_i64, c_i64, c_vp,      # topk_ids, numel, num_experts, block_size, expert_map
+        c_vp, c_i64, c_vp, c_i64, c_vp,       # sorted, numel, expert_ids, numel, ntpp
+        c_vp, c_int, c_i64, c_i64, c_i64,     # a, act_dtype, rows, cols, a_stride
+        c_vp, c_i64, c_vp,                    # out, out_stride, stream
+    ]),
     "marlin_moe_act": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, ctypes.c_float, c_vp, c_int,
                                c_vp]),
     "marlin_dequant": (c_int, [c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_vp]),

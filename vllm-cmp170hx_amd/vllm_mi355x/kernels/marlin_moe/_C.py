@@ -156,6 +156,27 @@ def permute_act(a, out) -> None:
     _native.check(status)
 
 
+def align_permute(topk_ids, num_experts, block_size, sorted_ids, expert_ids, ntpp, a, out) -> None:
+    """marlin_moe_align_permute: the deterministic alignment of topk_ids and
+    permute_act(a, out) in one launch."""
+    _require(topk_ids.dtype == torch.int32 and topk_ids.is_contiguous(), "topk_ids: int32")
+    for t, name in ((sorted_ids, "sorted_ids"), (expert_ids, "expert_ids"), (ntpp, "ntpp")):
+        _require(t.dtype == torch.int32 and t.is_contiguous(), f"{name}: contiguous int32")
+        _on(t, topk_ids.device, name)
+    _require(a.dtype in _DTYPE_CODES and out.dtype == a.dtype and a.dim() == 2 and out.dim() == 2
+             and a.stride(1) == 1 and out.stride(1) == 1 and out.shape == a.shape,
+             "a, out: same shape and dtype, unit inner stride")
+    _on(a, topk_ids.device, "a")
+    _on(out, topk_ids.device, "out")
+    with torch.cuda.device(a.device):
+        status = _native.load().marlin_moe_align_permute(
+            topk_ids.data_ptr(), topk_ids.numel(), int(num_experts), int(block_size), None,
+            sorted_ids.data_ptr(), sorted_ids.numel(), expert_ids.data_ptr(), expert_ids.numel(),
+            ntpp.data_ptr(), a.data_ptr(), _DTYPE_CODES[a.dtype], a.size(0), a.size(1), a.stride(0),
+            out.data_ptr(), out.stride(0), _stream(a.device))
+    _native.check(status)
+
+
 def act(part, ids, ksplit, n_slots, nh, limit, h) -> None:
     """marlin_moe_act on torch tensors."""
     _require(part.dtype == torch.float32 and part.is_contiguous(), "part: fp32")

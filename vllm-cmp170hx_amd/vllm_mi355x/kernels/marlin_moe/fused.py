@@ -157,17 +157,19 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
             t = torch.empty(numel, dtype=dtype, device=hidden_states.device)
             ws[name] = t
         buf[name] = t.view(-1)[:numel].view(shape)
-    kernel_moe_align_block_size(local, E, bs, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
-                                None)
     tw = topk_weights.to(torch.float32).contiguous().view(-1)
     if direct:
-        _C.permute_act(hidden_states, buf["xp"])
+        # the alignment and the w13 GEMM's k-permuted input in one launch
+        _C.align_permute(local, E, bs, buf["sorted"], buf["expert_ids"], buf["ntpp"], hidden_states,
+                         buf["xp"])
         _C.gemm_direct(buf["xp"], w1, w1_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
                        topk, slots, K, 2 * N, bs, _C.MODE_SWIGLU, 1, limit, out=buf["h"])
         _C.gemm_direct(buf["h"], w2, w2_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], tw, 1,
                        slots, N, K, bs, _C.MODE_TOPK, 1, out=buf["c3"])
         moe_sum(buf["c3"].view(M, topk, K), out, local, E)
         return out
+    kernel_moe_align_block_size(local, E, bs, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
+                                None)
     _C.gemm(hidden_states, w1, w1_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
             topk, slots, K, 2 * N, bs, _C.MODE_PARTIAL, ks, part=buf["part"])
     _C.act(buf["part"], local.view(-1), ks, slots, N, limit, buf["h"])
