@@ -127,4 +127,20 @@ __device__ __forceinline__ void h128_wave(float& v0, float& v1, int lane) {
   v1 = hi * kH128Scale;
 }
 
+// s_waitcnt with only vmcnt <= n (the other counters unconstrained), and a
+// compiler barrier: LDS reads of data an LDS-DMA load wrote must not move
+// above it.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt lgkmcnt(0) only: every LDS read issued so far has returned.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace vq

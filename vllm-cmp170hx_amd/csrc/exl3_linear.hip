@@ -272,21 +272,8 @@ __device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int 
   }
 }
 
-// s_waitcnt with only vmcnt <= n (the other counters unconstrained), and a
-// compiler barrier: LDS reads of data an LDS-DMA load wrote must not move
-// above it.
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(n >= 0 && n < 64, "vmcnt is six bits");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-  asm volatile("" ::: "memory");
-}
-
-// s_waitcnt lgkmcnt(0) only: every LDS read issued so far has returned.
-__device__ __forceinline__ void wait_lgkmcnt0() {
-  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
-  asm volatile("" ::: "memory");
-}
+using vq::wait_lgkmcnt0;
+using vq::wait_vmcnt;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 

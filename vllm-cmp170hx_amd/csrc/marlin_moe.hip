@@ -483,7 +483,10 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 template <int kMode>
 struct DirectShape {
   static constexpr int kTiles = kMode == kSwiglu ? 1 : 2;
-  static constexpr int kSlots = kMode == kSwiglu ? 4 : 2;
+  static constexpr int kSlots = 2;
+  // kSwiglu: the B operands go through LDS too (all four wavefronts read the
+  // same rows): two group slots
+  static constexpr bool kLdsB = kMode == kSwiglu;
 };
 inline int direct_tiles(int mode) { return mode == kSwiglu ? DirectShape<kSwiglu>::kTiles : DirectShape<kTopk>::kTiles; }
 // The kernel's per-tile arrays have this fixed size (loops run to the mode's
@@ -501,6 +504,15 @@ __global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direc
   __shared__ __attribute__((aligned(16))) u32x4_t ring1[kSlotVecs];
   __shared__ __attribute__((aligned(16))) u32x4_t ring2[kSlots > 2 ? kSlotVecs : 4];
   __shared__ __attribute__((aligned(16))) u32x4_t ring3[kSlots > 2 ? kSlotVecs : 4];
+  // B slot = [row / 4][row % 4][16-byte chunk ^ (row % 16)] of 16 bytes: one
+  // group (128 k) of the block's rows (the chunk swizzle keeps the 16 rows a
+  // B-operand read touches on distinct banks), then per wavefront 256 bytes:
+  // its tile's group scales (128 bytes) and zeros
+  constexpr bool kLdsB = DirectShape<kMode>::kLdsB;
+  constexpr int kBRowVecs = kSub * 16 * 16;
+  constexpr int kBVecs = kLdsB ? kBRowVecs + 4 * 16 : 4;
+  __shared__ __attribute__((aligned(16))) u32x4_t bring0[kBVecs];
+  __shared__ __attribute__((aligned(16))) u32x4_t bring1[kBVecs];
   __shared__ int s_slot[kMaxBlock];
 
   const int tid = threadIdx.x;
@@ -605,6 +617,87 @@ __global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direc
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int sb = 0; sb < kNs; ++sb) acc[x][j][sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (kLdsB) {
+      // The block's B operands of group i go to B slot i % 2 in 4 kNs
+      // loads of four rows (1 KB) each, kNs per wavefront: lane l fetches row
+      // 4d + l / 16, chunk (l % 16) ^ (row % 16).  Group i starts with this
+      // wavefront's own B loads of group i complete, then a workgroup
+      // barrier: every wavefront's loads of group i have landed and every
+      // wavefront is done with group i - 1, whose B slot group i + 1 reuses.
+      uint32_t brow[kNs];
+#pragma unroll
+      for (int j = 0; j < kNs; ++j) {
+        const int row = 4 * (wave * kNs + j) + (lane >> 4);
+        const int slot = s_slot[row];
+        const int chunk = (lane & 15) ^ (row & 15);
+        brow[j] = slot >= 0 ? uint32_t((int64_t(slot / g.top_k) * g.a_stride + 8 * chunk) * 2) : 0x80000000u;
+      }
+      // the scales go through LDS as well (dword loads, lanes 0-31; the others
+      // fall past the buffer): a VGPR load here would be the loop's only one,
+      // and the compiler, which does not count the LDS loads issued after it,
+      // would wait for every load in flight before its first use
+      const uint32_t sdw = lane < 32 ? uint32_t(tile_ok[0] ? tiles[0] : 0) * 128u + 4u * uint32_t(lane) : 0x80000000u;
+      auto load_bgroup = [&](int k, int i) {
+        u32x4_t* slot = k == 0 ? bring0 : bring1;
+#pragma unroll
+        for (int j = 0; j < kNs; ++j) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(abuf, (lds_ptr_t)(slot + (wave * kNs + j) * 64), 16, brow[j],
+                                                   int(uint32_t(g0 + i) * 256u), 0, 0);
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(sbuf, (lds_ptr_t)(slot + kBRowVecs + wave * 16), 4, sdw,
+                                                 int(uint32_t(i) * uint32_t(g.N) * 2u), 0, 0);
+      };
+      // this lane's B operand of step st, sub-block sb in a B slot
+      auto bread = [&](int k, int st, int sb) {
+        const int row = 16 * sb + col;
+        const int chunk = 4 * st + q;
+        return (k == 0 ? bring0 : bring1)[(row >> 2) * 64 + (row & 3) * 16 + (chunk ^ (row & 15))];
+      };
+      // per group i: [wait own B(i), barrier] [B(i + 1)] [weights of half 1,
+      // scales of i + 1] steps 0, 1 [weights of i + 1's half 0] steps 2, 3
+      load_bgroup(0, 0);
+      load_half(0, 0, 0);
+      for (int i0 = 0; i0 < gps; i0 += 2) {
+#pragma unroll
+        for (int gi = 0; gi < 2; ++gi) {
+          const int i = i0 + gi;
+          const bool live = i < gps;
+          // only the two weight loads of this group's half 0 in flight: B(i)
+          // and the scales of i have landed
+          vq::wait_vmcnt<2>();
+          __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+          Scales<kBF16> sc;
+          sc.set((gi == 0 ? bring0 : bring1)[kBRowVecs + wave * 16 + (lane & 7)], lane);
+          load_bgroup(gi ^ 1, i + 1);
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            if (half == 0) {
+              load_half(1, i, 1);
+            } else {
+              load_half(0, i + 1, 0);
+            }
+            asm volatile("" ::: "memory");
+            if (live) {
+#pragma unroll
+              for (int sl = 0; sl < 2; ++sl) {
+                const int st = 2 * half + sl;
+                u32x4_t bop[kNs];
+#pragma unroll
+                for (int sb = 0; sb < kNs; ++sb) bop[sb] = bread(gi, st, sb);
+                const u32x4_t v = slot_base(half)[sl * 64 + lane];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                  const u32x4_t a = sc.operand(combine(v[j], lane), j, masks);
+#pragma unroll
+                  for (int sb = 0; sb < kNs; ++sb) acc[0][j][sb] = mfma<kBF16>(a, bop[sb], acc[0][j][sb]);
+                }
+              }
+            }
+          }
+        }
+      }
+    } else {
     // B operands of the current group's steps; step st of the next group is
     // loaded into breg[st] as soon as step st of this one has been read
     u32x4_t breg[4][kNs];
@@ -671,6 +764,8 @@ __global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direc
         }
       }
     }
+
+    }  // kLdsB
 
     if constexpr (kMode == kSwiglu) {
       // up wavefronts 2, 3 hand their sums to gate wavefronts 0, 1 through
