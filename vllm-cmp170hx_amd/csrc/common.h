@@ -143,4 +143,28 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
   asm volatile("" ::: "memory");
 }
 
+// LDS accesses outside the compiler's tracking of LDS-DMA loads (buffer
+// loads into LDS, counted by vmcnt): the compiler waits for every such load
+// in flight before an LDS access it cannot prove disjoint from them.  The
+// caller guarantees the address is not the destination of a DMA load in
+// flight, and orders the access itself (lgkmcnt waits before a barrier).
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+__device__ __forceinline__ void lds_store_b16(uint32_t address, uint32_t v) {
+  asm volatile("ds_write_b16 %0, %1" ::"v"(address), "v"(v) : "memory");
+}
+
+__device__ __forceinline__ void lds_store_b32(uint32_t address, uint32_t v) {
+  asm volatile("ds_write_b32 %0, %1" ::"v"(address), "v"(v) : "memory");
+}
+
+// Read and wait for it.
+__device__ __forceinline__ uint32_t lds_load_b32(uint32_t address) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(address) : "memory");
+  return v;
+}
+
 }  // namespace vq

@@ -317,7 +317,10 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
   // for its row sums.
   constexpr int kActAll = kGroups * kActHalves;
   __shared__ __attribute__((aligned(16))) _Float16 act[kActAll > 2 * 128 * kRows * 2 ? kActAll : 2 * 128 * kRows * 2];
-  __shared__ int block_exp[kGroups][kBlocks][kRows];
+  // per (block, row) maxima of the formed activations: a group scales its
+  // rows by one power of two across its blocks, so the MFMA sums run over the
+  // whole range and fold once
+  __shared__ uint32_t block_max[kGroups][kBlocks][kRows];
   // LDS stream: kRingLoads slots of 1 KB (kP steps) per wavefront, one
   // array per slot: the compiler's wait for an LDS-DMA load before a read
   // of its data then names that load, not every load in flight.
@@ -457,11 +460,41 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  // c. forming: t = H128(x * suh) of a (block, row), split at a power-of-two
-  //    scale into FP16 high / low parts, written straight into B-operand
-  //    order: act = [step][g][B column 2r + (0 hi | 1 lo)][8 halves].
-  {
-    // half index of input k (within a block) at B column 0
+  // c. forming: t = H128(x * suh) of a (block, row) and its maximum |t|,
+  //    published in LDS; after the first barrier (in the stream loop) each
+  //    row's t is split at the group's power-of-two scale of that row into
+  //    FP16 high / low parts, written straight into B-operand order:
+  //    act = [step][g][B column 2r + (0 hi | 1 lo)][8 halves].  The LDS
+  //    stores bypass the compiler's LDS-DMA tracking (they never touch a
+  //    ring slot), so they do not wait for the trellis loads in flight.
+  float fv[kFormTasks][2];
+#pragma unroll
+  for (int f = 0; f < kFormTasks; ++f) {
+    const int t = wc + 4 * f;
+    fv[f][0] = fv[f][1] = 0.0f;
+    if (t < kTasks) {
+      float v0 = u16_act(uint16_t(xv[f][0]), a.x_dtype) * vq::f16_to_f32(uint16_t(sv[f][0]));
+      float v1 = u16_act(uint16_t(xv[f][1]), a.x_dtype) * vq::f16_to_f32(uint16_t(sv[f][1]));
+      vq::h128_wave(v0, v1, lane);
+      const float mx = vq::wave_max(fmaxf(fabsf(v0), fabsf(v1)), lane);
+      if (lane == 0) vq::lds_store_b32(vq::lds_address(&block_max[grp][t / kRows][t % kRows]),
+                                        __builtin_bit_cast(uint32_t, mx));
+      fv[f][0] = v0;
+      fv[f][1] = v1;
+    }
+  }
+  // scale exponent of row r of this group (maxima complete)
+  auto row_exponent = [&](int r) {
+    uint32_t mx = 0u;
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+      // nonnegative floats order as their bit patterns
+      const uint32_t v = vq::lds_load_b32(vq::lds_address(&block_max[grp][b][r]));
+      mx = v > mx ? v : mx;
+    }
+    return scale_exponent(mx);
+  };
+  auto split_store = [&]() {
     auto slot_of = [&](int k) {
       const int step = k >> 5;
       const int w = k & 31;
@@ -470,38 +503,34 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
       const int slot = 4 * (w >> 4) + (kk & 1) + 2 * (kk >> 3);
       return ((step * 4 + gg) * kCols) * 8 + slot;
     };
+    const uint32_t gact = vq::lds_address(act + grp * kActHalves);
     const int h0 = slot_of(lane);
     const int h1 = slot_of(lane + 64);
-    _Float16* gact = act + grp * kActHalves;
 #pragma unroll
     for (int f = 0; f < kFormTasks; ++f) {
       const int t = wc + 4 * f;
       const int b = t / kRows;
       const int r = t % kRows;
       if (t < kTasks) {
-        float v0 = u16_act(uint16_t(xv[f][0]), a.x_dtype) * vq::f16_to_f32(uint16_t(sv[f][0]));
-        float v1 = u16_act(uint16_t(xv[f][1]), a.x_dtype) * vq::f16_to_f32(uint16_t(sv[f][1]));
-        vq::h128_wave(v0, v1, lane);
-        const float mx = vq::wave_max(fmaxf(fabsf(v0), fabsf(v1)), lane);
-        const int e = scale_exponent(__builtin_bit_cast(uint32_t, mx));
-        if (lane == 0) block_exp[grp][b][r] = e;
-        const float t0 = ldexpf(v0, e);
-        const float t1 = ldexpf(v1, e);
+        const int e = row_exponent(r);
+        const float t0 = ldexpf(fv[f][0], e);
+        const float t1 = ldexpf(fv[f][1], e);
         const _Float16 hi0 = _Float16(t0), hi1 = _Float16(t1);
-        const int base = b * 4 * 4 * kCols * 8 + (2 * r) * 8;
-        gact[base + h0] = hi0;
-        gact[base + h0 + 8] = _Float16(t0 - float(hi0));
-        gact[base + h1] = hi1;
-        gact[base + h1 + 8] = _Float16(t1 - float(hi1));
+        const _Float16 lo0 = _Float16(t0 - float(hi0)), lo1 = _Float16(t1 - float(hi1));
+        const uint32_t base = gact + 2 * uint32_t(b * 4 * 4 * kCols * 8 + (2 * r) * 8);
+        vq::lds_store_b16(base + 2 * h0, __builtin_bit_cast(uint16_t, hi0));
+        vq::lds_store_b16(base + 2 * (h0 + 8), __builtin_bit_cast(uint16_t, lo0));
+        vq::lds_store_b16(base + 2 * h1, __builtin_bit_cast(uint16_t, hi1));
+        vq::lds_store_b16(base + 2 * (h1 + 8), __builtin_bit_cast(uint16_t, lo1));
       }
     }
-  }
+  };
 
-  // d. stream: decode step j while later steps are in flight.  Each block's
-  //    products accumulate in acc1/acc2 from zero and are folded, unscaled,
-  //    into tot1/tot2 (high + low parts: B columns 2r, 2r + 1 sit in
-  //    adjacent lanes) at the block's end, blocks in order.  Lanes m >= kCols
-  //    read B column m % kCols again: their MFMA columns are never used.
+  // d. stream: decode step j while later steps are in flight.  The products
+  //    of the whole range accumulate in acc1/acc2 (one scale per row), and
+  //    are folded, unscaled, into tot1/tot2 at the end (high + low parts:
+  //    B columns 2r, 2r + 1 sit in adjacent lanes).  Lanes m >= kCols read
+  //    B column m % kCols again: their MFMA columns are never used.
   uint32_t wv[kLds ? 1 : kSteps][2][G::kWords];
   auto gather = [&](int j) {
 #pragma unroll
@@ -518,8 +547,7 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
   const half8_t* bops = reinterpret_cast<const half8_t*>(act + grp * kActHalves) + g * kCols + (m % kCols);
   const int r_own = (m >> 1) < kRows ? (m >> 1) : 0;
   f32x4_t acc1 = {}, acc2 = {};
-  float tot1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  float tot2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float tot1[4], tot2[4];
   half8_t bop = {};
   if constexpr (!kLds) gather(0);
 #pragma unroll
@@ -563,18 +591,23 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
     uint32_t q0[4], q1[4];
     decode_words<kBitsX2, kCodebook>(L, w0, q0);
     decode_words<kBitsX2, kCodebook>(L, w1, q1);
-    // the activations are complete once every wavefront is past here (the
-    // first decode overlaps the wait).  LDS stream: a bare s_barrier after
-    // this wavefront's LDS writes; __syncthreads would also wait for every
-    // trellis load in flight.
+    // the activation maxima, then the B operands, are complete once every
+    // wavefront is past a barrier (the first decode overlaps the wait).  LDS
+    // stream: bare s_barriers after this wavefront's LDS writes;
+    // __syncthreads would also wait for every trellis load in flight.
     if (j == 0) {
-      if constexpr (kLds) {
-        wait_lgkmcnt0();
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-      } else {
-        __syncthreads();
-      }
+      auto barrier = [&]() {
+        if constexpr (kLds) {
+          wait_lgkmcnt0();
+          __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+        } else {
+          __syncthreads();
+        }
+      };
+      if constexpr (kBlocks > 1) barrier();
+      split_store();
+      barrier();
     }
     const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
     const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
@@ -584,19 +617,8 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
       asm volatile("" ::: "memory");
       bop = bops[j * 4 * kCols];
     }
-    const f32x4_t zero = {};
-    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), bop,
-                                                  (j & 3) == 0 ? zero : acc1, 0, 0, 0);
-    acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), bop,
-                                                  (j & 3) == 0 ? zero : acc2, 0, 0, 0);
-    if ((j & 3) == 3) {
-      const int e = block_exp[grp][j >> 2][r_own];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        tot1[i] += ldexpf(acc1[i] + vq::xor_lanes<1>(acc1[i], lane), -e);
-        tot2[i] += ldexpf(acc2[i] + vq::xor_lanes<1>(acc2[i], lane), -e);
-      }
-    }
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), bop, acc1, 0, 0, 0);
+    acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), bop, acc2, 0, 0, 0);
     // LDS stream: the slot's last step was read (its reads returned during
     // the decode): refill it with load i + kRingLoads
     if constexpr (kLds) {
@@ -604,6 +626,15 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
         wait_lgkmcnt0();
         load_lds(j / kP + kRingLoads);
       }
+    }
+  }
+
+  {
+    const int e = row_exponent(r_own);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      tot1[i] = ldexpf(acc1[i] + vq::xor_lanes<1>(acc1[i], lane), -e);
+      tot2[i] = ldexpf(acc2[i] + vq::xor_lanes<1>(acc2[i], lane), -e);
     }
   }
 
