@@ -37,7 +37,12 @@ namespace {
 
 constexpr int kRouteThreads = 1024;
 constexpr int64_t kMaxRouteExperts = 4096;
-constexpr int kTaskRows = 8;
+// Rows of one expert per GEMV task: every decoded weight operand feeds the
+// MFMAs of up to four 8-row sub-blocks, so a fixed-rate expert's weights
+// are decoded once per 32 of its rows.  The run-time-format decode needs the
+// registers the extra accumulators would take: 8 rows there.
+constexpr int kTaskRows = 32;
+constexpr int task_rows(int bits_x2) { return bits_x2 > 0 ? kTaskRows : 8; }
 
 // Routing of one call (reference: csrc/exl3/moe.cu:19-55).
 struct Routing {
@@ -86,7 +91,7 @@ struct MoeLayout {
 // ---- 1. route ------------------------------------------------------------------
 
 __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int64_t assignments,
-                                                           int* table) {
+                                                           int task_rows, int* table) {
   extern __shared__ int route_shared[];
   const int experts = int(routing.local_experts);
   int* count = route_shared;               // counts, then fill cursors
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
   int rows = 0, tasks = 0;
   for (int e = e0; e < e1; ++e) {
     rows += count[e];
-    tasks += (count[e] + kTaskRows - 1) / kTaskRows;
+    tasks += (count[e] + task_rows - 1) / task_rows;
   }
   scan_rows[tid] = rows;
   scan_tasks[tid] = tasks;
@@ -130,7 +135,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
     task_begin[e] = task_at;
     count[e] = row_at;  // fill cursor
     row_at += c;
-    task_at += (c + kTaskRows - 1) / kTaskRows;
+    task_at += (c + task_rows - 1) / task_rows;
   }
   const int total_rows = scan_rows[kRouteThreads - 1];
   const int total_tasks = scan_tasks[kRouteThreads - 1];
@@ -149,9 +154,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
       const int mid = (lo + hi) >> 1;
       if (task_begin[mid] <= t) lo = mid; else hi = mid;
     }
-    const int first = row_begin[lo] + (t - task_begin[lo]) * kTaskRows;
+    const int first = row_begin[lo] + (t - task_begin[lo]) * task_rows;
     const int end = lo + 1 < experts ? row_begin[lo + 1] : total_rows;
-    task_table[t] = make_int4(lo, first, min(kTaskRows, end - first), 0);
+    task_table[t] = make_int4(lo, first, min(task_rows, end - first), 0);
   }
   int* sorted = table + 4;
   for (int64_t a = tid; a < assignments; a += kRouteThreads) {
@@ -173,13 +178,9 @@ __device__ __forceinline__ int64_t b_order(int64_t k) {
 }
 
 // Writes one 128-input block of t (lane l holds inputs l, l + 64), scaled by
-// the block's power-of-two exponent, into an assignment's B-operand arrays.
+// the assignment's power-of-two exponent, into its B-operand arrays.
 __device__ __forceinline__ void store_block(_Float16* dst, int64_t kp, int64_t block, float v0,
-                                            float v1, int* exp_slot, int lane) {
-  float mx = fmaxf(fabsf(v0), fabsf(v1));
-  mx = vq::wave_max(mx, lane);
-  const int e = scale_exponent(__builtin_bit_cast(uint32_t, mx));
-  if (lane == 0) *exp_slot = e;
+                                            float v1, int e, int lane) {
   const float t0 = ldexpf(v0, e);
   const float t1 = ldexpf(v1, e);
   const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
@@ -193,68 +194,87 @@ __device__ __forceinline__ void store_block(_Float16* dst, int64_t kp, int64_t b
 // kActivate false: gate/up input, t = H128(x[a / topk] * suh_projection);
 // true: down input from the gate/up results (already H128 * svh):
 // clamp, SiLU(g) * u * suh_down, H128, into the act region.
-// One wavefront per (local assignment, 128-input block).  An expert whose
-// matrix is not kp rows long gets NaN operands (its suh is not read).
+// One workgroup per local assignment: pass 1 forms every 128-input block
+// (wavefront w takes blocks w, w + 4, ...) for the row maximum of |t|; pass 2
+// forms them again (the same operations, so the same values) and writes the
+// high / low parts at the row's one power-of-two scale, so the expert GEMV
+// sums the whole row before it unscales.  An expert whose matrix is not kp
+// rows long gets NaN operands (its suh is not read).
 template <bool kActivate>
 __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, int x_dtype,
                                                 int64_t hidden, int64_t intermediate, int projection,
                                                 const int* table, float* ws, MoeLayout lay,
                                                 float limit) {
+  __shared__ uint32_t row_max;
   const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int64_t kp = kActivate ? lay.ipad : lay.hpad;
   const int64_t blocks = kp / 128;
-  const int64_t task = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (task >= int64_t(table[0]) * blocks) return;
-  const int64_t a = table[4 + task / blocks];
-  const int64_t b = task % blocks;
+  if (int64_t(blockIdx.x) >= int64_t(table[0])) return;
+  const int64_t a = table[4 + blockIdx.x];
   const int64_t e = local_expert(routing, a);
   const int64_t* ptrs = routing.ptrs + e * 9;
-  const int64_t k0 = b * 128 + lane;
-  const int64_t k1 = k0 + 64;
-  float v0, v1;
-  _Float16* dst;
   int* exps = reinterpret_cast<int*>(ws + lay.ints()) + lay.exps() + a * (lay.kmax() / 128);
-  if (routing.meta[e * 12 + projection * 4] != kp) {
-    dst = reinterpret_cast<_Float16*>(ws + (kActivate ? lay.act() : lay.input()) + a * kp);
-    store_block(dst, kp, b, __builtin_nanf(""), __builtin_nanf(""), exps + b, lane);
-    return;
-  }
-  if constexpr (!kActivate) {
-    const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[projection * 3 + 1]);
-    const uint16_t* row = static_cast<const uint16_t*>(x) + (a / routing.topk) * hidden;
-    const uint32_t x0 = row[k0 < hidden ? k0 : 0], x1 = row[k1 < hidden ? k1 : 0];
-    const uint32_t s0 = suh[k0 < hidden ? k0 : 0], s1 = suh[k1 < hidden ? k1 : 0];
-    v0 = k0 < hidden ? u16_act(uint16_t(x0), x_dtype) * vq::f16_to_f32(uint16_t(s0)) : 0.0f;
-    v1 = k1 < hidden ? u16_act(uint16_t(x1), x_dtype) * vq::f16_to_f32(uint16_t(s1)) : 0.0f;
-    dst = reinterpret_cast<_Float16*>(ws + lay.input() + a * lay.hpad);
-  } else {
-    const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[projection * 3 + 1]);
-    const float* g = ws + lay.gate() + a * lay.ipad;
-    const float* u = ws + lay.up() + a * lay.ipad;
-    float gv[2] = {g[k0], g[k1]};
-    float uv[2] = {u[k0], u[k1]};
-    const uint32_t sd[2] = {suh[k0 < intermediate ? k0 : 0], suh[k1 < intermediate ? k1 : 0]};
-    float v[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int64_t k = i ? k1 : k0;
-      v[i] = 0.0f;
-      if (k < intermediate) {
-        float gg = gv[i], uu = uv[i];
-        if (limit > 0.0f) {
-          gg = fminf(gg, limit);
-          uu = fminf(fmaxf(uu, -limit), limit);
-        }
-        const float silu = gg / (1.0f + expf(-gg));
-        v[i] = (silu * uu) * vq::f16_to_f32(uint16_t(sd[i]));
-      }
+  _Float16* dst = reinterpret_cast<_Float16*>(ws + (kActivate ? lay.act() : lay.input()) + a * kp);
+  const bool bad = routing.meta[e * 12 + projection * 4] != kp;
+  const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[projection * 3 + 1]);
+  auto form = [&](int64_t b, float& v0, float& v1) {
+    const int64_t k0 = b * 128 + lane;
+    const int64_t k1 = k0 + 64;
+    if (bad) {
+      v0 = v1 = __builtin_nanf("");
+      return;
     }
-    v0 = v[0];
-    v1 = v[1];
-    dst = reinterpret_cast<_Float16*>(ws + lay.act() + a * lay.ipad);
+    if constexpr (!kActivate) {
+      const uint16_t* row = static_cast<const uint16_t*>(x) + (a / routing.topk) * hidden;
+      const uint32_t x0 = row[k0 < hidden ? k0 : 0], x1 = row[k1 < hidden ? k1 : 0];
+      const uint32_t s0 = suh[k0 < hidden ? k0 : 0], s1 = suh[k1 < hidden ? k1 : 0];
+      v0 = k0 < hidden ? u16_act(uint16_t(x0), x_dtype) * vq::f16_to_f32(uint16_t(s0)) : 0.0f;
+      v1 = k1 < hidden ? u16_act(uint16_t(x1), x_dtype) * vq::f16_to_f32(uint16_t(s1)) : 0.0f;
+    } else {
+      const float* g = ws + lay.gate() + a * lay.ipad;
+      const float* u = ws + lay.up() + a * lay.ipad;
+      const float gv[2] = {g[k0], g[k1]};
+      const float uv[2] = {u[k0], u[k1]};
+      const uint32_t sd[2] = {suh[k0 < intermediate ? k0 : 0], suh[k1 < intermediate ? k1 : 0]};
+      float v[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int64_t k = i ? k1 : k0;
+        v[i] = 0.0f;
+        if (k < intermediate) {
+          float gg = gv[i], uu = uv[i];
+          if (limit > 0.0f) {
+            gg = fminf(gg, limit);
+            uu = fminf(fmaxf(uu, -limit), limit);
+          }
+          const float silu = gg / (1.0f + expf(-gg));
+          v[i] = (silu * uu) * vq::f16_to_f32(uint16_t(sd[i]));
+        }
+      }
+      v0 = v[0];
+      v1 = v[1];
+    }
+    vq::h128_wave(v0, v1, lane);
+  };
+  if (threadIdx.x == 0) row_max = 0u;
+  __syncthreads();
+  float mx = 0.0f;
+  for (int64_t b = wave; b < blocks; b += 4) {
+    float v0, v1;
+    form(b, v0, v1);
+    mx = fmaxf(mx, fmaxf(fabsf(v0), fabsf(v1)));
   }
-  vq::h128_wave(v0, v1, lane);
-  store_block(dst, kp, b, v0, v1, exps + b, lane);
+  mx = vq::wave_max(mx, lane);
+  if (lane == 0) atomicMax(&row_max, __builtin_bit_cast(uint32_t, mx));
+  __syncthreads();
+  const int ex = scale_exponent(row_max);
+  if (threadIdx.x == 0) exps[0] = ex;
+  for (int64_t b = wave; b < blocks; b += 4) {
+    float v0, v1;
+    form(b, v0, v1);
+    store_block(dst, kp, b, v0, v1, ex, lane);
+  }
 }
 
 // ---- grouped expert GEMV ----------------------------------------------------------
@@ -303,18 +323,29 @@ struct GemvTask {
 };
 
 // One workgroup = (task, 128 output columns); wavefront w owns the column
-// pair (two tile columns) 4 * blockIdx.x + w over the whole K range.
+// pair (two tile columns) 4 * blockIdx.x + w over the whole K range.  Each
+// decoded step (two tile rows, 16 weights a lane) is an A operand of the
+// MFMAs of every 8-row sub-block of the task (B columns 2r, 2r + 1: row r's
+// high and low parts); the sums run over the whole row (one scale per
+// assignment row) and fold once.
 // kBitsX2 = 0: the expert's format at run time.
 template <int kBitsX2>
-__global__ __launch_bounds__(256) void moe_gemv(Routing routing, int projection, int64_t kp,
+__global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing routing, int projection, int64_t kp,
                                                 int64_t np, const int* table, float* ws,
                                                 MoeLayout lay, int64_t in_offset,
                                                 int64_t out_offset) {
   constexpr bool kFixed = kBitsX2 > 0;
-  constexpr int kDepth = 8;  // steps of trellis loads in flight
-  __shared__ __attribute__((aligned(16))) _Float16 bop[2][4][4][16][8];  // [buf][step][g][col][8]
-  __shared__ int bexp[2][kTaskRows];
-  __shared__ float red[kTaskRows][128];
+  constexpr int kDepth = 6;  // steps of trellis loads in flight
+  constexpr int kRows = task_rows(kBitsX2);
+  constexpr int kSub = kRows / 8;
+  constexpr int kCols = 2 * kRows;
+  constexpr int kChunks = kCols / 16;  // 16-byte B chunks per thread per block
+  // one 128-input block of B operands: [buf][step][g][column][8 halves]
+  // (the epilogue's per-row sums reuse it: kRows x 128 floats)
+  __shared__ __attribute__((aligned(16))) _Float16 bop[2][4][4][kCols][8];
+  __shared__ int rexp[kRows];
+  static_assert(sizeof(bop) >= sizeof(float) * kRows * 128, "row sums fit the B staging");
+  float (*red)[128] = reinterpret_cast<float (*)[128]>(&bop[0][0][0][0][0]);
 
   const int64_t task = blockIdx.y;
   if (task >= table[1]) return;
@@ -322,6 +353,7 @@ __global__ __launch_bounds__(256) void moe_gemv(Routing routing, int projection,
   const int expert = tk.x;
   const int first = tk.y;
   const int nrows = tk.z;
+  const int nsub = (nrows + 7) >> 3;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -360,24 +392,43 @@ __global__ __launch_bounds__(256) void moe_gemv(Routing routing, int projection,
   // the wavefront's two tiles of tile row 0
   const uint8_t* chunk = trellis + 2 * (4 * int64_t(blockIdx.x) + wave) * tile_bytes;
 
-  // B-operand staging: thread t copies 16 bytes (step t >> 6, g, column)
-  const int st_step = tid >> 6;
-  const int st_g = (tid >> 4) & 3;
-  const int st_col = tid & 15;
-  const int st_row = min(st_col >> 1, nrows - 1);
-  const int64_t st_a = sorted[first + st_row];
-  const _Float16* st_src = reinterpret_cast<const _Float16*>(ws + in_offset + st_a * kp) +
-                           (st_col & 1) * kp + st_step * 32 + st_g * 8;
-  const int* exps = reinterpret_cast<const int*>(ws + lay.ints()) + lay.exps();
-  const int64_t exp_stride = lay.kmax() / 128;
-  auto stage = [&](int64_t kb, u32x4_t& v, int& e) {
-    v = *reinterpret_cast<const u32x4_t*>(st_src + kb * 128);
-    e = tid < kTaskRows ? exps[int64_t(sorted[first + min(tid, nrows - 1)]) * exp_stride + kb] : 0;
+  // B-operand staging of a block: chunk c = tid + 256 i (i < kChunks) is 16
+  // bytes (step, g, column) = (c / (4 kCols), c / kCols % 4, c % kCols);
+  // columns of rows past the task read its last row again (their MFMA
+  // columns are never used)
+  //    The B operands are read through a buffer over the input region
+  //    (32-bit byte offsets: the region is A x kp floats, checked on the host).
+  const __amdgpu_buffer_rsrc_t st_buf = __builtin_amdgcn_make_buffer_rsrc(
+      ws + in_offset, 0, int(lay.assignments * kp * 4), 0x00020000);
+  uint32_t st_off[kChunks];
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i) {
+    const int c = tid + 256 * i;
+    const int col = c % kCols;
+    const int64_t a = sorted[first + min(col >> 1, nrows - 1)];
+    st_off[i] = uint32_t((a * 2 * kp + (col & 1) * kp + (c / (4 * kCols)) * 32 + (c / kCols % 4) * 8) * 2);
+  }
+  auto stage = [&](int64_t kb, u32x4_t (&v)[kChunks]) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      v[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(st_buf, int(st_off[i]),
+                                                                               int(kb * 256), 0));
+    }
   };
+  auto put = [&](int buf, const u32x4_t (&v)[kChunks]) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<u32x4_t*>(&bop[buf][c / (4 * kCols)][c / kCols % 4][c % kCols][0]) = v[i];
+    }
+  };
+  if (tid < kRows) {
+    const int* exps = reinterpret_cast<const int*>(ws + lay.ints()) + lay.exps();
+    rexp[tid] = exps[int64_t(sorted[first + min(tid, nrows - 1)]) * (lay.kmax() / 128)];
+  }
 
   // trellis ring (fixed rate: one coalesced dword per lane per tile row, words
   // gathered with ds_bpermute; run-time rate: decoded from the tile directly)
-  using FR = Ring<kFixed ? kBitsX2 : 8>;
   constexpr int kWords = LaneLoad<kFixed ? kBitsX2 : 8>::kWords;
   const int raw_off = lane < 8 * bits_x2 ? 4 * lane : 0;
   int widx[kWords];
@@ -395,23 +446,19 @@ __global__ __launch_bounds__(256) void moe_gemv(Routing routing, int projection,
       }
     }
   };
-  (void)sizeof(FR);
 
-  f32x4_t acc1 = {}, acc2 = {};
-  float tot1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  float tot2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  const int r_own = m >> 1;
+  f32x4_t acc1[kSub], acc2[kSub];
+#pragma unroll
+  for (int sb = 0; sb < kSub; ++sb) acc1[sb] = acc2[sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // prologue: block 0's B operands, the first kDepth steps of trellis
-  u32x4_t sv;
-  int se;
-  stage(0, sv, se);
+  u32x4_t sv[kChunks];
+  stage(0, sv);
 #pragma unroll
   for (int i = 0; i < kDepth; ++i) {
     if (i < steps) load_step(i, i);
   }
-  *reinterpret_cast<u32x4_t*>(&bop[0][st_step][st_g][st_col][0]) = sv;
-  if (tid < kTaskRows) bexp[0][tid] = se;
+  put(0, sv);
   __syncthreads();
 
   for (int64_t s0 = 0; s0 < steps; s0 += kDepth) {
@@ -421,7 +468,7 @@ __global__ __launch_bounds__(256) void moe_gemv(Routing routing, int projection,
       if (s < steps) {
         const int64_t kb = s >> 2;
         const int buf = int(kb & 1);
-        if ((s & 3) == 0 && kb + 1 < kblocks) stage(kb + 1, sv, se);
+        if ((s & 3) == 0 && kb + 1 < kblocks) stage(kb + 1, sv);
         uint32_t q0[4], q1[4];
         if constexpr (kFixed) {
           uint32_t w0[kWords], w1[kWords];
@@ -440,37 +487,40 @@ __global__ __launch_bounds__(256) void moe_gemv(Routing routing, int projection,
         }
         const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
         const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
-        const half8_t b = *reinterpret_cast<const half8_t*>(&bop[buf][s & 3][g][m][0]);
-        const f32x4_t zero = {};
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), b,
-                                                      (s & 3) == 0 ? zero : acc1, 0, 0, 0);
-        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), b,
-                                                      (s & 3) == 0 ? zero : acc2, 0, 0, 0);
-        if ((s & 3) == 3) {
-          const int e = bexp[buf][r_own];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            tot1[k] += ldexpf(acc1[k] + vq::xor_lanes<1>(acc1[k], lane), -e);
-            tot2[k] += ldexpf(acc2[k] + vq::xor_lanes<1>(acc2[k], lane), -e);
+        for (int sb = 0; sb < kSub; ++sb) {
+          if (sb < nsub) {
+            const half8_t b = *reinterpret_cast<const half8_t*>(&bop[buf][s & 3][g][16 * sb + m][0]);
+            acc1[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), b, acc1[sb], 0, 0, 0);
+            acc2[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), b, acc2[sb], 0, 0, 0);
           }
-          if (kb + 1 < kblocks) {
-            *reinterpret_cast<u32x4_t*>(&bop[buf ^ 1][st_step][st_g][st_col][0]) = sv;
-            if (tid < kTaskRows) bexp[buf ^ 1][tid] = se;
-          }
+        }
+        if ((s & 3) == 3) {
+          if (kb + 1 < kblocks) put(buf ^ 1, sv);
           __syncthreads();
         }
       }
     }
   }
 
-  // epilogue: rows' 128 columns through LDS, then H128 and svh per row
-  if ((m & 1) == 0) {
+  // epilogue: high + low parts (adjacent lanes) unscaled per row, the rows'
+  // 128 columns through LDS, then H128 and svh per row
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int row = 4 * g + k;
-      const int col = 32 * wave + (row & 7) + 16 * (row >> 3);
-      red[r_own][col] = tot1[k];
-      red[r_own][col + 8] = tot2[k];
+  for (int sb = 0; sb < kSub; ++sb) {
+    if (sb < nsub) {
+      const int r = 8 * sb + (m >> 1);
+      const int e = rexp[r];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float v1 = ldexpf(acc1[sb][k] + vq::xor_lanes<1>(acc1[sb][k], lane), -e);
+        const float v2 = ldexpf(acc2[sb][k] + vq::xor_lanes<1>(acc2[sb][k], lane), -e);
+        const int row = 4 * g + k;
+        const int col = 32 * wave + (row & 7) + 16 * (row >> 3);
+        if ((m & 1) == 0 && r < nrows) {
+          red[r][col] = v1;
+          red[r][col + 8] = v2;
+        }
+      }
     }
   }
   __syncthreads();
@@ -552,6 +602,10 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   }
   const int64_t assignments = rows * topk;
   if (assignments > INT_MAX) return fail("EXL3 MoE has too many routed assignments");
+  // the expert GEMV reads its B operands through 32-bit byte offsets
+  if (assignments * exl3::padded(std::max(hidden, intermediate_size)) * 4 > INT_MAX) {
+    return fail("EXL3 MoE: rows * topk * hidden too large for one call (split the rows)");
+  }
   const int64_t need = exl3_moe_workspace_size(rows, hidden, intermediate_size, topk, local_experts);
   if (need < 0) return kInvalidArgument;
   if (workspace_numel < need) return fail("EXL3 MoE workspace is too small");
@@ -566,11 +620,13 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   const bool any = local_experts > 0 && assignments > 0;
   if (any) {
     int* table = reinterpret_cast<int*>(workspace + lay.ints());
+    const int task_rows = exl3::task_rows(int(bits_x2));
     hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads),
-                       size_t(3 * local_experts + 1) * sizeof(int), s, routing, assignments, table);
+                       size_t(3 * local_experts + 1) * sizeof(int), s, routing, assignments, task_rows,
+                       table);
     if (int rc = check_launch("exl3 moe_route")) return rc;
     const int64_t max_tasks =
-        std::min<int64_t>(assignments, (assignments + exl3::kTaskRows - 1) / exl3::kTaskRows + local_experts);
+        std::min<int64_t>(assignments, (assignments + task_rows - 1) / task_rows + local_experts);
     if (max_tasks > 65535) return fail("EXL3 MoE has too many routed assignments");
     auto gemv = [&](int projection, int64_t kp, int64_t np, int64_t in_off, int64_t out_off) {
       const dim3 grid(unsigned(np / 128), unsigned(max_tasks));
@@ -585,8 +641,9 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       return check_launch("exl3 moe_gemv");
     };
     if (bits_x2 > 8) return fail("EXL3 MoE v2 supports mul1 rates up to 4 bits");
-    const int64_t form_h = (assignments * (lay.hpad / 128) + 3) / 4;
-    const int64_t form_i = (assignments * (lay.ipad / 128) + 3) / 4;
+    // moe_form: one workgroup per assignment (the routed ones do work)
+    const int64_t form_h = assignments;
+    const int64_t form_i = assignments;
     for (int p = 0; p < 2; ++p) {
       hipLaunchKernelGGL(exl3::moe_form<false>, dim3(unsigned(form_h)), dim3(256), 0, s, routing, x,
                          x_dtype, hidden, intermediate_size, p, table, workspace, lay, swiglu_limit);
