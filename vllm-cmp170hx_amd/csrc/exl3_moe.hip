@@ -318,9 +318,19 @@ __device__ __forceinline__ void decode_runtime(const uint8_t* tile, bool aligned
   }
 }
 
-struct GemvTask {
-  int expert, first, rows;
-};
+// Wave priority from progress (quarter q of the wavefront's steps: 3 - q).
+// The SIMD issues from its oldest wavefront first: equal wavefronts sharing a
+// saturated SIMD would otherwise finish one after another, and the last
+// ones, left alone, cannot keep it busy.  Ranking them by progress keeps
+// them level.
+__device__ __forceinline__ void progress_priority(int64_t step, int64_t steps) {
+  switch (int((4 * step) / steps)) {
+    case 0: __builtin_amdgcn_s_setprio(3); break;
+    case 1: __builtin_amdgcn_s_setprio(2); break;
+    case 2: __builtin_amdgcn_s_setprio(1); break;
+    default: __builtin_amdgcn_s_setprio(0); break;
+  }
+}
 
 // One workgroup = (task, 128 output columns); wavefront w owns the column
 // pair (two tile columns) 4 * blockIdx.x + w over the whole K range.  Each
@@ -436,13 +446,24 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
   int src[kWords];
 #pragma unroll
   for (int i = 0; i < kWords; ++i) src[i] = 4 * ((m >> 3) * 4 * kBitsX2 + widx[i]);
+  // Buffer loads over the wavefront's tile pair of every tile row (32-bit
+  // offsets; the host keeps an expert's matrix below 2 GiB): vmcnt only, so
+  // the LDS waits of each step (ds_bpermute) do not also wait for the
+  // trellis loads in flight, as flat loads would make them.
+  const __amdgpu_buffer_rsrc_t tr_buf = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(chunk), 0, int((steps * 2 - 1) * row_bytes + 2 * tile_bytes), 0x00020000);
   uint32_t raw[kDepth][2];
   auto load_step = [&](int slot, int64_t s) {
     if constexpr (kFixed) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const uint8_t* row = chunk + (2 * s + h) * row_bytes;
-        raw[slot][h] = aligned ? tile_word<true>(row, raw_off) : tile_word<false>(row, raw_off);
+        const int row = int((2 * s + h) * row_bytes);
+        if (aligned) {
+          raw[slot][h] = __builtin_amdgcn_raw_buffer_load_b32(tr_buf, raw_off, row, 0);
+        } else {
+          raw[slot][h] = uint32_t(__builtin_amdgcn_raw_buffer_load_b16(tr_buf, raw_off, row, 0)) |
+                         (uint32_t(__builtin_amdgcn_raw_buffer_load_b16(tr_buf, raw_off + 2, row, 0)) << 16);
+        }
       }
     }
   };
@@ -468,7 +489,10 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
       if (s < steps) {
         const int64_t kb = s >> 2;
         const int buf = int(kb & 1);
-        if ((s & 3) == 0 && kb + 1 < kblocks) stage(kb + 1, sv);
+        if ((s & 3) == 0) {
+          progress_priority(s, steps);
+          if (kb + 1 < kblocks) stage(kb + 1, sv);
+        }
         uint32_t q0[4], q1[4];
         if constexpr (kFixed) {
           uint32_t w0[kWords], w1[kWords];
@@ -487,12 +511,17 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
         }
         const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
         const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
+        // every sub-block's B operand in one batch of LDS reads (the staged
+        // columns past the task hold its last row: valid data), then the
+        // MFMAs of the task's sub-blocks
+        half8_t b[kSub];
+#pragma unroll
+        for (int sb = 0; sb < kSub; ++sb) b[sb] = *reinterpret_cast<const half8_t*>(&bop[buf][s & 3][g][16 * sb + m][0]);
 #pragma unroll
         for (int sb = 0; sb < kSub; ++sb) {
           if (sb < nsub) {
-            const half8_t b = *reinterpret_cast<const half8_t*>(&bop[buf][s & 3][g][16 * sb + m][0]);
-            acc1[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), b, acc1[sb], 0, 0, 0);
-            acc2[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), b, acc2[sb], 0, 0, 0);
+            acc1[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), b[sb], acc1[sb], 0, 0, 0);
+            acc2[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), b[sb], acc2[sb], 0, 0, 0);
           }
         }
         if ((s & 3) == 3) {
@@ -602,9 +631,13 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   }
   const int64_t assignments = rows * topk;
   if (assignments > INT_MAX) return fail("EXL3 MoE has too many routed assignments");
-  // the expert GEMV reads its B operands through 32-bit byte offsets
+  // the expert GEMV reads its B operands and each expert matrix through
+  // 32-bit byte offsets
   if (assignments * exl3::padded(std::max(hidden, intermediate_size)) * 4 > INT_MAX) {
     return fail("EXL3 MoE: rows * topk * hidden too large for one call (split the rows)");
+  }
+  if (exl3::padded(hidden) * exl3::padded(intermediate_size) * 2 > INT_MAX) {
+    return fail("EXL3 MoE: an expert matrix must stay below 2 GiB");
   }
   const int64_t need = exl3_moe_workspace_size(rows, hidden, intermediate_size, topk, local_experts);
   if (need < 0) return kInvalidArgument;
