@@ -5,14 +5,16 @@
 // Launch sequence on the caller's stream (as the reference's run_moe_out):
 //  1. moe_route: one workgroup groups the local assignments by local expert
 //     (counts, scan, sorted list) and cuts each expert's rows into tasks of
-//     at most 8 rows (the per-expert token sort).
+//     at most 32 rows (8 for the run-time-format decode: the per-expert
+//     token sort).
 //  2. per projection (gate, up): moe_form builds t = H128(x[a / topk] * suh)
 //     of every local assignment, as FP16 high/low parts in MFMA B-operand
-//     order with a per-(assignment, 128-input block) power-of-two scale;
-//     moe_gemv runs every task against its expert's matrix: one workgroup =
-//     (task, 128 output columns) over the whole K range, trellis streamed
-//     with coalesced loads, decoded in registers, v_mfma_f32_16x16x32_f16,
-//     then the output H128 and svh in the same kernel.
+//     order with one power-of-two scale per assignment row; moe_gemv runs
+//     every task against its expert's matrix: one workgroup = (task, 128
+//     output columns) over the whole K range, trellis streamed with
+//     coalesced buffer loads, decoded in registers, each decoded operand fed
+//     to v_mfma_f32_16x16x32_f16 for every 8-row sub-block of the task, then
+//     the output H128 and svh in the same kernel.
 //  3. moe_form (activation): clamp, SiLU(gate) * up * suh_down, H128 - the
 //     down projection's activations, in the same B-operand form.
 //  4. moe_gemv for the down projection.
