@@ -274,11 +274,13 @@ def test_linear_unaligned_trellis_matches_oracle(ops, device, offset_bytes, bits
     _assert_fp32_close(out.cpu().numpy(), want, f"offset={offset_bytes}")
 
 
-@pytest.mark.parametrize("rows", [9, 64, 300, 513])
+@pytest.mark.parametrize("rows", [9, 32, 33, 64, 300, 513])
 @pytest.mark.parametrize("bits_x2,codebook", [(8, 2), (4, 1), (6, 2), (3, 2)])
 def test_prefill_matches_oracle(ops, device, rows, bits_x2, codebook):
-    """Large-M path (decode to LDS + MFMA); rows are independent, so the
-    oracle checks a sample of them."""
+    """Rows past one small-M launch: up to 32 the small-M kernel in chunks
+    of 8 rows, above that the large-M path (decode to LDS + MFMA, output
+    transform in its epilogue); rows are independent, so the oracle checks a
+    sample of them."""
     print(f"prefill rows={rows} bits_x2={bits_x2} cb={codebook}", flush=True)
     rng = np.random.default_rng(5000 + rows + bits_x2)
     k, n = 1024, 2048 + 128  # a partial 256-column tile too

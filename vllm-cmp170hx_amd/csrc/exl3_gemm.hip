@@ -1,8 +1,8 @@
 // EXL3 dense linear for many rows (prefill), gfx950.
 //
-// Three launches on the caller's stream, like the reference's operator
-// (csrc/exl3/dense.cu:115-148: linear_input, GEMM, linear_output), but the
-// GEMM runs on the matrix cores:
+// Two launches on the caller's stream, where the reference's operator has
+// three (csrc/exl3/dense.cu:115-148: linear_input, GEMM, linear_output); the
+// GEMM runs on the matrix cores and applies the output transform itself:
 //  1. prefill_input: one workgroup per row forms t = H128(x * suh) over the
 //     whole row, picks a per-row power-of-two scale from the row maximum, and
 //     writes t as FP16 high and low parts (t * 2^e = hi + lo, ~22 bits).
@@ -10,17 +10,20 @@
 //     along N, 64 x 128 each = 2 x 4 v_mfma_f32_32x32x16_f16 tiles).  Per
 //     K step of 32 inputs the workgroup decodes the 32 x 256 weight slab
 //     (32 trellis tiles, two encoder lanes per thread) straight into LDS as
-//     W^T [n][k] in FP16 (exact values), stages the activation tiles, and
+//     W^T [n][k] in FP16 (exact values) and stages the activation tiles;
 //     every wavefront accumulates hi * W and lo * W into one FP32
-//     accumulator.  The next step's trellis words and activations are
-//     loaded into registers while the current step's MFMAs run.  Rows are
-//     unscaled (2^-e) in the epilogue and written as the FP32 core result.
-//  3. the shared finish: H128 over each 128-column block, times svh,
-//     rounded to the output dtype.
+//     accumulator.  The slab and tiles are double-buffered: step s + 1 is
+//     decoded and staged while the MFMAs of step s run (one barrier a step),
+//     with its trellis words and activations loaded two steps ahead.  The
+//     epilogue unscales each row (2^-e) and applies the output transform:
+//     H128 over each wavefront's 128-column band (one H128 block), times
+//     svh, rounded to the output dtype.
 //
-// Workspace (FP32 elements, rows x ...): [hi | lo halves: padded_in][core
-// result: padded_out] and one int row exponent per row after them.
+// Workspace (FP32 elements, rows x ...): [hi | lo halves: padded_in][padded_out,
+// unused] and one int row exponent per row after them.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "common.h"
 #include "exl3_codec.h"
@@ -98,21 +101,26 @@ struct PrefillArgs {
   const _Float16* lo;     // [rows][kp]
   const int* row_exp;     // [rows]
   const uint8_t* trellis;
-  float* core;            // [rows][np]
+  const uint16_t* svh;    // [np]
+  void* out;              // [rows][logical_out]
   int64_t rows;
   int64_t kp;
   int64_t np;
   int64_t tiles_n;
+  int64_t logical_out;
+  int out_dtype;
 };
 
 template <int kBitsX2, int kCodebook, bool kAligned>
 __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
   using R = Ring<kBitsX2>;
   constexpr int kWords = LaneLoad<kBitsX2>::kWords;
-  // W^T slab [n][k] and the two activation tiles [m][k], FP16, 80-byte rows
-  __shared__ __attribute__((aligned(16))) _Float16 w_lds[kBN * kLdsK];
-  __shared__ __attribute__((aligned(16))) _Float16 hi_lds[kBM * kLdsK];
-  __shared__ __attribute__((aligned(16))) _Float16 lo_lds[kBM * kLdsK];
+  // two buffers of: the W^T slab [n][k] and the two activation tiles [m][k],
+  // FP16, 80-byte rows.  Step s+1 is decoded and staged into one buffer while
+  // the MFMAs of step s read the other: one barrier per step.
+  __shared__ __attribute__((aligned(16))) _Float16 w_lds[2][kBN * kLdsK];
+  __shared__ __attribute__((aligned(16))) _Float16 hi_lds[2][kBM * kLdsK];
+  __shared__ __attribute__((aligned(16))) _Float16 lo_lds[2][kBM * kLdsK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -158,86 +166,150 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
 
-  uint32_t words[2][kWords];
-  u32x4_t hv[2], lv[2];
-  auto fetch = [&](int step) {
+  // two register slots of fetched step data: slot s & 1 holds step s, loaded
+  // two steps before it is decoded
+  uint32_t words[2][2][kWords];
+  u32x4_t hv[2][2], lv[2][2];
+  auto fetch = [&](int slot, int step) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int w = 0; w < kWords; ++w)
-        words[i][w] = tile_word<kAligned>(task_src[i] + step * step_bytes, off[i][w]);
+        words[slot][i][w] = tile_word<kAligned>(task_src[i] + step * step_bytes, off[i][w]);
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
-      hv[v] = *reinterpret_cast<const u32x4_t*>(hi_src + int64_t(step) * kBK + 8 * v);
-      lv[v] = *reinterpret_cast<const u32x4_t*>(lo_src + int64_t(step) * kBK + 8 * v);
+      hv[slot][v] = *reinterpret_cast<const u32x4_t*>(hi_src + int64_t(step) * kBK + 8 * v);
+      lv[slot][v] = *reinterpret_cast<const u32x4_t*>(lo_src + int64_t(step) * kBK + 8 * v);
     }
   };
-
-  fetch(0);
-  for (int step = 0; step < steps; ++step) {
-    // decode the slab and stage the activations
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint32_t pair[4];
-      decode_words<kBitsX2, kCodebook>(task_l[i], words[i], pair);
-      if (!task_on[i]) pair[0] = pair[1] = pair[2] = pair[3] = 0u;
-      const int L = task_l[i];
-      const int k = task_tr[i] * 16 + 2 * (L & 3);
-      const int n = task_tc[i] * 16 + (L >> 2);
-      // pair p = values (2p, 2p+1): k and k+1 of one column
-      *reinterpret_cast<uint32_t*>(w_lds + n * kLdsK + k) = pair[0];
-      *reinterpret_cast<uint32_t*>(w_lds + n * kLdsK + k + 8) = pair[1];
-      *reinterpret_cast<uint32_t*>(w_lds + (n + 8) * kLdsK + k) = pair[2];
-      *reinterpret_cast<uint32_t*>(w_lds + (n + 8) * kLdsK + k + 8) = pair[3];
-    }
+  // decode task i of the step in register slot `slot` into W buffer `buf`
+  auto decode_task = [&](int slot, int buf, int i) {
+    uint32_t pair[4];
+    decode_words<kBitsX2, kCodebook>(task_l[i], words[slot][i], pair);
+    if (!task_on[i]) pair[0] = pair[1] = pair[2] = pair[3] = 0u;
+    const int L = task_l[i];
+    const int k = task_tr[i] * 16 + 2 * (L & 3);
+    const int n = task_tc[i] * 16 + (L >> 2);
+    // pair p = values (2p, 2p+1): k and k+1 of one column
+    _Float16* w = w_lds[buf];
+    *reinterpret_cast<uint32_t*>(w + n * kLdsK + k) = pair[0];
+    *reinterpret_cast<uint32_t*>(w + n * kLdsK + k + 8) = pair[1];
+    *reinterpret_cast<uint32_t*>(w + (n + 8) * kLdsK + k) = pair[2];
+    *reinterpret_cast<uint32_t*>(w + (n + 8) * kLdsK + k + 8) = pair[3];
+  };
+  auto stage = [&](int slot, int buf) {
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
-      *reinterpret_cast<u32x4_t*>(hi_lds + st_row * kLdsK + st_half + 8 * v) = hv[v];
-      *reinterpret_cast<u32x4_t*>(lo_lds + st_row * kLdsK + st_half + 8 * v) = lv[v];
+      *reinterpret_cast<u32x4_t*>(hi_lds[buf] + st_row * kLdsK + st_half + 8 * v) = hv[slot][v];
+      *reinterpret_cast<u32x4_t*>(lo_lds[buf] + st_row * kLdsK + st_half + 8 * v) = lv[slot][v];
     }
-    __syncthreads();
-    if (step + 1 < steps) fetch(step + 1);
-    // two k16 chunks: A = activations (rows l % 32, k 8 (l / 32) + i),
-    // B = W (k 8 (l / 32) + i, columns l % 32)
+  };
+  // the MFMAs of one k16 chunk of buffer `buf`: A = activations (rows l % 32,
+  // k 8 (l / 32) + i), B = W (k 8 (l / 32) + i, columns l % 32)
+  auto mfma_chunk = [&](int buf, int kc) {
+    const int ko = kc * 16 + 8 * (lane >> 5);
+    half8_t ah[2], al[2], b[4];
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
-      const int ko = kc * 16 + 8 * (lane >> 5);
-      half8_t ah[2], al[2], b[4];
+    for (int i = 0; i < 2; ++i) {
+      const int m = wm * 64 + i * 32 + (lane & 31);
+      ah[i] = *reinterpret_cast<const half8_t*>(hi_lds[buf] + m * kLdsK + ko);
+      al[i] = *reinterpret_cast<const half8_t*>(lo_lds[buf] + m * kLdsK + ko);
+    }
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int m = wm * 64 + i * 32 + (lane & 31);
-        ah[i] = *reinterpret_cast<const half8_t*>(hi_lds + m * kLdsK + ko);
-        al[i] = *reinterpret_cast<const half8_t*>(lo_lds + m * kLdsK + ko);
-      }
+    for (int j = 0; j < 4; ++j) {
+      const int n = wn * 128 + j * 32 + (lane & 31);
+      b[j] = *reinterpret_cast<const half8_t*>(w_lds[buf] + n * kLdsK + ko);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int n = wn * 128 + j * 32 + (lane & 31);
-        b[j] = *reinterpret_cast<const half8_t*>(w_lds + n * kLdsK + ko);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], acc[i][j], 0, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], acc[i][j], 0, 0, 0);
-        }
+  };
+
+  // prologue: steps 0 and 1 in flight, step 0 decoded and staged into buffer 0.
+  // Every fetch is issued unconditionally (past the last step it reloads the
+  // last one): a load a branch may skip leaves the compiler unsure of the
+  // loads in flight, and it then waits for more of them than a step needs.
+  const int last = steps - 1;
+  fetch(0, 0);
+  fetch(1, min(1, last));
+  decode_task(0, 0, 0);
+  decode_task(0, 0, 1);
+  stage(0, 0);
+  fetch(0, min(2, last));
+  __syncthreads();
+  // step s: the MFMAs of buffer s & 1, interleaved with the decode and staging
+  // of step s + 1 (register slot (s + 1) & 1) into the other buffer, then the
+  // fetch of step s + 3 into the slot just decoded.  Steps run in pairs so the
+  // buffer and slot indices are constants (registers cannot be indexed).
+  auto iteration = [&](int step, int buf) {
+    const int nslot = buf ^ 1;
+    const bool more = step + 1 < steps;
+    mfma_chunk(buf, 0);
+    if (more) decode_task(nslot, buf ^ 1, 0);
+    mfma_chunk(buf, 1);
+    if (more) {
+      decode_task(nslot, buf ^ 1, 1);
+      stage(nslot, buf ^ 1);
     }
+    fetch(nslot, min(step + 3, last));
     __syncthreads();
+  };
+  for (int step = 0; step < steps; step += 2) {
+    iteration(step, 0);
+    if (step + 1 < steps) iteration(step + 1, 1);
   }
 
-  // epilogue: lane l, register r of tile (i, j) is row 8 (r / 4) + 4 (l / 32)
-  // + r % 4, column l % 32
+  // epilogue, the output transform fused: lane l, register r of tile (i, j)
+  // is row 8 (r / 4) + 4 (l / 32) + r % 4, column 32 j + l % 32 of the
+  // wavefront's 128-column band, which is one H128 block.  Per row: unscale
+  // (2^-e), H128 (butterfly distances 1..16 across the 32 lanes of the row's
+  // half-wavefront, 32 and 64 across the four registers j, in that order, as
+  // the standalone transform), times svh, rounded to the output dtype.
+  const int64_t band = col0 + wn * 128;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int64_t row = row0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      if (row < a.rows) {
-        const int e = a.row_exp[row];
+      const int e = a.row_exp[row < a.rows ? row : a.rows - 1];
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = ldexpf(acc[i][j][r], -e);
+      auto lane_stage = [&](auto d_tag) {
+        constexpr int d = decltype(d_tag)::value;
+        const bool upper = (lane & d) != 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int64_t col = col0 + wn * 128 + j * 32 + (lane & 31);
-          if (col < a.np) a.core[row * a.np + col] = ldexpf(acc[i][j][r], -e);
+          const float o = vq::xor_lanes<d>(v[j], lane);
+          v[j] = o + (upper ? -v[j] : v[j]);
+        }
+      };
+      lane_stage(std::integral_constant<int, 1>{});
+      lane_stage(std::integral_constant<int, 2>{});
+      lane_stage(std::integral_constant<int, 4>{});
+      lane_stage(std::integral_constant<int, 8>{});
+      lane_stage(std::integral_constant<int, 16>{});
+      // distance 32 (registers j, j ^ 1), then 64 (j, j ^ 2) with the scale
+      float w[4];
+      w[0] = v[0] + v[1];
+      w[1] = v[0] - v[1];
+      w[2] = v[2] + v[3];
+      w[3] = v[2] - v[3];
+      v[0] = (w[0] + w[2]) * vq::kH128Scale;
+      v[2] = (w[0] - w[2]) * vq::kH128Scale;
+      v[1] = (w[1] + w[3]) * vq::kH128Scale;
+      v[3] = (w[1] - w[3]) * vq::kH128Scale;
+      if (row < a.rows) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t col = band + j * 32 + (lane & 31);
+          if (col < a.logical_out) {
+            vq::store_act(a.out, a.out_dtype, row * a.logical_out + col, v[j] * vq::f16_to_f32(a.svh[col]));
+          }
         }
       }
     }
@@ -266,12 +338,13 @@ int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trel
   if (rows > 65535 * int64_t(kBM)) return vq::fail("EXL3 linear has too many rows");
   _Float16* hi = reinterpret_cast<_Float16*>(workspace);
   _Float16* lo = hi + rows * kp;
-  float* core = workspace + rows * kp;
-  int* row_exp = reinterpret_cast<int*>(core + rows * np);
+  // (the FP32 core result region between them is not used: the GEMM
+  // applies the output transform itself)
+  int* row_exp = reinterpret_cast<int*>(workspace + rows * kp + rows * np);
   hipLaunchKernelGGL(prefill_input, dim3(unsigned(rows)), dim3(256), 0, stream, x, x_dtype,
                      logical_in, kp, suh, hi, lo, row_exp);
   if (int rc = vq::check_launch("exl3 prefill_input")) return rc;
-  PrefillArgs a{hi, lo, row_exp, trellis, core, rows, kp, np, tiles_n};
+  PrefillArgs a{hi, lo, row_exp, trellis, svh, out, rows, kp, np, tiles_n, logical_out, out_dtype};
   const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
   int rc = vq::kOk;
   bool done = false;
@@ -283,8 +356,7 @@ int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trel
   VQ_EXL3_FORMATS(VQ_CASE)
 #undef VQ_CASE
   if (!done) return vq::fail("Unsupported EXL3 rate/codebook combination");
-  if (rc != vq::kOk) return rc;
-  return launch_output(core, 1, int(rows), np, svh, logical_out, out, out_dtype, stream);
+  return rc;
 }
 
 }  // namespace exl3

@@ -52,6 +52,10 @@ using vq::kFP32;
 
 constexpr int kThreads = 256;
 constexpr int kMaxGemvRows = 8;
+// Calls of up to this many rows run the small-M kernel in chunks of
+// kMaxGemvRows (each chunk streams the matrix once); the prefill GEMM's
+// 256-row tiles only pay off above it.
+constexpr int kGemvChunkedRows = 32;
 
 // Per-rate geometry of the small-M kernel.
 //
@@ -958,7 +962,7 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
   if (rows == 0) return kOk;
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (rows > exl3::kMaxGemvRows) {
+  if (rows > exl3::kGemvChunkedRows) {
     return exl3::prefill_linear(x, x_dtype, rows, static_cast<const uint8_t*>(trellis), tiles_k,
                                 tiles_n, static_cast<const uint16_t*>(suh),
                                 static_cast<const uint16_t*>(svh), int(bits_x2), int(codebook),
