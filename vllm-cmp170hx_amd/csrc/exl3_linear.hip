@@ -554,34 +554,50 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
   float tot1[4], tot2[4];
   half8_t bop = {};
   if constexpr (!kLds) gather(0);
+  //    LDS stream: the words of step j + 1 are read at the start of step j,
+  //    so their latency hides behind step j's decode (a wavefront running
+  //    alone on its SIMD would otherwise wait for every step's reads).
+  //    Reading step s, the first step of load i = s / kP, needs load i
+  //    landed.  The reads of step s > 0 are issued in step s - 1, before
+  //    that step's refill, so the loads issued by then are 0 .. min(i - 2 +
+  //    kRingLoads, kLoads - 1), and at most min(kRingLoads - 2, kLoads - 1 -
+  //    i) of them may still be pending; before step 0, kRingLoads - 1.
+  uint32_t nw0[G::kWords], nw1[G::kWords];
+  auto read_words = [&](int s) {
+    const int i = s / kP;
+    if (s % kP == 0) {
+      const int younger = s == 0 ? kRingLoads - 1
+                                 : (kRingLoads - 2 < kLoads - 1 - i ? kRingLoads - 2 : kLoads - 1 - i);
+      switch (younger) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<1>(); break;
+        case 2: wait_vmcnt<2>(); break;
+        default: wait_vmcnt<3>(); break;
+      }
+    }
+    const uint32_t* slot = slot_of_load(i) + (2 * (s % kP)) * (G::kChunk / 4);
+#pragma unroll
+    for (int q = 0; q < G::kWords; ++q) {
+      nw0[q] = slot[src[q]];
+      nw1[q] = slot[G::kChunk / 4 + src[q]];
+    }
+  };
+  if constexpr (kLds) read_words(0);
 #pragma unroll
   for (int j = 0; j < kSteps; ++j) {
     uint32_t w0[G::kWords], w1[G::kWords];
     if constexpr (kLds) {
-      const int i = j / kP;
-      if (j % kP == 0) {
-        // load i has landed: at most the loads issued after it are pending
-        if (i + kRingLoads - 1 < kLoads) {
-          wait_vmcnt<kRingLoads - 1>();
-        } else {
-          // the tail: no loads were issued after the last kRingLoads
-          switch (kLoads - 1 - i) {
-            case 0: wait_vmcnt<0>(); break;
-            case 1: wait_vmcnt<1>(); break;
-            case 2: wait_vmcnt<2>(); break;
-            case 3: wait_vmcnt<3>(); break;
-            case 4: wait_vmcnt<4>(); break;
-            case 5: wait_vmcnt<5>(); break;
-            case 6: wait_vmcnt<6>(); break;
-            default: wait_vmcnt<7>(); break;
-          }
-        }
-      }
-      const uint32_t* slot = slot_of_load(i) + (2 * (j % kP)) * (G::kChunk / 4);
 #pragma unroll
       for (int q = 0; q < G::kWords; ++q) {
-        w0[q] = slot[src[q]];
-        w1[q] = slot[G::kChunk / 4 + src[q]];
+        w0[q] = nw0[q];
+        w1[q] = nw1[q];
+      }
+      if (j + 1 < kSteps) read_words(j + 1);
+      // this step's B operand, read ahead of the decode (step 0's are
+      // written after it, below)
+      if (j > 0 && m < kCols) {
+        asm volatile("" ::: "memory");
+        bop = bops[j * 4 * kCols];
       }
     } else {
       if (j + 1 < kSteps) gather(j + 1);
@@ -617,14 +633,15 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
     const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
     // only the lanes of used B columns read (LDS bandwidth): the others keep
     // a stale operand, whose MFMA columns are never looked at
-    if (m < kCols) {
+    if ((!kLds || j == 0) && m < kCols) {
       asm volatile("" ::: "memory");
       bop = bops[j * 4 * kCols];
     }
     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), bop, acc1, 0, 0, 0);
     acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), bop, acc2, 0, 0, 0);
-    // LDS stream: the slot's last step was read (its reads returned during
-    // the decode): refill it with load i + kRingLoads
+    // LDS stream: the slot's last step was read in the previous step (its
+    // reads returned during this step's decode): refill it with load
+    // i + kRingLoads
     if constexpr (kLds) {
       if (j % kP == kP - 1 && j / kP + kRingLoads < kLoads) {
         wait_lgkmcnt0();
