@@ -27,10 +27,14 @@ The same line also carries:
              router logits ~N(0,1) -> softmax top-8) at 1, 16, 64 and 256
              tokens: tokens/s, HBM GB/s over the touched experts' bytes,
              and MFMA utilisation against the 2.5 PFLOP/s fp16 peak;
-  exl3_prefill  the 8192 x 28672 4-bit linear at M = 2048: TFLOP/s;
+  exl3_gemv_configs  the same linear at M = 4 and 8, at 3 and 2 bits per
+             weight, and the transposed 14336 x 4096 matrix: GB/s;
+  exl3_prefill  the 8192 x 28672 4-bit linear at M = 2048 (and 512, 8192):
+             TFLOP/s;
   exl3_moe   the 3-bit EXL3 MoE (256 routed experts + 1 shared, hidden
              7168, intermediate 2048, top-8 from Zipf(1.1)-skewed logits)
-             at 64 decode tokens: tokens/s and HBM GB/s;
+             at 64 decode tokens (and 2048 prefill tokens): tokens/s and
+             HBM GB/s;
 and the CPU baselines: the reference's CPU dequantize-then-matmul paths
 (oracle/exl3_torch_ref.py, oracle/marlin_torch_ref.py) on this host's
 cores, each on a bounded sample of its workload.
@@ -130,6 +134,40 @@ def gpu_gemv(args, torch):
     ms, steps, warm = time_graph(torch, call, GRAPH_CALLS, args.warmup, args.steps)
     del mats
     return ms, steps, warm
+
+
+def gpu_gemv_configs(args, torch):
+    """The other small-M linear shapes of the decode workload: more rows,
+    fewer bits per weight, and the transposed (down-projection) matrix.  Each
+    rotates enough weight copies (>= 400 MB) that every call streams from
+    HBM."""
+    from vllm_mi355x.kernels.exl3 import ops
+
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device)
+    gen.manual_seed(4321)
+    results = {}
+    for name, k, n, bits_x2, rows in (("4bit_m4", K_IN, N_OUT, 8, 4), ("4bit_m8", K_IN, N_OUT, 8, 8),
+                                      ("3bit_m1", K_IN, N_OUT, 6, 1), ("2bit_m1", K_IN, N_OUT, 4, 1),
+                                      ("4bit_m1_14336x4096", N_OUT, K_IN, 8, 1)):
+        nbytes = gemv_bytes(k, n, bits_x2, rows)
+        copies = max(COPIES, -(-400_000_000 // nbytes))
+        mats = [make_matrix(torch, gen, device, k, n, bits_x2) for _ in range(copies)]
+        x = torch.randn(rows, k, device=device, generator=gen).half()
+        out = torch.empty(rows, n, dtype=torch.float16, device=device)
+        ws = torch.empty(ops.linear_workspace_size(rows, k, n), dtype=torch.float32, device=device)
+
+        def call(i, mats=mats, x=x, out=out, ws=ws, k=k, n=n, bits_x2=bits_x2):
+            t, suh, svh = mats[i % len(mats)]
+            ops.linear_out(x, t, suh, svh, bits_x2, CODEBOOK, k, n, out, ws)
+
+        ms, _, _ = time_graph(torch, call, GRAPH_CALLS, args.warmup, max(240, args.steps // 2))
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        results[name] = {"k": k, "n": n, "bits_per_weight": bits_x2 / 2, "rows": rows,
+                         "us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del mats
+    return results
 
 
 def measured_traffic():
@@ -244,7 +282,7 @@ def cpu_marlin_moe(seconds: float, torch):
 
 # ---- EXL3 prefill and MoE ---------------------------------------------------------------
 
-def gpu_exl3_prefill(torch, rows=2048, k=8192, n=28672):
+def gpu_exl3_prefill(torch, rows=2048, k=8192, n=28672, other_rows=(512, 8192)):
     from vllm_mi355x.kernels.exl3 import ops
 
     ops.ensure_extension()
@@ -252,20 +290,28 @@ def gpu_exl3_prefill(torch, rows=2048, k=8192, n=28672):
     gen = torch.Generator(device=device)
     gen.manual_seed(7)
     t, suh, svh = make_matrix(torch, gen, device, k, n, 8)
-    x = torch.randn(rows, k, device=device, generator=gen).half()
-    out = torch.empty(rows, n, dtype=torch.float16, device=device)
-    ws = torch.empty(ops.linear_workspace_size(rows, k, n), dtype=torch.float32, device=device)
 
-    def call(i):
-        ops.linear_out(x, t, suh, svh, 8, CODEBOOK, k, n, out, ws)
+    def measure(m):
+        x = torch.randn(m, k, device=device, generator=gen).half()
+        out = torch.empty(m, n, dtype=torch.float16, device=device)
+        ws = torch.empty(ops.linear_workspace_size(m, k, n), dtype=torch.float32, device=device)
 
-    ms, _, _ = time_graph(torch, call, 4, 4, 12)
-    tflops = 2 * rows * k * n / (ms * 1e-3) / 1e12
-    return {"workload": f"{k}x{n} 4-bit mul1, M={rows}, fp16", "ms": round(ms, 3),
-            "tflops": round(tflops, 1), "mfma_util": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4)}
+        def call(i):
+            ops.linear_out(x, t, suh, svh, 8, CODEBOOK, k, n, out, ws)
+
+        ms, _, _ = time_graph(torch, call, 4, 4, 12)
+        tflops = 2 * m * k * n / (ms * 1e-3) / 1e12
+        return {"ms": round(ms, 3), "tflops": round(tflops, 1),
+                "mfma_util": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4)}
+
+    result = {"workload": f"{k}x{n} 4-bit mul1, M={rows}, fp16", **measure(rows)}
+    result["by_rows"] = {str(m): measure(m) for m in other_rows}
+    return result
 
 
-def gpu_exl3_moe(torch, tokens=64, experts=256, hidden=7168, inter=2048, topk=8, bits_x2=6):
+def gpu_exl3_moe(torch, tokens=(64, 2048), experts=256, hidden=7168, inter=2048, topk=8, bits_x2=6):
+    """The first token count is the line's headline; every count is in
+    by_tokens."""
     from vllm_mi355x.kernels.exl3 import ops
 
     ops.ensure_extension()
@@ -289,30 +335,40 @@ def gpu_exl3_moe(torch, tokens=64, experts=256, hidden=7168, inter=2048, topk=8,
     # plus the shared expert with weight 1 in slot 8
     ranks = torch.randperm(experts, generator=torch.Generator().manual_seed(10)).float() + 1.0
     bias = (-1.1 * torch.log(ranks)).to(device)
-    logits = torch.randn(tokens, experts, generator=gen, device=device) + bias
-    tw, ti = softmax_topk(torch, logits, topk)
-    ids = torch.cat([ti, torch.full((tokens, 1), experts, dtype=torch.int32, device=device)], 1)
-    weights = torch.cat([tw, torch.ones(tokens, 1, device=device)], 1).contiguous()
     emap = torch.arange(local, dtype=torch.int32, device=device)
-    x = torch.randn(tokens, hidden, generator=gen, device=device).half()
-    out = torch.empty_like(x)
-    ws = torch.empty(ops.moe_workspace_size_v2(tokens, hidden, inter, topk + 1, local),
-                     dtype=torch.float32, device=device)
-
-    def call(i):
-        ops.moe_out_v2(x, ids.contiguous(), weights, ptrs, meta, emap, inter, bits_x2, out, ws)
-
-    ms, _, _ = time_graph(torch, call, 10, 10, 50)
-    touched = int(torch.unique(ids).numel())
     per_expert = 3 * hidden * inter * bits_x2 // 16 + 2 * 2 * (hidden + inter) + 2 * (hidden + inter)
-    nbytes = touched * per_expert + 2 * 2 * tokens * hidden
-    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    def measure(t_count):
+        logits = torch.randn(t_count, experts, generator=gen, device=device) + bias
+        tw, ti = softmax_topk(torch, logits, topk)
+        ids = torch.cat([ti, torch.full((t_count, 1), experts, dtype=torch.int32, device=device)], 1)
+        ids = ids.contiguous()
+        weights = torch.cat([tw, torch.ones(t_count, 1, device=device)], 1).contiguous()
+        x = torch.randn(t_count, hidden, generator=gen, device=device).half()
+        out = torch.empty_like(x)
+        ws = torch.empty(ops.moe_workspace_size_v2(t_count, hidden, inter, topk + 1, local),
+                         dtype=torch.float32, device=device)
+
+        def call(i):
+            ops.moe_out_v2(x, ids, weights, ptrs, meta, emap, inter, bits_x2, out, ws)
+
+        reps = 10 if t_count <= 256 else 2
+        ms, _, _ = time_graph(torch, call, reps, reps, 5 * reps)
+        touched = int(torch.unique(ids).numel())
+        nbytes = touched * per_expert + 2 * 2 * t_count * hidden
+        flops = 2 * 3 * hidden * inter * t_count * (topk + 1)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        tflops = flops / (ms * 1e-3) / 1e12
+        return {"us_per_forward": round(ms * 1e3, 1), "tokens_per_s": round(t_count / (ms * 1e-3)),
+                "experts_touched": touched, "hbm_gbs": round(gbs, 1),
+                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "tflops": round(tflops, 1),
+                "mfma_util": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4)}
+
+    by_tokens = {str(t_count): measure(t_count) for t_count in tokens}
     del keep
     return {"workload": (f"{experts}+1 experts, {hidden}/{inter}, {bits_x2 / 2:g}-bit mul1, top-{topk} "
-                         f"Zipf(1.1), {tokens} tokens, fp16"),
-            "us_per_forward": round(ms * 1e3, 1), "tokens_per_s": round(tokens / (ms * 1e-3)),
-            "experts_touched": touched, "hbm_gbs": round(gbs, 1),
-            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+                         f"Zipf(1.1), {tokens[0]} tokens, fp16"),
+            **by_tokens[str(tokens[0])], "by_tokens": by_tokens}
 
 
 def cpu_baseline(seconds: float, torch):
@@ -416,6 +472,7 @@ def main() -> int:
             "bound_at_256": "hbm",
             "by_tokens": moe,
         }
+        result["exl3_gemv_configs"] = gpu_gemv_configs(args, torch)
         result["exl3_prefill"] = gpu_exl3_prefill(torch)
         result["exl3_moe"] = gpu_exl3_moe(torch)
     if not args.no_cpu:
