@@ -87,6 +87,18 @@ __device__ __forceinline__ float xor_lanes(float v, int lane) {
   return __builtin_bit_cast(float, r);
 }
 
+// A wavefront-uniform value the compiler cannot prove uniform (read through a
+// pointer into memory the kernel also writes, so with a vector load, or
+// derived from threadIdx.x / 64) moved to a scalar register: buffer
+// resources and scalar offsets built from it then need no per-lane loop.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uniform(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u >> 32)));
+  return static_cast<int64_t>(uint64_t(lo) | (uint64_t(hi) << 32));
+}
+
 // Max over the wavefront (every lane gets it).
 __device__ __forceinline__ float wave_max(float v, int lane) {
   v = fmaxf(v, xor_lanes<32>(v, lane));

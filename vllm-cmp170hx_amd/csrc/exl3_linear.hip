@@ -234,7 +234,7 @@ __device__ __forceinline__ void finish_row_block(const float* __restrict__ parti
 // wavefront w applies H128 and svh to rows w, w + 4.
 __device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int tid, int cblk) {
   const int col = tid & 127;
-  const int part = tid >> 7;
+  const int part = vq::uniform(tid >> 7);   // the split's scalar offset
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int64_t base = 128 * int64_t(cblk);

@@ -325,12 +325,17 @@ __device__ __forceinline__ void decode_runtime(const uint8_t* tile, bool aligned
 // saturated SIMD would otherwise finish one after another, and the last
 // ones, left alone, cannot keep it busy.  Ranking them by progress keeps
 // them level.
-__device__ __forceinline__ void progress_priority(int64_t step, int64_t steps) {
-  switch (int((4 * step) / steps)) {
-    case 0: __builtin_amdgcn_s_setprio(3); break;
-    case 1: __builtin_amdgcn_s_setprio(2); break;
-    case 2: __builtin_amdgcn_s_setprio(1); break;
-    default: __builtin_amdgcn_s_setprio(0); break;
+// Compares rather than a division (none in hardware).
+__device__ __forceinline__ void progress_priority(int step, int steps) {
+  const int q = 4 * step;
+  if (q < steps) {
+    __builtin_amdgcn_s_setprio(3);
+  } else if (q < 2 * steps) {
+    __builtin_amdgcn_s_setprio(2);
+  } else if (q < 3 * steps) {
+    __builtin_amdgcn_s_setprio(1);
+  } else {
+    __builtin_amdgcn_s_setprio(0);
   }
 }
 
@@ -361,22 +366,27 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
 
   const int64_t task = blockIdx.y;
   if (task >= table[1]) return;
+  // the task, the expert's pointers and geometry are read with vector loads
+  // (the table lies in the workspace this kernel writes): uniform() keeps
+  // them, and the buffer resources built from them, in scalar registers
   const int4 tk = reinterpret_cast<const int4*>(table + lay.tasks())[task];
-  const int expert = tk.x;
-  const int first = tk.y;
-  const int nrows = tk.z;
+  const int expert = vq::uniform(tk.x);
+  const int first = vq::uniform(tk.y);
+  const int nrows = vq::uniform(tk.z);
   const int nsub = (nrows + 7) >> 3;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = vq::uniform(tid >> 6);
   const int g = lane >> 4;
   const int m = lane & 15;
   const int L = 4 * (m & 7) + g;
   const int* sorted = table + 4;
   const int64_t* ptrs = routing.ptrs + expert * 9 + projection * 3;
-  const int64_t* meta = routing.meta + expert * 12 + projection * 4;
-  const uint8_t* trellis = reinterpret_cast<const uint8_t*>(ptrs[0]);
-  const uint16_t* svh = reinterpret_cast<const uint16_t*>(ptrs[2]);
+  const int64_t* meta_p = routing.meta + expert * 12 + projection * 4;
+  const int64_t meta[4] = {vq::uniform(meta_p[0]), vq::uniform(meta_p[1]), vq::uniform(meta_p[2]),
+                           vq::uniform(meta_p[3])};
+  const uint8_t* trellis = reinterpret_cast<const uint8_t*>(vq::uniform(ptrs[0]));
+  const uint16_t* svh = reinterpret_cast<const uint16_t*>(vq::uniform(ptrs[2]));
   const int64_t tiles_n = meta[1] / 16;
   const int bits_x2 = kFixed ? kBitsX2 : int(meta[2]);
   const int codebook = kFixed ? 2 : int(meta[3]);
@@ -399,8 +409,9 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
   const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
   const int tile_bytes = 16 * bits_x2;
   const int64_t row_bytes = tiles_n * tile_bytes;
-  const int64_t steps = kp / 32;
-  const int64_t kblocks = kp / 128;
+  // (int: the host keeps the A x kp floats of a region below 2 GiB)
+  const int steps = int(kp / 32);
+  const int kblocks = int(kp / 128);
   // the wavefront's two tiles of tile row 0
   const uint8_t* chunk = trellis + 2 * (4 * int64_t(blockIdx.x) + wave) * tile_bytes;
 
@@ -420,7 +431,7 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
     const int64_t a = sorted[first + min(col >> 1, nrows - 1)];
     st_off[i] = uint32_t((a * 2 * kp + (col & 1) * kp + (c / (4 * kCols)) * 32 + (c / kCols % 4) * 8) * 2);
   }
-  auto stage = [&](int64_t kb, u32x4_t (&v)[kChunks]) {
+  auto stage = [&](int kb, u32x4_t (&v)[kChunks]) {
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       v[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(st_buf, int(st_off[i]),
@@ -455,7 +466,7 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
   const __amdgpu_buffer_rsrc_t tr_buf = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(chunk), 0, int((steps * 2 - 1) * row_bytes + 2 * tile_bytes), 0x00020000);
   uint32_t raw[kDepth][2];
-  auto load_step = [&](int slot, int64_t s) {
+  auto load_step = [&](int slot, int s) {
     if constexpr (kFixed) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -484,12 +495,12 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
   put(0, sv);
   __syncthreads();
 
-  for (int64_t s0 = 0; s0 < steps; s0 += kDepth) {
+  for (int s0 = 0; s0 < steps; s0 += kDepth) {
 #pragma unroll
     for (int i = 0; i < kDepth; ++i) {
-      const int64_t s = s0 + i;
+      const int s = s0 + i;
       if (s < steps) {
-        const int64_t kb = s >> 2;
+        const int kb = s >> 2;
         const int buf = int(kb & 1);
         if ((s & 3) == 0) {
           progress_priority(s, steps);

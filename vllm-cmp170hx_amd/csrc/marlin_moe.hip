@@ -240,7 +240,8 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
   const int b = blockIdx.y;
   const int ks = blockIdx.z;
   if (int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
-  const int e = g.eids[b];
+  // (a vector load: the kernel writes memory the compiler cannot tell apart)
+  const int e = vq::uniform(g.eids[b]);
   if (e < 0 || e >= g.experts) return;
   if (tid < kMaxBlock) {
     int slot = -1;
@@ -537,7 +538,8 @@ __global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direc
   const int b = blockIdx.y;
   const int ks = blockIdx.z;
   if (int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
-  const int e = g.eids[b];
+  // (a vector load: the kernel writes memory the compiler cannot tell apart)
+  const int e = vq::uniform(g.eids[b]);
   if (e < 0 || e >= g.experts) return;
   if (tid < kMaxBlock) {
     int slot = -1;
