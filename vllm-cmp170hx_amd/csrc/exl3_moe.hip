@@ -580,24 +580,47 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
 
 // ---- 5. combine ------------------------------------------------------------------
 
-// One thread per (token, column): each local route's down output (already
-// H128 * svh) times its routing weight, one FMA per route in route order.
+// One workgroup per (token, 256 columns): the token's routes (whether local,
+// the row of the down output, the routing weight) are read once into LDS;
+// each thread then sums its column over the local routes in route order, one
+// FMA each (the reference's order), with the loads of every route in flight
+// together (a route that is not local loads a valid row and is not added:
+// its own row may hold anything).
 __global__ __launch_bounds__(256) void moe_combine(Routing routing, const float* down,
                                                    const float* weights, int64_t rows,
                                                    int64_t hidden, int64_t hpad, void* out,
                                                    int out_dtype, bool any_local) {
-  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= rows * hidden) return;
-  const int64_t r = idx / hidden;
-  const int64_t c = idx - r * hidden;
-  float sum = 0.0f;
-  if (any_local) {
-    for (int64_t k = 0; k < routing.topk; ++k) {
-      const int64_t a = r * routing.topk + k;
-      if (local_expert(routing, a) >= 0) sum = fmaf(down[a * hpad + c], weights[a], sum);
+  constexpr int kRoutes = 32;  // routes staged per round
+  __shared__ int64_t route_row[kRoutes];
+  __shared__ float route_w[kRoutes];
+  __shared__ int route_ok[kRoutes];
+  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const bool mine = c < hidden;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    float sum = 0.0f;
+    if (any_local) {
+      for (int64_t k0 = 0; k0 < routing.topk; k0 += kRoutes) {
+        const int n = int(routing.topk - k0 < kRoutes ? routing.topk - k0 : kRoutes);
+        if (int(threadIdx.x) < n) {
+          const int64_t a = r * routing.topk + k0 + threadIdx.x;
+          const bool ok = local_expert(routing, a) >= 0;
+          route_ok[threadIdx.x] = ok;
+          route_row[threadIdx.x] = ok ? a * hpad : 0;
+          route_w[threadIdx.x] = ok ? weights[a] : 0.0f;
+        }
+        __syncthreads();
+        if (mine) {
+#pragma unroll 8
+          for (int k = 0; k < n; ++k) {
+            const float v = down[route_row[k] + c];
+            sum = route_ok[k] ? fmaf(v, route_w[k], sum) : sum;
+          }
+        }
+        __syncthreads();
+      }
     }
+    if (mine) vq::store_act(out, out_dtype, r * hidden + c, sum);
   }
-  vq::store_act(out, out_dtype, idx, sum);
 }
 
 int64_t padded(int64_t n) { return (n + 127) / 128 * 128; }
@@ -701,8 +724,8 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
     if (int rc = check_launch("exl3 moe_form")) return rc;
     if (int rc = gemv(2, lay.ipad, lay.hpad, lay.act(), lay.input())) return rc;
   }
-  const int64_t elems = rows * hidden;
-  hipLaunchKernelGGL(exl3::moe_combine, dim3(unsigned((elems + 255) / 256)), dim3(256), 0, s,
+  const dim3 combine_grid(unsigned((hidden + 255) / 256), unsigned(std::min<int64_t>(rows, 65535)));
+  hipLaunchKernelGGL(exl3::moe_combine, combine_grid, dim3(256), 0, s,
                      routing, workspace + lay.input(), topk_weights, rows, hidden, lay.hpad, out,
                      out_dtype, any);
   return check_launch("exl3 moe_combine");
