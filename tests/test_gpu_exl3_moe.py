@@ -18,7 +18,10 @@ Cases follow the reference's tests: expert maps with masked, padding and
 out-of-range ids (test_exl3_kernels.py:242-278), every mul1 rate of the
 fixed-rate variant, the SwiGLU clamp at the DeepSeek routed-expert shape
 (test_exl3_moe_swiglu_clamp.py:51-86), empty and fully masked routes, and
-the operator's error checks.
+the operator's error checks; at the benchmark's expert geometry (7168 /
+2048, 3 bits) against the oracle, and the whole 257-expert layer by
+properties that hold at any size (row independence, token order,
+determinism).
 """
 
 import numpy as np
@@ -261,6 +264,90 @@ def test_moe_expert_geometry_mismatch_gives_nan_rows(ops, device):
     bad = (ids[:, 0] == 1)
     assert torch.isnan(out[bad]).all()
     assert torch.isfinite(out[~bad]).all()
+
+
+def test_moe_v2_full_expert_geometry_matches_oracle(ops, device):
+    """The routed-expert geometry of the 3-bit MoE decode workload (hidden
+    7168, intermediate 2048, mul1): four local experts, the last taken by
+    every token as a shared expert with weight 1, with the reference's test
+    scales (svh ~ 0.05 N(0, 1): the +-1 benchmark scales overflow FP16 in the
+    down projection of random weights).  moe_out_v2 against the oracle, and
+    moe_out bitwise."""
+    print("moe_v2 full expert geometry 7168/2048 3-bit", flush=True)
+    rng = np.random.default_rng(7168)
+    hidden, intermediate, experts, rows = 7168, 2048, 4, 4
+    layer = Layer(rng, experts, hidden, intermediate, [(6, 2)], device)
+    routed = np.stack([rng.permutation(experts - 1)[:2] for _ in range(rows)])
+    ids = np.concatenate([routed, np.full((rows, 1), experts - 1)], 1)
+    weights = np.concatenate([rng.random((rows, 2)), np.ones((rows, 1))], 1).astype(np.float32)
+    expert_map = np.arange(experts, dtype=np.int64)
+    x_host, code, x = _acts(rng, rows, hidden, "fp16", device)
+    args = (_dev(ids, device), _dev(weights, device), layer, _dev(expert_map, device), intermediate)
+    fixed = _run(ops, x, *args, bits_x2=6)
+    generic = _run(ops, x, *args)
+    expected = O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map, intermediate,
+                         out_dtype=code)
+    _assert_moe_close(_out_np(fixed), _oracle_f32(expected, code), "full expert geometry")
+    assert torch.equal(fixed.view(torch.int16), generic.view(torch.int16))
+
+
+def test_moe_v2_full_layer_row_independent_and_deterministic(ops, device):
+    """The whole 3-bit MoE layer of the decode workload (256 routed experts +
+    1 shared, hidden 7168, intermediate 2048, top-8 from Zipf(1.1)-skewed
+    logits, 64 tokens), checked by properties that hold at any size: a
+    token's output depends only on its own row and routes (the rows of a
+    task are independent MFMA columns, each with its own scale), so
+    reordering the tokens reorders the outputs bitwise and a token routed
+    alone gets the same bits; two calls agree bitwise; every output is
+    finite and nonzero somewhere."""
+    print("moe_v2 full layer 257 x 7168/2048 3-bit, 64 tokens", flush=True)
+    hidden, intermediate, experts, topk, rows, bits_x2 = 7168, 2048, 256, 8, 64, 6
+    gen = torch.Generator(device=device)
+    gen.manual_seed(64)
+    keep, ptrs, meta = [], [], []
+    for _ in range(experts + 1):
+        p, m = [], []
+        for kk, nn in ((hidden, intermediate), (hidden, intermediate), (intermediate, hidden)):
+            t = torch.randint(-(2 ** 15), 2 ** 15, (kk // 16, nn // 16, 8 * bits_x2), dtype=torch.int16,
+                              device=device, generator=gen)
+            # the reference's test scales (the +-1 benchmark scales overflow
+            # FP16 in the down projection of random weights)
+            u = torch.randn(kk, device=device, generator=gen).half()
+            v = (0.05 * torch.randn(nn, device=device, generator=gen)).half()
+            keep += [t, u, v]
+            p.append([t.data_ptr(), u.data_ptr(), v.data_ptr()])
+            m.append([kk, nn, bits_x2, 2])
+        ptrs.append(p)
+        meta.append(m)
+
+    class Full:
+        pass
+
+    Full.ptrs = torch.tensor(ptrs, dtype=torch.int64, device=device)
+    Full.meta = torch.tensor(meta, dtype=torch.int64, device=device)
+    ranks = torch.randperm(experts, generator=torch.Generator().manual_seed(65)).float() + 1.0
+    logits = torch.randn(rows, experts, generator=gen, device=device) + (-1.1 * torch.log(ranks)).to(device)
+    tw, ti = torch.topk(torch.softmax(logits, -1), topk, dim=-1)
+    tw = tw / tw.sum(-1, keepdim=True)
+    ids = torch.cat([ti.int(), torch.full((rows, 1), experts, dtype=torch.int32, device=device)], 1)
+    weights = torch.cat([tw.float(), torch.ones(rows, 1, device=device)], 1).contiguous()
+    emap = torch.arange(experts + 1, dtype=torch.int32, device=device)
+    x = torch.randn(rows, hidden, generator=gen, device=device).half()
+
+    def call(xx, ii, ww):
+        return _run(ops, xx, ii.contiguous(), ww.contiguous(), Full, emap, intermediate, bits_x2=bits_x2,
+                    poison=False)
+
+    out = call(x, ids, weights)
+    assert torch.isfinite(out.float()).all() and out.float().abs().max() > 0
+    assert torch.equal(out.view(torch.int16), call(x, ids, weights).view(torch.int16))
+    perm = torch.randperm(rows, generator=torch.Generator().manual_seed(66)).to(device)
+    permuted = call(x[perm], ids[perm], weights[perm])
+    assert torch.equal(permuted.view(torch.int16), out[perm].view(torch.int16))
+    for r in (0, 37):
+        alone = call(x[r:r + 1], ids[r:r + 1], weights[r:r + 1])
+        assert torch.equal(alone.view(torch.int16), out[r:r + 1].view(torch.int16)), f"token {r}"
+    del keep
 
 
 def test_moe_rejects_bad_arguments(ops, device):
