@@ -2,7 +2,7 @@
 """Benchmark of the quantized-weight matmul hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
-                    [--no-extras]
+                    [--no-extras] [--only prefill|exl3_moe|marlin]
 
 Headline workload (one "step"): one EXL3 dense linear at the decode-GEMV
 shape, a 4096 x 14336 matrix at 4 bits per weight (bits_x2 8, mul1
@@ -410,6 +410,9 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-extras", action="store_true",
                         help="only the headline GEMV (profiling runs)")
+    parser.add_argument("--only", choices=("prefill", "exl3_moe", "marlin"), default=None,
+                        help="profiling runs: only this workload, its JSON on one line (not the "
+                             "benchmark line)")
     parser.add_argument("--copy-mb", type=int, default=0,
                         help="also run 10 plain device copies of this many MiB (the counter "
                              "calibration of FETCH_SIZE / WRITE_SIZE)")
@@ -423,6 +426,10 @@ def main() -> int:
     import torch
 
     torch.set_num_threads(os.cpu_count() or 1)
+    if args.only:
+        run = {"prefill": gpu_exl3_prefill, "exl3_moe": gpu_exl3_moe, "marlin": gpu_marlin_moe}[args.only]
+        print(json.dumps({args.only: run(torch)}))
+        return 0
     ms, steps, warm = gpu_gemv(args, torch)
     if args.copy_mb:
         src = torch.ones(args.copy_mb << 18, dtype=torch.float32, device="cuda:0")
