@@ -6,10 +6,10 @@
 //  1. prefill_input: one workgroup per row forms t = H128(x * suh) over the
 //     whole row, picks a per-row power-of-two scale from the row maximum, and
 //     writes t as FP16 high and low parts (t * 2^e = hi + lo, ~22 bits).
-//  2. prefill_gemm: 256 x 256 output tiles, 8 wavefronts (4 along M x 2
-//     along N, 64 x 128 each = 2 x 4 v_mfma_f32_32x32x16_f16 tiles).  Per
-//     K step of 32 inputs the workgroup decodes the 32 x 256 weight slab
-//     (32 trellis tiles, two encoder lanes per thread) straight into LDS as
+//  2. prefill_gemm: 256 x 256 output tiles, 16 wavefronts, four per SIMD
+//     (8 along M x 2 along N, 32 x 128 each = 1 x 4 v_mfma_f32_32x32x16_f16
+//     tiles).  Per K step of 32 inputs the workgroup decodes the 32 x 256
+//     weight slab (32 trellis tiles, one encoder lane per thread) straight into LDS as
 //     W^T [n][k] in FP16 (exact values) and stages the activation tiles;
 //     every wavefront accumulates hi * W and lo * W into one FP32
 //     accumulator.  The slab and tiles are double-buffered: step s + 1 is
@@ -35,7 +35,13 @@ namespace {
 constexpr int kBM = 256;            // rows per workgroup
 constexpr int kBN = 256;            // columns per workgroup
 constexpr int kBK = 32;             // inputs per K step (two tile rows)
-constexpr int kGemmThreads = 512;   // 8 wavefronts
+constexpr int kGemmThreads = 1024;  // 16 wavefronts, four per SIMD
+constexpr int kWaves = kGemmThreads / 64;
+constexpr int kBandsM = kWaves / 2;   // wavefronts along M (two 128-column bands along N)
+constexpr int kMT = kBM / kBandsM / 32;                       // 32-row MFMA tiles per wavefront
+constexpr int kTasks = 1024 / kGemmThreads;                   // decode tasks per thread (32 tiles x 32 lanes)
+constexpr int kStageVecs = kBM * 32 * 2 / 16 / kGemmThreads;  // 16-byte activation vectors per thread and tile
+static_assert(kMT >= 1 && kTasks >= 1 && kStageVecs >= 1, "workgroup shape");
 constexpr int kLdsK = kBK + 8;      // LDS row stride in halves (80 bytes)
 
 // ---- 1. activations ----------------------------------------------------------
@@ -125,26 +131,33 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave & 3;           // 64-row band
-  const int wn = wave >> 2;          // 128-column band
+  const int wm = wave % kBandsM;     // row band of kMT 32-row tiles
+  const int wn = wave / kBandsM;     // 128-column band
   const int64_t row0 = int64_t(blockIdx.x) * kBM;
   const int64_t col0 = int64_t(blockIdx.y) * kBN;
   const int64_t tile_col0 = col0 / 16;
   const int steps = int(a.kp / kBK);
 
-  // activation staging: thread t copies 32 bytes of row t >> 1 of each tile
-  const int st_row = tid >> 1;
-  const int st_half = (tid & 1) * 16;  // halves
-  const int64_t src_row = min(row0 + st_row, a.rows - 1);
-  const _Float16* hi_src = a.hi + src_row * a.kp + st_half;
-  const _Float16* lo_src = a.lo + src_row * a.kp + st_half;
-
-  // decode tasks: (tile row tr, tile column tc, encoder lane L), two per thread
-  int task_tr[2], task_tc[2], task_l[2], off[2][kWords];
-  bool task_on[2];
-  const uint8_t* task_src[2];
+  // activation staging: thread t copies 16-byte vectors t + kGemmThreads v of
+  // each tile (row = vector / 4, halves 8 (vector % 4) ..)
+  int st_off[kStageVecs];
+  const _Float16* hi_src[kStageVecs];
+  const _Float16* lo_src[kStageVecs];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int v = 0; v < kStageVecs; ++v) {
+    const int vec = tid + kGemmThreads * v;
+    st_off[v] = (vec >> 2) * kLdsK + 8 * (vec & 3);
+    const int64_t src_row = min(row0 + (vec >> 2), a.rows - 1);
+    hi_src[v] = a.hi + src_row * a.kp + 8 * (vec & 3);
+    lo_src[v] = a.lo + src_row * a.kp + 8 * (vec & 3);
+  }
+
+  // decode tasks: (tile row tr, tile column tc, encoder lane L), kTasks per thread
+  int task_tr[kTasks], task_tc[kTasks], task_l[kTasks], off[kTasks][kWords];
+  bool task_on[kTasks];
+  const uint8_t* task_src[kTasks];
+#pragma unroll
+  for (int i = 0; i < kTasks; ++i) {
     const int task = tid + kGemmThreads * i;
     const int tile = task >> 5;
     task_tr[i] = tile >> 4;
@@ -160,26 +173,26 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
   }
   const int64_t step_bytes = 2 * a.tiles_n * R::kTileBytes;  // two tile rows
 
-  f32x16_t acc[2][4];
+  f32x16_t acc[kMT][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kMT; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
 
   // two register slots of fetched step data: slot s & 1 holds step s, loaded
   // two steps before it is decoded
-  uint32_t words[2][2][kWords];
-  u32x4_t hv[2][2], lv[2][2];
+  uint32_t words[2][kTasks][kWords];
+  u32x4_t hv[2][kStageVecs], lv[2][kStageVecs];
   auto fetch = [&](int slot, int step) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kTasks; ++i)
 #pragma unroll
       for (int w = 0; w < kWords; ++w)
         words[slot][i][w] = tile_word<kAligned>(task_src[i] + step * step_bytes, off[i][w]);
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      hv[slot][v] = *reinterpret_cast<const u32x4_t*>(hi_src + int64_t(step) * kBK + 8 * v);
-      lv[slot][v] = *reinterpret_cast<const u32x4_t*>(lo_src + int64_t(step) * kBK + 8 * v);
+    for (int v = 0; v < kStageVecs; ++v) {
+      hv[slot][v] = *reinterpret_cast<const u32x4_t*>(hi_src[v] + int64_t(step) * kBK);
+      lv[slot][v] = *reinterpret_cast<const u32x4_t*>(lo_src[v] + int64_t(step) * kBK);
     }
   };
   // decode task i of the step in register slot `slot` into W buffer `buf`
@@ -199,19 +212,19 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
   };
   auto stage = [&](int slot, int buf) {
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      *reinterpret_cast<u32x4_t*>(hi_lds[buf] + st_row * kLdsK + st_half + 8 * v) = hv[slot][v];
-      *reinterpret_cast<u32x4_t*>(lo_lds[buf] + st_row * kLdsK + st_half + 8 * v) = lv[slot][v];
+    for (int v = 0; v < kStageVecs; ++v) {
+      *reinterpret_cast<u32x4_t*>(hi_lds[buf] + st_off[v]) = hv[slot][v];
+      *reinterpret_cast<u32x4_t*>(lo_lds[buf] + st_off[v]) = lv[slot][v];
     }
   };
   // the MFMAs of one k16 chunk of buffer `buf`: A = activations (rows l % 32,
   // k 8 (l / 32) + i), B = W (k 8 (l / 32) + i, columns l % 32)
   auto mfma_chunk = [&](int buf, int kc) {
     const int ko = kc * 16 + 8 * (lane >> 5);
-    half8_t ah[2], al[2], b[4];
+    half8_t ah[kMT], al[kMT], b[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int m = wm * 64 + i * 32 + (lane & 31);
+    for (int i = 0; i < kMT; ++i) {
+      const int m = wm * 32 * kMT + i * 32 + (lane & 31);
       ah[i] = *reinterpret_cast<const half8_t*>(hi_lds[buf] + m * kLdsK + ko);
       al[i] = *reinterpret_cast<const half8_t*>(lo_lds[buf] + m * kLdsK + ko);
     }
@@ -221,7 +234,7 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
       b[j] = *reinterpret_cast<const half8_t*>(w_lds[buf] + n * kLdsK + ko);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kMT; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
@@ -236,8 +249,8 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
   const int last = steps - 1;
   fetch(0, 0);
   fetch(1, min(1, last));
-  decode_task(0, 0, 0);
-  decode_task(0, 0, 1);
+#pragma unroll
+  for (int i = 0; i < kTasks; ++i) decode_task(0, 0, i);
   stage(0, 0);
   fetch(0, min(2, last));
   __syncthreads();
@@ -252,7 +265,8 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
     if (more) decode_task(nslot, buf ^ 1, 0);
     mfma_chunk(buf, 1);
     if (more) {
-      decode_task(nslot, buf ^ 1, 1);
+#pragma unroll
+      for (int i = 1; i < kTasks; ++i) decode_task(nslot, buf ^ 1, i);
       stage(nslot, buf ^ 1);
     }
     fetch(nslot, min(step + 3, last));
@@ -271,10 +285,10 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
   // the standalone transform), times svh, rounded to the output dtype.
   const int64_t band = col0 + wn * 128;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kMT; ++i) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int64_t row = row0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const int64_t row = row0 + wm * 32 * kMT + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
       const int e = a.row_exp[row < a.rows ? row : a.rows - 1];
       float v[4];
 #pragma unroll
