@@ -243,7 +243,40 @@ __device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int 
   const int stride_bytes = 4 * a.rows * int(a.np);
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       a.partial + base, 0, (a.splits - 1) * stride_bytes + 4 * ((a.rows - 1) * int(a.np) + 128), 0x00020000);
-  for (int r = 0; r < a.rows && tid < 256; ++r) {
+  if (a.splits <= 32 && tid < 256) {
+    // one round of 16 loads per row (the split index clamped to a valid one,
+    // the extra terms not added), the next row's loads issued before this
+    // row's sum: rows one memory round trip apart in the pipeline, not one
+    // round trip each
+    auto load_row = [&](int r, float (&t)[16]) {
+      const int voff = 4 * (r * int(a.np) + col);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int sp = min(part + 2 * u, a.splits - 1);
+        t[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff, sp * stride_bytes,
+                                                                              kCachePolicySc1));
+      }
+    };
+    auto sum_row = [&](int r, const float (&t)[16]) {
+      float v = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        if (part + 2 * u < a.splits) v += t[u];
+      }
+      red[(part * a.rows + r) * 128 + col] = v;
+    };
+    float ta[16], tb[16];
+    load_row(0, ta);
+    for (int r = 0; r < a.rows; r += 2) {
+      load_row(min(r + 1, a.rows - 1), tb);
+      sum_row(r, ta);
+      if (r + 1 < a.rows) {
+        load_row(min(r + 2, a.rows - 1), ta);
+        sum_row(r + 1, tb);
+      }
+    }
+  }
+  for (int r = 0; a.splits > 32 && r < a.rows && tid < 256; ++r) {
     const int voff = 4 * (r * int(a.np) + col);
     float v = 0.0f;
     // 16 loads in flight (32 splits) per round, split order
