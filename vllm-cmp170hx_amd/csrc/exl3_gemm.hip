@@ -258,23 +258,25 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
   // of step s + 1 (register slot (s + 1) & 1) into the other buffer, then the
   // fetch of step s + 3 into the slot just decoded.  Steps run in pairs so the
   // buffer and slot indices are constants (registers cannot be indexed).
+  //   The body has no branch: steps is a multiple of 4 (kp of whole
+  //   128-input blocks), and after the last step the decode and staging of
+  //   the clamped step land in the buffer no MFMA reads again.  (A branch
+  //   here leaves the compiler unsure of the loads in flight where the paths
+  //   meet, and it then waits for the prefetch of the step after as well.)
   auto iteration = [&](int step, int buf) {
     const int nslot = buf ^ 1;
-    const bool more = step + 1 < steps;
     mfma_chunk(buf, 0);
-    if (more) decode_task(nslot, buf ^ 1, 0);
+    decode_task(nslot, buf ^ 1, 0);
     mfma_chunk(buf, 1);
-    if (more) {
 #pragma unroll
-      for (int i = 1; i < kTasks; ++i) decode_task(nslot, buf ^ 1, i);
-      stage(nslot, buf ^ 1);
-    }
+    for (int i = 1; i < kTasks; ++i) decode_task(nslot, buf ^ 1, i);
+    stage(nslot, buf ^ 1);
     fetch(nslot, min(step + 3, last));
     __syncthreads();
   };
   for (int step = 0; step < steps; step += 2) {
     iteration(step, 0);
-    if (step + 1 < steps) iteration(step + 1, 1);
+    iteration(step + 1, 1);
   }
 
   // epilogue, the output transform fused: lane l, register r of tile (i, j)
