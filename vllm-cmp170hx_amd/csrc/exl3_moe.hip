@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 #include "../../include/vllm_mi355x.h"
 #include "common.h"
@@ -352,7 +353,9 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
                                                 MoeLayout lay, int64_t in_offset,
                                                 int64_t out_offset) {
   constexpr bool kFixed = kBitsX2 > 0;
-  constexpr int kDepth = 6;  // steps of trellis loads in flight
+  // steps of trellis loads in flight: one B block, so the loop body below
+  // is one block with no branch around a load (steps is a multiple of 4)
+  constexpr int kDepth = 4;
   constexpr int kRows = task_rows(kBitsX2);
   constexpr int kSub = kRows / 8;
   constexpr int kCols = 2 * kRows;
@@ -466,12 +469,15 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
   const __amdgpu_buffer_rsrc_t tr_buf = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(chunk), 0, int((steps * 2 - 1) * row_bytes + 2 * tile_bytes), 0x00020000);
   uint32_t raw[kDepth][2];
-  auto load_step = [&](int slot, int s) {
+  // (the alignment is a compile-time branch of the stream below: with a
+  // run-time branch in the loop the compiler, unsure of the loads in flight
+  // where the paths meet, waits for all of them before each use)
+  auto load_step = [&](auto aligned_tag, int slot, int s) {
     if constexpr (kFixed) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int row = int((2 * s + h) * row_bytes);
-        if (aligned) {
+        if constexpr (decltype(aligned_tag)::value) {
           raw[slot][h] = __builtin_amdgcn_raw_buffer_load_b32(tr_buf, raw_off, row, 0);
         } else {
           raw[slot][h] = uint32_t(__builtin_amdgcn_raw_buffer_load_b16(tr_buf, raw_off, row, 0)) |
@@ -485,64 +491,76 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
 #pragma unroll
   for (int sb = 0; sb < kSub; ++sb) acc1[sb] = acc2[sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // prologue: block 0's B operands, the first kDepth steps of trellis
-  u32x4_t sv[kChunks];
-  stage(0, sv);
-#pragma unroll
-  for (int i = 0; i < kDepth; ++i) {
-    if (i < steps) load_step(i, i);
-  }
-  put(0, sv);
-  __syncthreads();
+  auto stream = [&](auto aligned_tag) {
+    // prologue: block 0's B operands, the first kDepth steps of trellis
+    u32x4_t sv[kChunks];
+    stage(0, sv);
+  #pragma unroll
+    for (int i = 0; i < kDepth; ++i) load_step(aligned_tag, i, min(i, steps - 1));
+    put(0, sv);
+    __syncthreads();
 
-  for (int s0 = 0; s0 < steps; s0 += kDepth) {
-#pragma unroll
-    for (int i = 0; i < kDepth; ++i) {
-      const int s = s0 + i;
-      if (s < steps) {
-        const int kb = s >> 2;
-        const int buf = int(kb & 1);
-        if ((s & 3) == 0) {
-          progress_priority(s, steps);
-          if (kb + 1 < kblocks) stage(kb + 1, sv);
-        }
-        uint32_t q0[4], q1[4];
-        if constexpr (kFixed) {
-          uint32_t w0[kWords], w1[kWords];
-#pragma unroll
-          for (int k = 0; k < kWords; ++k) {
-            w0[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][0])));
-            w1[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][1])));
+    // one 128-input block (4 steps) per iteration, branch-free around the
+    // loads: the last block re-stages itself into the buffer no step reads
+    // again, and the trellis loads past the end reload the last step
+    for (int s0 = 0; s0 < steps; s0 += kDepth) {
+  #pragma unroll
+      for (int i = 0; i < kDepth; ++i) {
+        const int s = s0 + i;
+        {
+          const int kb = s >> 2;
+          const int buf = int(kb & 1);
+          if (i == 0) {
+            progress_priority(s, steps);
+            stage(min(kb + 1, kblocks - 1), sv);
           }
-          if (s + kDepth < steps) load_step(i, s + kDepth);
-          decode_words<kBitsX2, 2>(L, w0, q0);
-          decode_words<kBitsX2, 2>(L, w1, q1);
-        } else {
-          const uint8_t* t0 = chunk + (2 * s) * row_bytes + (m >> 3) * tile_bytes;
-          decode_runtime(t0, aligned, bits_x2, codebook, L, q0);
-          decode_runtime(t0 + row_bytes, aligned, bits_x2, codebook, L, q1);
-        }
-        const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
-        const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
-        // every sub-block's B operand in one batch of LDS reads (the staged
-        // columns past the task hold its last row: valid data), then the
-        // MFMAs of the task's sub-blocks
-        half8_t b[kSub];
-#pragma unroll
-        for (int sb = 0; sb < kSub; ++sb) b[sb] = *reinterpret_cast<const half8_t*>(&bop[buf][s & 3][g][16 * sb + m][0]);
-#pragma unroll
-        for (int sb = 0; sb < kSub; ++sb) {
-          if (sb < nsub) {
-            acc1[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), b[sb], acc1[sb], 0, 0, 0);
-            acc2[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), b[sb], acc2[sb], 0, 0, 0);
+          uint32_t q0[4], q1[4];
+          if constexpr (kFixed) {
+            uint32_t w0[kWords], w1[kWords];
+  #pragma unroll
+            for (int k = 0; k < kWords; ++k) {
+              w0[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][0])));
+              w1[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][1])));
+            }
+            load_step(aligned_tag, i, min(s + kDepth, steps - 1));
+            decode_words<kBitsX2, 2>(L, w0, q0);
+            decode_words<kBitsX2, 2>(L, w1, q1);
+          } else {
+            const uint8_t* t0 = chunk + (2 * s) * row_bytes + (m >> 3) * tile_bytes;
+            decode_runtime(t0, aligned, bits_x2, codebook, L, q0);
+            decode_runtime(t0 + row_bytes, aligned, bits_x2, codebook, L, q1);
           }
-        }
-        if ((s & 3) == 3) {
-          if (kb + 1 < kblocks) put(buf ^ 1, sv);
-          __syncthreads();
+          const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
+          const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
+          // every sub-block's B operand in one batch of LDS reads (the staged
+          // columns past the task hold its last row: valid data), then the
+          // MFMAs of the task's sub-blocks
+          half8_t b[kSub];
+  #pragma unroll
+          for (int sb = 0; sb < kSub; ++sb) b[sb] = *reinterpret_cast<const half8_t*>(&bop[buf][s & 3][g][16 * sb + m][0]);
+  #pragma unroll
+          for (int sb = 0; sb < kSub; ++sb) {
+            if (sb < nsub) {
+              acc1[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), b[sb], acc1[sb], 0, 0, 0);
+              acc2[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), b[sb], acc2[sb], 0, 0, 0);
+            }
+          }
+          if (i == 3) {
+            put(buf ^ 1, sv);
+            __syncthreads();
+          }
         }
       }
     }
+  };
+  if constexpr (kFixed) {
+    if (aligned) {
+      stream(std::true_type{});
+    } else {
+      stream(std::false_type{});
+    }
+  } else {
+    stream(std::true_type{});  // the run-time decode reads the tiles itself
   }
 
   // epilogue: high + low parts (adjacent lanes) unscaled per row, the rows'
