@@ -44,16 +44,26 @@ int vllm_mi355x_abi_version(void);
 /* ---- EXL3 ---------------------------------------------------------------- */
 
 /*
- * FP32 workspace elements exl3_linear_out needs for up to max_rows rows of
- * a padded_in x padded_out matrix: max_rows * (padded_in + padded_out + 1)
- * (large-M path: FP16 high/low activations, FP32 core result, one row
- * exponent per row) plus min(max_rows, 8) * (padded_in / 128) * padded_out
- * for the K-split partial sums of the small-M kernel.  Returns -1 (with an error message)
- * for a negative row count or padded sizes that are not positive multiples
- * of 128.
+ * FP32 workspace elements exl3_linear_out needs for calls of up to max_rows
+ * rows of a padded_in x padded_out matrix: the larger of the small-M path's
+ * K-split partial sums, min(max_rows, 8) * splits * padded_out (splits =
+ * padded_in / 128 / blocks, with the automatic blocks per workgroup, at most
+ * 32 where the shape allows), and, above exl3_linear_prefill_rows() rows,
+ * the large-M path's max_rows * (padded_in + 1) (FP16 high/low activations,
+ * one row exponent per row).  The two paths never run in one call.  Returns
+ * -1 (with an error message) for a negative row count or padded sizes that
+ * are not positive multiples of 128.
  * Replaces _exl3_C::linear_workspace_size (csrc/exl3/dense.cu:72-78).
  */
 int64_t exl3_linear_workspace_size(int64_t max_rows, int64_t padded_in, int64_t padded_out);
+
+/*
+ * The row count above which exl3_linear_out runs the large-M (prefill) GEMM;
+ * up to it, the small-M kernel in chunks of 8 rows.  The reference's routing
+ * question _exl3_C::linear_prefill_applies (vllm_sm80/kernels/exl3/
+ * dense_prefill_tc.py:57-80) answers from it.
+ */
+int exl3_linear_prefill_rows(void);
 
 /*
  * out[r][n] = RN_out( H128(C[r])[n] * svh[n] ),
@@ -72,7 +82,9 @@ int64_t exl3_linear_workspace_size(int64_t max_rows, int64_t padded_in, int64_t 
  * The weights are decoded bit-exactly; the products are summed in FP32 on
  * the matrix cores, with the activations split into FP16 high and low parts
  * (about 22 significant bits), so the result agrees with the reference's
- * sequential FP32 chain to FP32 rounding, not bit for bit.
+ * sequential FP32 chain to FP32 rounding, not bit for bit.  A small-M call
+ * whose K-split partials (under a forced exl3_set_gemv_blocks, or an
+ * unaligned trellis) exceed the workspace runs in column ranges that fit.
  * Replaces _exl3_C::linear_out (csrc/exl3/dense.cu:80-149; schema
  * csrc/exl3/module.cpp:13-15).
  */
@@ -109,9 +121,11 @@ int64_t exl3_moe_workspace_size(int64_t max_rows, int64_t hidden_size, int64_t i
  * packed_ptrs [local][3][3] device addresses {trellis, suh, svh} of gate,
  * up, down, packed_meta [local][3][4] {padded_in, padded_out, bits_x2,
  * codebook} (the caller keeps the matrices alive).  bits_x2 = 0 decodes
- * every expert's own format (moe_out); bits_x2 = 2..8 is the layer's one
- * mul1 rate (moe_out_v2).  An expert whose matrices are not hpad x ipad /
- * ipad x hpad, or (bits_x2 > 0) not of that rate, yields NaN rows.
+ * every expert's own format (moe_out); bits_x2 = 2..16 is the layer's one
+ * mul1 rate (moe_out_v2; 2..8 run a decode specialized for the rate, 10..16
+ * the run-time decode).  An expert whose matrices are not hpad x ipad /
+ * ipad x hpad, or (bits_x2 > 0) not of that rate, yields NaN rows.  Every
+ * argument check runs before the first launch.
  * Replaces _exl3_C::moe_out (csrc/exl3/moe.cu:450-458) and
  * _exl3_C::moe_out_v2 (csrc/exl3/moe_v2.h:19-30; schema module.cpp:19-26).
  */
@@ -126,9 +140,11 @@ int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hidden, const
  * Test and tuning switch, process-wide: how exl3_linear_out finishes its
  * small-M (<= 8 rows) launches.  -1 (default): the last workgroup of each
  * 128-column block sums the K-split partials and writes the outputs, using
- * one bank of arrival counters per stream (64 per device; streams beyond
- * that use the separate kernel); 0: always a separate output kernel; 1: as
- * -1.  Both finishes add in the same order, so results are bitwise equal.
+ * arrival counters from a static pool of 128 ranges per device, one range
+ * per (stream, graph capture) so launches that may overlap never share one
+ * (once the ranges are spent, later streams and captures use the separate
+ * kernel); 0: always a separate output kernel; 1: as -1.  Both finishes add
+ * in the same order, so results are bitwise equal.
  * No counterpart in the reference (its nearest is the test-only
  * set_gemm_shape_override, csrc/exl3/gemm.cu:400-409).
  */
@@ -163,6 +179,24 @@ int exl3_set_gemv_groups(int groups);
  */
 int exl3_decode(const void* trellis, int64_t tiles_k, int64_t tiles_n, int64_t trellis_words,
                 int64_t bits_x2, int64_t codebook, void* out, void* stream);
+
+/*
+ * Selected rows of an EXL3 PLE table (trellis-compressed embeddings), BF16:
+ * packed_rows int16 [rows][words], words = 1 + dim * bits / 16 (an FP16
+ * scale, then a little-endian ring of dim * bits bits); channel c's state
+ * takes bit m from ring bit ((c - m / bits) mod dim) * bits + m % bits; the
+ * value is RN_bf16(RN32(RN16(RN32(RN32(1024 + bytesum(state * 0x83DCD12D)) *
+ * fp16(0x1EEE)) + fp16(0xC931))) * scale) + head_bias[head][c]) for a row
+ * whose global id lies in [owner_lo, owner_hi) and inside the vocabulary of
+ * the last head starting at or before it (head_offsets / head_vocab_sizes
+ * int64 [heads], head_bias fp16 [heads][dim]); every other row is zero.
+ * Replaces _exl3_C::ple_decode_out (csrc/exl3/ple.cu:167-234; schema
+ * csrc/exl3/module.cpp:30-32).
+ */
+int exl3_ple_decode_out(const void* packed_rows, int64_t rows, int64_t words,
+                        const int64_t* global_ids, const void* head_bias, int64_t heads,
+                        const int64_t* head_offsets, const int64_t* head_vocab_sizes, int64_t dim,
+                        int64_t owner_lo, int64_t owner_hi, int64_t bits, void* out, void* stream);
 
 /* ---- Marlin-format int4 fused MoE ------------------------------------------
  *
@@ -260,6 +294,16 @@ int marlin_dequant(const int32_t* w, const void* scales, int act_dtype, int64_t 
  */
 int moe_sum(const void* in, int act_dtype, int64_t tokens, int64_t topk, int64_t hidden,
             const int32_t* ids, int64_t experts, void* out, void* stream);
+
+/*
+ * The routed sum with the shared expert's output folded in, one launch:
+ * out[t][c] = RN(f32(RN(FP32 sum over slots in order of in[t][k][c])) +
+ * f32(shared[t * shared_stride0 + c * shared_stride1])) (element strides).
+ * Replaces moe_sum_add (vllm_sm80/kernels/moe/sum.py:18-56).
+ */
+int moe_sum_add(const void* in, int act_dtype, int64_t tokens, int64_t topk, int64_t hidden,
+                const void* shared, int64_t shared_stride0, int64_t shared_stride1, void* out,
+                void* stream);
 
 /*
  * Deterministic block alignment of routed rows: rows grouped by (mapped)

@@ -19,8 +19,9 @@
 //     H128 over each wavefront's 128-column band (one H128 block), times
 //     svh, rounded to the output dtype.
 //
-// Workspace (FP32 elements, rows x ...): [hi | lo halves: padded_in][padded_out,
-// unused] and one int row exponent per row after them.
+// Workspace (FP32 elements): rows x padded_in floats holding the FP16 high
+// halves [rows][padded_in] then the low halves, and one int row exponent per
+// row after them.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -354,9 +355,7 @@ int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trel
   if (rows > 65535 * int64_t(kBM)) return vq::fail("EXL3 linear has too many rows");
   _Float16* hi = reinterpret_cast<_Float16*>(workspace);
   _Float16* lo = hi + rows * kp;
-  // (the FP32 core result region between them is not used: the GEMM
-  // applies the output transform itself)
-  int* row_exp = reinterpret_cast<int*>(workspace + rows * kp + rows * np);
+  int* row_exp = reinterpret_cast<int*>(workspace + rows * kp);
   hipLaunchKernelGGL(prefill_input, dim3(unsigned(rows)), dim3(256), 0, stream, x, x_dtype,
                      logical_in, kp, suh, hi, lo, row_exp);
   if (int rc = vq::check_launch("exl3 prefill_input")) return rc;

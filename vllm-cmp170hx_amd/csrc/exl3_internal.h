@@ -57,9 +57,10 @@ __device__ __forceinline__ float u16_act(uint16_t v, int dtype) {
   return dtype == vq::kBF16 ? vq::bf16_to_f32(v) : vq::f16_to_f32(v);
 }
 
-// Large-M (prefill) dense linear, rows > 8 (exl3_gemm.hip).  Arguments as
-// exl3_linear_out's, validated by it; workspace holds rows * (padded_in +
-// padded_out) floats plus the row exponents.
+// Large-M (prefill) dense linear, rows > 32 (exl3_gemm.hip).  Arguments as
+// exl3_linear_out's, validated by it; workspace holds rows * padded_in
+// floats (the FP16 high and low activation halves) plus one int32 row
+// exponent per row.
 int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trellis,
                    int64_t tiles_k, int64_t tiles_n, const uint16_t* suh, const uint16_t* svh,
                    int bits_x2, int codebook, int64_t logical_in, int64_t logical_out, void* out,
@@ -68,6 +69,7 @@ int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trel
 // The finish of exl3_linear_out: out = RN(H128(sum of `splits` partial rows)
 // * svh) for every (row, 128-column block) (exl3_linear.hip).
 int launch_output(const float* partial, int splits, int rows, int64_t np, const uint16_t* svh,
-                  int64_t logical_out, void* out, int out_dtype, hipStream_t stream);
+                  int64_t logical_out, int64_t out_stride, void* out, int out_dtype,
+                  hipStream_t stream);
 
 }  // namespace exl3

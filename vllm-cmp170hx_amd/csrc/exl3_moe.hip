@@ -46,6 +46,11 @@ constexpr int64_t kMaxRouteExperts = 4096;
 // registers the extra accumulators would take: 8 rows there.
 constexpr int kTaskRows = 32;
 constexpr int task_rows(int bits_x2) { return bits_x2 > 0 ? kTaskRows : 8; }
+// The rate of the fixed-rate GEMV serving a call's bits_x2 (moe_out_v2's
+// 2..8, decoded by specialized kernels), or 0: the run-time-format decode,
+// which serves moe_out (any admitted format per expert) and moe_out_v2 at
+// 10..16 (checked per expert against the layer's rate).
+constexpr int fixed_rate(int64_t bits_x2) { return bits_x2 >= 2 && bits_x2 <= 8 ? int(bits_x2) : 0; }
 
 // Routing of one call (reference: csrc/exl3/moe.cu:19-55).
 struct Routing {
@@ -347,11 +352,13 @@ __device__ __forceinline__ void progress_priority(int step, int steps) {
 // high and low parts); the sums run over the whole row (one scale per
 // assignment row) and fold once.
 // kBitsX2 = 0: the expert's format at run time.
+// want_bits (run-time decode only): the layer's mul1 rate every expert must
+// have (moe_out_v2 above 4 bits), or 0 for any admitted format (moe_out).
 template <int kBitsX2>
 __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing routing, int projection, int64_t kp,
                                                 int64_t np, const int* table, float* ws,
                                                 MoeLayout lay, int64_t in_offset,
-                                                int64_t out_offset) {
+                                                int64_t out_offset, int want_bits) {
   constexpr bool kFixed = kBitsX2 > 0;
   // steps of trellis loads in flight: one B block, so the loop body below
   // is one block with no branch around a load (steps is a multiple of 4)
@@ -398,9 +405,10 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
   // admitted format) would be read out of bounds: its rows get NaN instead.
   const bool bad = meta[0] != kp || meta[1] != np ||
                    (kFixed ? (meta[2] != kBitsX2 || meta[3] != 2)
-                           : !(meta[3] == 1 ? (bits_x2 >= 2 && bits_x2 <= 16 && bits_x2 % 2 == 0)
-                                            : (meta[3] == 2 && bits_x2 >= 2 && bits_x2 <= 16 &&
-                                               (bits_x2 % 2 == 0 || bits_x2 <= 7))));
+                           : (want_bits > 0 && (meta[2] != want_bits || meta[3] != 2)) ||
+                                 !(meta[3] == 1 ? (bits_x2 >= 2 && bits_x2 <= 16 && bits_x2 % 2 == 0)
+                                                : (meta[3] == 2 && bits_x2 >= 2 && bits_x2 <= 16 &&
+                                                   (bits_x2 % 2 == 0 || bits_x2 <= 7))));
   if (bad) {
     for (int r = wave; r < nrows; r += 4) {
       float* dst = ws + out_offset + int64_t(table[4 + first + r]) * np + 128 * int64_t(blockIdx.x);
@@ -705,29 +713,31 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   exl3::Routing routing{topk_ids, expert_map, packed_ptrs, packed_meta, global_experts,
                         local_experts, topk, ids64 != 0, map64 != 0};
   const bool any = local_experts > 0 && assignments > 0;
+  // every check before the first launch
+  const int fixed = exl3::fixed_rate(bits_x2);
+  const int task_rows = exl3::task_rows(fixed);
+  const int64_t max_tasks =
+      std::min<int64_t>(assignments, (assignments + task_rows - 1) / task_rows + local_experts);
+  if (any && max_tasks > 65535) return fail("EXL3 MoE has too many routed assignments");
   if (any) {
     int* table = reinterpret_cast<int*>(workspace + lay.ints());
-    const int task_rows = exl3::task_rows(int(bits_x2));
     hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads),
                        size_t(3 * local_experts + 1) * sizeof(int), s, routing, assignments, task_rows,
                        table);
     if (int rc = check_launch("exl3 moe_route")) return rc;
-    const int64_t max_tasks =
-        std::min<int64_t>(assignments, (assignments + task_rows - 1) / task_rows + local_experts);
-    if (max_tasks > 65535) return fail("EXL3 MoE has too many routed assignments");
+    const int want_bits = fixed == 0 ? int(bits_x2) : 0;
     auto gemv = [&](int projection, int64_t kp, int64_t np, int64_t in_off, int64_t out_off) {
       const dim3 grid(unsigned(np / 128), unsigned(max_tasks));
-      switch (bits_x2) {
-#define VQ_MOE(B) case B: hipLaunchKernelGGL(exl3::moe_gemv<B>, grid, dim3(256), 0, s, routing, projection, kp, np, table, workspace, lay, in_off, out_off); break;
+      switch (fixed) {
+#define VQ_MOE(B) case B: hipLaunchKernelGGL(exl3::moe_gemv<B>, grid, dim3(256), 0, s, routing, projection, kp, np, table, workspace, lay, in_off, out_off, 0); break;
         VQ_MOE(2) VQ_MOE(3) VQ_MOE(4) VQ_MOE(5) VQ_MOE(6) VQ_MOE(7) VQ_MOE(8)
 #undef VQ_MOE
         default:
           hipLaunchKernelGGL(exl3::moe_gemv<0>, grid, dim3(256), 0, s, routing, projection, kp, np,
-                             table, workspace, lay, in_off, out_off);
+                             table, workspace, lay, in_off, out_off, want_bits);
       }
       return check_launch("exl3 moe_gemv");
     };
-    if (bits_x2 > 8) return fail("EXL3 MoE v2 supports mul1 rates up to 4 bits");
     // moe_form: one workgroup per assignment (the routed ones do work)
     const int64_t form_h = assignments;
     const int64_t form_i = assignments;

@@ -947,10 +947,15 @@ __device__ __forceinline__ float act_f32(uint16_t v) {
 }
 
 // kVec columns per thread (8 with 16-byte loads when hidden % 8 == 0, else 1).
+// With `shared` (the shared expert's output, element strides sh0 / sh1; sh1
+// == 1 when kVec == 8): out[t][c] = RN(f32(RN(sum)) + f32(shared[t][c])), the
+// routed sum rounded as moe_sum stores it, then one rounded add
+// (vllm_sm80/kernels/moe/sum.py:18-56).
 template <bool kBF16, int kVec>
 __global__ __launch_bounds__(kThreads) void moe_sum_kernel(const uint16_t* in, int topk, int64_t hidden,
                                                            const int32_t* ids, int experts,
-                                                           uint16_t* out) {
+                                                           const uint16_t* shared, int64_t sh0,
+                                                           int64_t sh1, uint16_t* out) {
   const int64_t t = blockIdx.y;
   const int64_t c = (int64_t(blockIdx.x) * kThreads + threadIdx.x) * kVec;
   if (c >= hidden) return;
@@ -970,6 +975,18 @@ __global__ __launch_bounds__(kThreads) void moe_sum_kernel(const uint16_t* in, i
     } else {
       acc[0] += act_f32<kBF16>(row[0]);
     }
+  }
+  if (shared) {
+    float sh[kVec];
+    if constexpr (kVec == 8) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(shared + t * sh0 + c);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sh[u] = act_f32<kBF16>(uint16_t(v[u >> 1] >> (16 * (u & 1))));
+    } else {
+      sh[0] = act_f32<kBF16>(shared[t * sh0 + c * sh1]);
+    }
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) acc[u] = act_f32<kBF16>(to_act<kBF16>(acc[u])) + sh[u];
   }
   if constexpr (kVec == 8) {
     u32x4_t o;
@@ -1414,30 +1431,53 @@ extern "C" int marlin_dequant(const int32_t* w, const void* scales, int act_dtyp
   return check_launch("marlin_dequant");
 }
 
-extern "C" int moe_sum(const void* in, int act_dtype, int64_t tokens, int64_t topk, int64_t hidden,
-                       const int32_t* ids, int64_t experts, void* out, void* stream) {
+namespace marlin {
+namespace {
+
+int launch_moe_sum(const void* in, int act_dtype, int64_t tokens, int64_t topk, int64_t hidden,
+                   const int32_t* ids, int64_t experts, const void* shared, int64_t sh0, int64_t sh1,
+                   void* out, void* stream, const char* what) {
   using namespace vq;
-  if (act_dtype != kBF16 && act_dtype != kFP16) return fail("moe_sum: bf16 or fp16");
+  if (act_dtype != kBF16 && act_dtype != kFP16) return fail(std::string(what) + ": bf16 or fp16");
   if (tokens < 0 || tokens > 65535 || topk <= 0 || hidden <= 0 || experts < 0 || experts > INT_MAX ||
       topk > INT_MAX) {
-    return fail("moe_sum: sizes out of range");
+    return fail(std::string(what) + ": sizes out of range");
   }
   if (tokens == 0) return kOk;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const auto* ip = static_cast<const uint16_t*>(in);
+  const auto* sp = static_cast<const uint16_t*>(shared);
   auto* op = static_cast<uint16_t*>(out);
-  const bool vec = hidden % 8 == 0 && marlin::aligned16(in) && marlin::aligned16(out);
-  const int64_t per_block = int64_t(marlin::kThreads) * (vec ? 8 : 1);
+  const bool vec = hidden % 8 == 0 && aligned16(in) && aligned16(out) &&
+                   (!shared || (sh1 == 1 && sh0 % 8 == 0 && aligned16(shared)));
+  const int64_t per_block = int64_t(kThreads) * (vec ? 8 : 1);
   const dim3 grid(unsigned((hidden + per_block - 1) / per_block), unsigned(tokens));
-#define VQ_SUM(B, V) hipLaunchKernelGGL((marlin::moe_sum_kernel<B, V>), grid, dim3(marlin::kThreads), 0, s, \
-                                        ip, int(topk), hidden, ids, int(experts), op)
+#define VQ_SUM(B, V) hipLaunchKernelGGL((moe_sum_kernel<B, V>), grid, dim3(kThreads), 0, s, \
+                                        ip, int(topk), hidden, ids, int(experts), sp, sh0, sh1, op)
   if (act_dtype == kBF16) {
     if (vec) VQ_SUM(true, 8); else VQ_SUM(true, 1);
   } else {
     if (vec) VQ_SUM(false, 8); else VQ_SUM(false, 1);
   }
 #undef VQ_SUM
-  return check_launch("moe_sum");
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace marlin
+
+extern "C" int moe_sum(const void* in, int act_dtype, int64_t tokens, int64_t topk, int64_t hidden,
+                       const int32_t* ids, int64_t experts, void* out, void* stream) {
+  return marlin::launch_moe_sum(in, act_dtype, tokens, topk, hidden, ids, experts, nullptr, 0, 0, out,
+                                stream, "moe_sum");
+}
+
+extern "C" int moe_sum_add(const void* in, int act_dtype, int64_t tokens, int64_t topk, int64_t hidden,
+                           const void* shared, int64_t shared_stride0, int64_t shared_stride1,
+                           void* out, void* stream) {
+  if (!shared) return vq::fail("moe_sum_add: shared is required");
+  return marlin::launch_moe_sum(in, act_dtype, tokens, topk, hidden, nullptr, 0, shared, shared_stride0,
+                                shared_stride1, out, stream, "moe_sum_add");
 }
 
 namespace marlin {

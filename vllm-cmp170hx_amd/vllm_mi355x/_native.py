@@ -13,6 +13,10 @@ import threading
 
 LIBRARY_NAME = "libvllm_mi355x.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
+# The host-only torch custom classes the reference's loader requires
+# (csrc/torch_classes.cpp), loaded with torch.ops.load_library.
+TORCH_CLASSES_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                  "libvllm_mi355x_torch.so")
 ABI_VERSION = 1
 
 BF16, FP16, FP32 = 0, 1, 2
@@ -27,6 +31,7 @@ SIGNATURES = {
     "vllm_mi355x_last_error": (ctypes.c_char_p, []),
     "vllm_mi355x_abi_version": (c_int, []),
     "exl3_linear_workspace_size": (c_i64, [c_i64, c_i64, c_i64]),
+    "exl3_linear_prefill_rows": (c_int, []),
     "exl3_linear_out": (c_int, [
         c_vp, c_int, c_i64, c_i64,            # x, x_dtype, rows, x_cols
         c_vp, c_i64, c_i64, c_i64,            # trellis, tiles_k, tiles_n, trellis_words
@@ -36,6 +41,12 @@ SIGNATURES = {
         c_vp, c_i64, c_vp,                    # workspace, workspace_numel, stream
     ]),
     "exl3_decode": (c_int, [c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp]),
+    "exl3_ple_decode_out": (c_int, [
+        c_vp, c_i64, c_i64, c_vp,             # packed_rows, rows, words, global_ids
+        c_vp, c_i64, c_vp, c_vp,              # head_bias, heads, head_offsets, head_vocab_sizes
+        c_i64, c_i64, c_i64, c_i64,           # dim, owner_lo, owner_hi, bits
+        c_vp, c_vp,                           # out, stream
+    ]),
     "exl3_set_gemv_finish": (c_int, [c_int]),
     "exl3_set_gemv_blocks": (c_int, [c_int]),
     "exl3_set_gemv_groups": (c_int, [c_int]),
@@ -79,6 +90,7 @@ SIGNATURES = {
                                c_vp]),
     "marlin_dequant": (c_int, [c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_vp]),
     "moe_sum": (c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp]),
+    "moe_sum_add": (c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "moe_align_block_size": (c_int, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64,
                                      c_vp, c_vp]),
 }

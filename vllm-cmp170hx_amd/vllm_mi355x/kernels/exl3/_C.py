@@ -8,6 +8,8 @@ geometry, workspace and overlap checks are made by the native library.
 
 from __future__ import annotations
 
+import os
+
 import torch
 
 from ... import _native
@@ -51,8 +53,9 @@ SCHEMAS = {
     "moe_workspace_size_v2": (
         "moe_workspace_size_v2(int max_rows, int hidden_size, int intermediate_size, "
         "int topk, int local_experts) -> int"),
-    # PLE rows (out of this build's scope): registered so the reference's
-    # loader finds every operator it checks; calling them raises.
+    # PLE rows: ple_decode_out decodes selected rows on the GPU; ple_read_rows
+    # (host file reads, outside this library's matmul path) is registered so
+    # the reference's loader finds it, and raises when called.
     "ple_decode_out": (
         "ple_decode_out(Tensor packed_rows, Tensor global_ids, Tensor head_bias, "
         "Tensor head_offsets, Tensor head_vocab_sizes, int owner_lo, "
@@ -243,13 +246,63 @@ def moe_out_v2_mixed_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, e
               0, out, workspace, swiglu_limit)
 
 
-def ple_unavailable(*args, **kwargs):
-    raise NotImplementedError("PLE row decoding is not part of the gfx950 quantized-matmul library")
+def _ple_check(t, name, dtype, ndim, device) -> None:
+    """The reference's per-tensor checks and wording (csrc/exl3/ple.cu:150-165)."""
+    if t is None:
+        raise RuntimeError(f"ple_decode_out: {name} must be defined")
+    if not t.is_cuda:
+        raise RuntimeError(f"ple_decode_out: {name} must be a CUDA tensor (use a CUDA/UVA view "
+                           "for pinned rows)")
+    if t.device != device:
+        raise RuntimeError(f"ple_decode_out: {name} must be on the output device")
+    if t.dtype != dtype:
+        raise RuntimeError(f"ple_decode_out: {name} has an invalid dtype")
+    if t.dim() != ndim:
+        raise RuntimeError(f"ple_decode_out: {name} must have {ndim} dimensions")
+    if not t.is_contiguous():
+        raise RuntimeError(f"ple_decode_out: {name} must be contiguous")
+
+
+def ple_decode_out_impl(packed_rows, global_ids, head_bias, head_offsets, head_vocab_sizes,
+                        owner_lo, owner_hi, bits, out) -> None:
+    """Selected PLE rows decoded to BF16 (csrc/exl3/ple.cu:167-234)."""
+    if out is None or not out.is_cuda:
+        raise RuntimeError("ple_decode_out: out must be a defined CUDA tensor")
+    device = out.device
+    _ple_check(out, "out", torch.bfloat16, 2, device)
+    _ple_check(packed_rows, "packed_rows", torch.int16, 2, device)
+    _ple_check(global_ids, "global_ids", torch.int64, 1, device)
+    _ple_check(head_bias, "head_bias", torch.float16, 2, device)
+    _ple_check(head_offsets, "head_offsets", torch.int64, 1, device)
+    _ple_check(head_vocab_sizes, "head_vocab_sizes", torch.int64, 1, device)
+    rows, dim, heads = global_ids.size(0), out.size(1), head_bias.size(0)
+    if not (out.size(0) == rows and packed_rows.size(0) == rows):
+        raise RuntimeError("ple_decode_out: packed_rows must be [R, 1 + dim*bits/16] and out must "
+                           "be [R, dim], with R = global_ids.numel()")
+    if not (heads > 0 and head_bias.size(1) == dim and head_offsets.size(0) == heads
+            and head_vocab_sizes.size(0) == heads):
+        raise RuntimeError("ple_decode_out: head_bias must be [heads, dim] and offsets/vocab sizes "
+                           "must be [heads], with heads > 0")
+    lib = _native.load()
+    with torch.cuda.device(device):
+        status = lib.exl3_ple_decode_out(
+            packed_rows.data_ptr(), rows, packed_rows.size(1), global_ids.data_ptr(),
+            head_bias.data_ptr(), heads, head_offsets.data_ptr(), head_vocab_sizes.data_ptr(),
+            dim, int(owner_lo), int(owner_hi), int(bits), out.data_ptr(), _stream(device))
+    _native.check(status)
+
+
+def ple_read_rows_unavailable(*args, **kwargs):
+    raise NotImplementedError(
+        "ple_read_rows reads compressed rows from files on the host; it is not part of the gfx950 "
+        "quantized-matmul library")
 
 
 def linear_prefill_applies_impl(rows, padded_in, padded_out, bits_x2, codebook) -> bool:
-    """The decode-to-LDS MFMA GEMM serves every format above 8 rows."""
-    return int(rows) > 8
+    """The large-M MFMA GEMM serves every format above the native library's
+    own threshold (exl3_linear_prefill_rows), so this answer cannot drift
+    from its dispatch."""
+    return int(rows) > int(_native.load().exl3_linear_prefill_rows())
 
 
 def _no_op(*args) -> None:
@@ -280,6 +333,11 @@ def register() -> None:
     lib = torch.library.Library("_exl3_C", "DEF")
     for schema in SCHEMAS.values():
         lib.define(schema)
+    # torch.classes._exl3_C.PleHostReader / EngramHostFetch (stubs that raise)
+    if not os.path.exists(_native.TORCH_CLASSES_PATH):
+        raise ImportError(f"{_native.TORCH_CLASSES_PATH} is not built: run "
+                          "python vllm-cmp170hx_amd/build.py")
+    torch.ops.load_library(_native.TORCH_CLASSES_PATH)
     lib.impl("linear_out", linear_out_impl, "CUDA")
     lib.impl("linear_out_splitk", linear_out_impl, "CUDA")
     lib.impl("exl3_decode", decode_impl, "CUDA")
@@ -299,8 +357,8 @@ def register() -> None:
         lib.impl(name, moe_out_v2_mixed_impl, "CUDA")
     for name in _SIZE_ALIASES:
         lib.impl(name, moe_workspace_size_impl, "CompositeImplicitAutograd")
-    lib.impl("ple_decode_out", ple_unavailable, "CUDA")
-    lib.impl("ple_read_rows", ple_unavailable, "CompositeImplicitAutograd")
+    lib.impl("ple_decode_out", ple_decode_out_impl, "CUDA")
+    lib.impl("ple_read_rows", ple_read_rows_unavailable, "CompositeImplicitAutograd")
     lib.impl("linear_prefill_applies", linear_prefill_applies_impl, "CompositeImplicitAutograd")
     for name in ("set_prefill_schedule", "set_gemm_shape_override", "moe_v2_draft_force_rows"):
         lib.impl(name, _no_op, "CompositeImplicitAutograd")

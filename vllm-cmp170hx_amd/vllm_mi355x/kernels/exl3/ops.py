@@ -58,12 +58,27 @@ def _moe_v2_fake(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map
               intermediate_size, out, workspace, swiglu_limit)
 
 
+def _ple_fake(packed_rows, global_ids, head_bias, head_offsets, head_vocab_sizes, owner_lo,
+              owner_hi, bits, out):
+    torch._check(out.dtype == torch.bfloat16)
+    torch._check(out.shape[0] == packed_rows.shape[0])
+    torch._check(out.shape[1] == head_bias.shape[1])
+    torch._check(global_ids.numel() == packed_rows.shape[0])
+
+
+# Classes the reference's loader requires (ops.py:205): registered by
+# libvllm_mi355x_torch.so, raising when used.
+_CLASSES = ("PleHostReader", "EngramHostFetch")
+
+
 def _validate_extension() -> None:
     built = _C.build_info()
     if built["abi_version"] != _C.ABI_VERSION:
         raise ValueError(f"abi_version mismatch: {built['abi_version']} vs {_C.ABI_VERSION}")
     for name in _OPERATORS:
         torch._C._dispatch_find_schema_or_throw(f"_exl3_C::{name}", "")
+    for name in _CLASSES:
+        getattr(torch.classes._exl3_C, name)
 
 
 def ensure_extension() -> None:
@@ -87,6 +102,7 @@ def ensure_extension() -> None:
                  "moe_out_v2_try_mixed"):
         torch.library.register_fake(f"_exl3_C::{name}")(_moe_v2_fake)
     torch.library.register_fake("_exl3_C::linear_out_prefill")(_linear_fake)
+    torch.library.register_fake("_exl3_C::ple_decode_out")(_ple_fake)
     _loaded = True
 
 
@@ -165,6 +181,15 @@ def moe_out_v2(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
     ensure_extension()
     torch.ops._exl3_C.moe_out_v2(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
                                  intermediate_size, bits_x2, out, workspace, swiglu_limit)
+
+
+def ple_decode_out(packed_rows, global_ids, head_bias, head_offsets, head_vocab_sizes,
+                   owner_lo: int, owner_hi: int, bits: int, out) -> None:
+    """Selected rows of an EXL3 PLE table decoded to BF16 (reference
+    ops.py:1301-1323)."""
+    ensure_extension()
+    torch.ops._exl3_C.ple_decode_out(packed_rows, global_ids, head_bias, head_offsets,
+                                     head_vocab_sizes, owner_lo, owner_hi, bits, out)
 
 
 def decode(trellis: torch.Tensor, bits_x2: int, codebook: int) -> torch.Tensor:

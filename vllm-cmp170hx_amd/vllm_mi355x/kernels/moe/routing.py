@@ -37,7 +37,21 @@ def moe_sum(inp: torch.Tensor, out: torch.Tensor | None = None,
 
 
 def moe_sum_add(inp: torch.Tensor, shared: torch.Tensor) -> torch.Tensor:
-    """shared + moe_sum(inp): the routed sum rounded to the dtype, then one
-    rounded add (sum.py:22-28)."""
-    routed = moe_sum(inp)
-    return torch.add(shared, routed)
+    """shared + moe_sum(inp) in one kernel (sum.py:18-56): the routed FP32
+    slot-order sum rounded to the dtype, then one rounded add of the shared
+    expert's output; inp [M, topk, H], shared [M, H] (any strides)."""
+    M, topk, H = inp.shape
+    if inp.dtype not in _DTYPE_CODES or not inp.is_contiguous():
+        raise RuntimeError("moe_sum_add: contiguous bf16 or fp16 input")
+    if shared.shape != (M, H) or shared.dtype != inp.dtype or shared.device != inp.device:
+        raise RuntimeError("moe_sum_add: shared must be [M, H] of the input dtype and device")
+    out = torch.empty((M, H), dtype=inp.dtype, device=inp.device)
+    if M == 0:
+        return out
+    with torch.cuda.device(inp.device):
+        status = _native.load().moe_sum_add(
+            inp.data_ptr(), _DTYPE_CODES[inp.dtype], M, topk, H, shared.data_ptr(),
+            shared.stride(0), shared.stride(1), out.data_ptr(),
+            torch.cuda.current_stream(inp.device).cuda_stream)
+    _native.check(status)
+    return out
