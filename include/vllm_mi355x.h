@@ -58,6 +58,33 @@ int vllm_mi355x_abi_version(void);
 int64_t exl3_linear_workspace_size(int64_t max_rows, int64_t padded_in, int64_t padded_out);
 
 /*
+ * exl3_linear_out without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  No counterpart in the
+ * reference.  The same checks, kernels and results as exl3_linear_out; the
+ * K-split partials (rows <= 32, in column ranges that fit) or the large-M
+ * activations live in a static 16 MiB device array of the library (one per
+ * device, held until the process ends; its address is looked up on the
+ * first call on each device).  Calls of more than 32 rows need rows *
+ * (padded_in + 1) floats of it: larger ones are rejected with an error
+ * (exl3_linear_scratch_rows gives the limit).  Calls on one device share
+ * the array: calls that overlap in time on one GPU (different streams)
+ * race and must be ordered by the caller.  Allocates nothing.
+ */
+int exl3_linear_out_scratch(const void* x, int x_dtype, int64_t rows, int64_t x_cols,
+                            const void* trellis, int64_t tiles_k, int64_t tiles_n,
+                            int64_t trellis_words, const void* suh, int64_t suh_numel,
+                            const void* svh, int64_t svh_numel, int64_t bits_x2, int64_t codebook,
+                            int64_t logical_in, int64_t logical_out, void* out, int out_dtype,
+                            int64_t out_rows, int64_t out_cols, void* stream);
+
+/*
+ * The most rows one exl3_linear_out_scratch call takes for a padded_in x
+ * padded_out matrix (-1 for bad sizes).  No counterpart in the reference.
+ */
+int64_t exl3_linear_scratch_rows(int64_t padded_in, int64_t padded_out);
+
+/*
  * The row count above which exl3_linear_out runs the large-M (prefill) GEMM;
  * up to it, the small-M kernel in chunks of 8 rows.  The reference's routing
  * question _exl3_C::linear_prefill_applies (vllm_sm80/kernels/exl3/

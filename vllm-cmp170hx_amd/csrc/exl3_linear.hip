@@ -391,6 +391,85 @@ extern "C" int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t
                             workspace_numel, s);
 }
 
+namespace exl3 {
+namespace {
+
+// The scratch of exl3_linear_out_scratch: the small-M path's K-split
+// partials (in column ranges that fit) or the large-M path's activations.
+// One copy per device, held until the process ends.
+constexpr int64_t kScratchFloats = int64_t(4) << 20;  // 16 MiB
+__device__ __align__(256) float scratch[kScratchFloats];
+
+// The device address of `scratch` on the current device, looked up once per
+// device (each device holds its own copy, at its own address); null on
+// failure, with the error recorded.
+float* scratch_address() {
+  static std::mutex mutex;
+  static std::map<int, float*> addresses;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) {
+    (void)hipGetLastError();
+    vq::fail("EXL3 linear scratch: no current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mutex);
+  const auto it = addresses.find(device);
+  if (it != addresses.end()) return it->second;
+  float* ptr = nullptr;
+  if (hipGetSymbolAddress(reinterpret_cast<void**>(&ptr), HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+    (void)hipGetLastError();
+    vq::fail("EXL3 linear scratch: hipGetSymbolAddress failed");
+    return nullptr;
+  }
+  addresses[device] = ptr;
+  return ptr;
+}
+
+}  // namespace
+}  // namespace exl3
+
+extern "C" int64_t exl3_linear_scratch_rows(int64_t padded_in, int64_t padded_out) {
+  if (exl3::check_padded(padded_in) != vq::kOk || exl3::check_padded(padded_out) != vq::kOk) return -1;
+  // small-M calls always fit (column ranges); large-M needs rows * (padded_in + 1)
+  const int64_t large = exl3::kScratchFloats / (padded_in + 1);
+  return std::max<int64_t>(exl3::kGemvChunkedRows, large);
+}
+
+extern "C" int exl3_linear_out_scratch(const void* x, int x_dtype, int64_t rows, int64_t x_cols,
+                                       const void* trellis, int64_t tiles_k, int64_t tiles_n,
+                                       int64_t trellis_words, const void* suh, int64_t suh_numel,
+                                       const void* svh, int64_t svh_numel, int64_t bits_x2,
+                                       int64_t codebook, int64_t logical_in, int64_t logical_out,
+                                       void* out, int out_dtype, int64_t out_rows, int64_t out_cols,
+                                       void* stream) {
+  if (int rc = exl3::check_linear(x, x_dtype, rows, x_cols, trellis, tiles_k, tiles_n, trellis_words,
+                                  suh, suh_numel, svh, svh_numel, bits_x2, codebook, logical_in,
+                                  logical_out, out, out_dtype, out_rows, out_cols, nullptr, -1)) {
+    return rc;
+  }
+  const int64_t padded_in = tiles_k * 16;
+  if (rows > exl3::kGemvChunkedRows && rows * (padded_in + 1) > exl3::kScratchFloats) {
+    return vq::fail("EXL3 linear: " + std::to_string(rows) + " rows of " + std::to_string(padded_in) +
+                    " inputs exceed the 16 MiB static scratch (at most " +
+                    std::to_string(exl3::kScratchFloats / (padded_in + 1)) +
+                    " rows above 32 per call): split the rows or use exl3_linear_out");
+  }
+  if (rows == 0) return vq::kOk;
+  float* scratch = exl3::scratch_address();
+  if (!scratch) return vq::kHipFailure;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rows > exl3::kGemvChunkedRows) {
+    return exl3::prefill_linear(x, x_dtype, rows, static_cast<const uint8_t*>(trellis), tiles_k,
+                                tiles_n, static_cast<const uint16_t*>(suh),
+                                static_cast<const uint16_t*>(svh), int(bits_x2), int(codebook),
+                                logical_in, logical_out, out, out_dtype, scratch, s);
+  }
+  return exl3::small_linear(x, x_dtype, rows, static_cast<const uint8_t*>(trellis), tiles_k, tiles_n,
+                            static_cast<const uint16_t*>(suh), static_cast<const uint16_t*>(svh),
+                            bits_x2, codebook, logical_in, logical_out, out, out_dtype, scratch,
+                            exl3::kScratchFloats, s);
+}
+
 extern "C" int exl3_set_gemv_blocks(int blocks) {
   if (blocks != 0 && blocks != 1 && blocks != 2 && blocks != 4 && blocks != 8) {
     return vq::fail("EXL3 GEMV blocks per workgroup must be 0 (automatic), 1, 2, 4 or 8");

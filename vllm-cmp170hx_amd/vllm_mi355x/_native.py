@@ -40,6 +40,15 @@ SIGNATURES = {
         c_vp, c_int, c_i64, c_i64,            # out, out_dtype, out_rows, out_cols
         c_vp, c_i64, c_vp,                    # workspace, workspace_numel, stream
     ]),
+    "exl3_linear_out_scratch": (c_int, [
+        c_vp, c_int, c_i64, c_i64,            # x, x_dtype, rows, x_cols
+        c_vp, c_i64, c_i64, c_i64,            # trellis, tiles_k, tiles_n, trellis_words
+        c_vp, c_i64, c_vp, c_i64,             # suh, suh_numel, svh, svh_numel
+        c_i64, c_i64, c_i64, c_i64,           # bits_x2, codebook, logical_in, logical_out
+        c_vp, c_int, c_i64, c_i64,            # out, out_dtype, out_rows, out_cols
+        c_vp,                                 # stream
+    ]),
+    "exl3_linear_scratch_rows": (c_i64, [c_i64, c_i64]),
     "exl3_decode": (c_int, [c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp]),
     "exl3_ple_decode_out": (c_int, [
         c_vp, c_i64, c_i64, c_vp,             # packed_rows, rows, words, global_ids
