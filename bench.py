@@ -71,16 +71,22 @@ def gemv_bytes(k: int, n: int, bits_x2: int, rows: int) -> int:
     return k * n * bits_x2 // 16 + 2 * (k + n) + 2 * rows * k + 2 * rows * n
 
 
-def make_matrix(torch, gen, device, k, n, bits_x2):
+def make_matrix(torch, gen, device, k, n, bits_x2, scales="sign"):
+    """Seeded trellis words and scales: "sign" = +-1 x N(1, 0.05) (the
+    benchmark description), "test" = suh ~ N(0, 1), svh ~ 0.05 N(0, 1) (the
+    reference's tests, test_exl3_kernels.py:174-180)."""
     trellis = torch.randint(-(2 ** 15), 2 ** 15, (k // 16, n // 16, 8 * bits_x2), dtype=torch.int16,
                             device=device, generator=gen)
 
-    def scales(size):
+    def sign_scales(size):
         sign = torch.randint(0, 2, (size,), device=device, generator=gen).float() * 2 - 1
         mag = 1.0 + 0.05 * torch.randn(size, device=device, generator=gen)
         return (sign * mag).half()
 
-    return trellis, scales(k), scales(n)
+    if scales == "test":
+        return (trellis, torch.randn(k, device=device, generator=gen).half(),
+                (0.05 * torch.randn(n, device=device, generator=gen)).half())
+    return trellis, sign_scales(k), sign_scales(n)
 
 
 def time_graph(torch, calls, per_graph, warmup, steps):
@@ -311,7 +317,11 @@ def gpu_exl3_prefill(torch, rows=2048, k=8192, n=28672, other_rows=(512, 8192)):
 
 def gpu_exl3_moe(torch, tokens=(64, 2048), experts=256, hidden=7168, inter=2048, topk=8, bits_x2=6):
     """The first token count is the line's headline; every count is in
-    by_tokens."""
+    by_tokens.  The expert scales are the reference's test scales: with the
+    +-1 x N(1, 0.05) scales of the benchmark description, random weights
+    overflow FP16 in the down projection (the outputs would be infinite and
+    carry no correctness check); the tests check this layer with the same
+    scales."""
     from vllm_mi355x.kernels.exl3 import ops
 
     ops.ensure_extension()
@@ -323,7 +333,7 @@ def gpu_exl3_moe(torch, tokens=(64, 2048), experts=256, hidden=7168, inter=2048,
     for _ in range(local):
         p, m = [], []
         for kk, nn in ((hidden, inter), (hidden, inter), (inter, hidden)):
-            t, suh, svh = make_matrix(torch, gen, device, kk, nn, bits_x2)
+            t, suh, svh = make_matrix(torch, gen, device, kk, nn, bits_x2, scales="test")
             keep += [t, suh, svh]
             p.append([t.data_ptr(), suh.data_ptr(), svh.data_ptr()])
             m.append([kk, nn, bits_x2, 2])
@@ -354,6 +364,8 @@ def gpu_exl3_moe(torch, tokens=(64, 2048), experts=256, hidden=7168, inter=2048,
 
         reps = 10 if t_count <= 256 else 2
         ms, _, _ = time_graph(torch, call, reps, reps, 5 * reps)
+        if not torch.isfinite(out.float()).all():
+            raise RuntimeError(f"EXL3 MoE bench: non-finite outputs at {t_count} tokens")
         touched = int(torch.unique(ids).numel())
         nbytes = touched * per_expert + 2 * 2 * t_count * hidden
         flops = 2 * 3 * hidden * inter * t_count * (topk + 1)
@@ -371,33 +383,79 @@ def gpu_exl3_moe(torch, tokens=(64, 2048), experts=256, hidden=7168, inter=2048,
             **by_tokens[str(tokens[0])], "by_tokens": by_tokens}
 
 
-def cpu_baseline(seconds: float, torch):
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        m = re.search(r"^Model name:\s*(.+)$", out, flags=re.M)
+        if m:
+            return m.group(1).strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        m = re.search(r"^model name\s*:\s*(.+)$", open("/proc/cpuinfo").read(), flags=re.M)
+        return m.group(1).strip() if m else "unknown"
+    except OSError:
+        return "unknown"
+
+
+def _time_cpu_linear(torch, k, n, seconds, dtype, seed):
+    """Median seconds per call of the reference's CPU dequantize-then-matmul
+    on a k x n 4-bit mul1 matrix with +-1 x N(1, 0.05) scales and one fp16
+    row ~N(0, 1), and the number of calls timed (1 warm-up first)."""
     from oracle.exl3_torch_ref import DenseDecoder, linear_fp64
 
-    g = torch.Generator().manual_seed(99)
-    trellis = torch.randint(-(2 ** 15), 2 ** 15, (K_IN // 16, N_OUT // 16, 8 * BITS_X2),
-                            dtype=torch.int16, generator=g)
-    suh = torch.randn(K_IN, generator=g).half()
-    svh = torch.randn(N_OUT, generator=g).half()
-    x = torch.randn(ROWS, K_IN, generator=g).half()
+    g = torch.Generator().manual_seed(seed)
+    trellis = torch.randint(-(2 ** 15), 2 ** 15, (k // 16, n // 16, 8 * BITS_X2), dtype=torch.int16,
+                            generator=g)
+
+    def scales(size):
+        sign = torch.randint(0, 2, (size,), generator=g).float() * 2 - 1
+        return (sign * (1.0 + 0.05 * torch.randn(size, generator=g))).half()
+
+    suh, svh = scales(k), scales(n)
+    x = torch.randn(ROWS, k, generator=g).half()
     dec = DenseDecoder(BITS_X2, CODEBOOK)
-    linear_fp64(dec, x, trellis, suh, svh, N_OUT)  # warm-up
+    linear_fp64(dec, x, trellis, suh, svh, n, dtype)  # warm-up
     times = []
     t_end = time.perf_counter() + seconds
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
         t0 = time.perf_counter()
-        linear_fp64(dec, x, trellis, suh, svh, N_OUT)
+        linear_fp64(dec, x, trellis, suh, svh, n, dtype)
         times.append(time.perf_counter() - t0)
-    per_call = statistics.median(times)
-    gbs = gemv_bytes(K_IN, N_OUT, BITS_X2, ROWS) / per_call / 1e9
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(seconds: float, torch):
+    """The reference's CPU dequantize-then-matmul path (LUT decode of every
+    tile, block H128, matmul) on this host: the headline 4096 x 14336
+    shape in FP64 (the line's value) and FP32, and the 4096 x 4096
+    CPU-plumbing configuration in both."""
+    per_call, calls = _time_cpu_linear(torch, K_IN, N_OUT, seconds, torch.float64, 99)
+    per32, calls32 = _time_cpu_linear(torch, K_IN, N_OUT, seconds / 2, torch.float32, 98)
+    c1_64, c1_calls = _time_cpu_linear(torch, 4096, 4096, seconds / 3, torch.float64, 97)
+    c1_32, c1_calls32 = _time_cpu_linear(torch, 4096, 4096, seconds / 3, torch.float32, 96)
+    gb = gemv_bytes(K_IN, N_OUT, BITS_X2, ROWS) / 1e9
+    gb_c1 = gemv_bytes(4096, 4096, BITS_X2, ROWS) / 1e9
     return {
-        "value": round(gbs, 4),
+        "value": round(gb / per_call, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{len(times)} calls (median {per_call * 1e3:.1f} ms) of the {K_IN}x{N_OUT} "
-                   "4-bit mul1 M=1 linear via the reference's CPU path restated in torch "
-                   "(65536-entry LUT decode of every tile, FP64 block H128, FP64 matmul)"),
+        "sample": (f"{calls} calls (median {per_call * 1e3:.1f} ms) of the {K_IN}x{N_OUT} 4-bit mul1 "
+                   "M=1 linear via the reference's CPU path restated in torch (65536-entry LUT decode "
+                   "of every tile, FP64 block H128, FP64 matmul), +-1 x N(1, 0.05) scales"),
+        "fp32": {"value": round(gb / per32, 4), "unit": "GB/s", "ms_per_call": round(per32 * 1e3, 2),
+                 "calls": calls32},
+        "cpu_plumbing_4096x4096": {
+            "fp64": {"value": round(gb_c1 / c1_64, 4), "unit": "GB/s", "ms_per_call": round(c1_64 * 1e3, 2),
+                     "calls": c1_calls},
+            "fp32": {"value": round(gb_c1 / c1_32, 4), "unit": "GB/s", "ms_per_call": round(c1_32 * 1e3, 2),
+                     "calls": c1_calls32},
+        },
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
     }
 
 
@@ -406,7 +464,7 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=1200)
     parser.add_argument("--warmup", type=int, default=120)
-    parser.add_argument("--cpu-seconds", type=float, default=15.0)
+    parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-extras", action="store_true",
                         help="only the headline GEMV (profiling runs)")

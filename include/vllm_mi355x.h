@@ -107,9 +107,13 @@ int exl3_linear_prefill_rows(void);
  *   workspace FP32, >= exl3_linear_workspace_size(rows, ...) elements,
  *            16-byte aligned, overlapping no other argument.
  * The weights are decoded bit-exactly; the products are summed in FP32 on
- * the matrix cores, with the activations split into FP16 high and low parts
- * (about 22 significant bits), so the result agrees with the reference's
- * sequential FP32 chain to FP32 rounding, not bit for bit.  A small-M call
+ * the matrix cores.  Up to 32 rows the activations are split into FP16 high
+ * and low parts (about 22 significant bits), so the result agrees with the
+ * reference's sequential FP32 chain to FP32 rounding, not bit for bit.
+ * Above 32 rows, at up to 4 bits per weight with a 16-byte aligned trellis,
+ * the many-row tile GEMM rounds each rotated input once to FP16 (as the
+ * reference's GPU kernels do): FP16-operand tolerance, an rms error of about
+ * 2^-12 rms(result); other many-row calls keep the split.  A small-M call
  * whose K-split partials (under a forced exl3_set_gemv_blocks, or an
  * unaligned trellis) exceed the workspace runs in column ranges that fit.
  * Replaces _exl3_C::linear_out (csrc/exl3/dense.cu:80-149; schema
@@ -162,6 +166,20 @@ int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hidden, const
                  int map64, int64_t global_experts, int64_t intermediate_size, int64_t bits_x2,
                  void* out, int out_dtype, float* workspace, int64_t workspace_numel,
                  float swiglu_limit, void* stream);
+
+/*
+ * Test and tuning switch, process-wide: the routed-row count from which an
+ * expert of a fixed-rate (moe_out_v2, up to 4 bits per weight) call runs on
+ * the many-row tile GEMM (tasks of up to 128 rows) instead of the small-M
+ * GEMV (tasks of up to 32 rows); 0 = automatic (48 rows, and only when
+ * the call's tile tasks make at least 128 workgroups in the narrower
+ * projection), any other value = that threshold with no workgroup minimum
+ * (1: every expert with 16-byte aligned matrices).  The tile GEMM rounds
+ * each rotated input once to FP16 (FP16-operand tolerance), the GEMV keeps
+ * FP16 high and low parts.  No counterpart in the reference (its nearest is
+ * the prefill routing of moe_out_prefill, ops.py:1880-1910).
+ */
+int exl3_set_moe_tile_rows(int rows);
 
 /*
  * Test and tuning switch, process-wide: how exl3_linear_out finishes its

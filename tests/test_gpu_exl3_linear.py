@@ -59,6 +59,23 @@ def _assert_fp32_close(actual, expected, name):
     assert (err <= bound).all(), f"{name}: err {err.flat[worst]:.3g} > {bound.flat[worst]:.3g} (rms {rms:.3g})"
 
 
+def _assert_tile_close(actual, expected, name):
+    """The many-row path's bar (FP16 operand tolerance): that path rounds each
+    rotated input once to FP16 (relative error <= 2^-11, as the reference's
+    GPU kernels do) and accumulates in FP32, so an output's error is a sum of
+    K independent rounding terms, about 2^-12 rms(ref) in rms.  Bar: every
+    output within 2^-8 rms(ref) + 2^-10 |ref| (max-abs), and the rms error
+    within 2^-10 rms(ref)."""
+    expected = expected.astype(np.float64)
+    rms = float(np.sqrt(np.mean(expected ** 2)))
+    err = np.abs(actual.astype(np.float64) - expected)
+    bound = 2.0 ** -8 * rms + 2.0 ** -10 * np.abs(expected)
+    worst = int(np.argmax(err - bound))
+    assert np.isfinite(actual).all(), f"{name}: non-finite output"
+    assert (err <= bound).all(), f"{name}: err {err.flat[worst]:.3g} > {bound.flat[worst]:.3g} (rms {rms:.3g})"
+    assert np.sqrt(np.mean(err ** 2)) <= 2.0 ** -10 * rms, f"{name}: rms error"
+
+
 def _assert_round_close(actual, expected, name):
     rms = float(np.sqrt(np.mean(expected.astype(np.float64) ** 2)))
     err = np.abs(actual.astype(np.float64) - expected)
@@ -291,7 +308,8 @@ def test_prefill_matches_oracle(ops, device, rows, bits_x2, codebook):
                               logical_out, torch.float32))
     sample = sorted({0, 1, rows // 2, rows - 2, rows - 1})
     want = O.linear_out(x[sample], code, trellis, suh, svh, bits_x2, codebook, logical_out, O.FP32)
-    _assert_fp32_close(got[sample], want, f"prefill rows={rows}")
+    check = _assert_fp32_close if rows <= 32 else _assert_tile_close
+    check(got[sample], want, f"prefill rows={rows}")
 
 
 def test_prefill_benchmark_shape(ops, device):
@@ -304,4 +322,4 @@ def test_prefill_benchmark_shape(ops, device):
     got = _out_np(_run_linear(ops, device, trellis, suh, svh, x, code, 8, 2, n, torch.float32))
     sample = [0, 255, 511]
     want = O.linear_out(x[sample], code, trellis, suh, svh, 8, 2, n, O.FP32)
-    _assert_fp32_close(got[sample], want, "prefill 8192x28672")
+    _assert_tile_close(got[sample], want, "prefill 8192x28672")

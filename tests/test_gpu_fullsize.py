@@ -3,13 +3,15 @@ CPU oracle on sampled rows / tokens (rows and tokens are independent, so a
 sample pins the path at the full grid) and by size-independent properties.
 
   * EXL3 prefill, 8192 x 28672, 4 bits, M = 2048 and 8192: sampled rows
-    against the oracle (bar of test_gpu_exl3_linear: FP32 outputs within
-    2^-14 rms(ref) + 2^-16 |ref|).
+    against the oracle (the many-row path's FP16-operand bar of
+    test_gpu_exl3_linear: 2^-8 rms(ref) + 2^-10 |ref| max-abs, 2^-10
+    rms(ref) rms).
   * EXL3 3-bit MoE, 256 routed + 1 shared experts, 7168 / 2048, top-8 from
     Zipf(1.1)-skewed logits, 2048 tokens: a token's output depends only on
-    its own row and routes (bitwise under a token permutation, and routed
-    alone), two calls agree bitwise, and sampled tokens whose routes are set
-    to three routed experts plus the shared one match the oracle (bar of
+    its own row and routes (bitwise under a token permutation; routed alone,
+    where its experts take the small-M GEMV, to the MoE bar), two calls
+    agree bitwise, and sampled tokens whose routes are set to three routed
+    experts plus the shared one match the oracle (bar of
     test_gpu_exl3_moe).  Scales are the reference's test scales (suh ~
     N(0, 1), svh ~ 0.05 N(0, 1)): the +-1 x N(1, 0.05) scales of the
     benchmark description overflow FP16 in the down projection of random
@@ -25,7 +27,7 @@ import torch
 from oracle import exl3_oracle as O
 from oracle import marlin_oracle as M
 from tests.exl3_cases import random_acts, random_matrix
-from tests.test_gpu_exl3_linear import _assert_fp32_close, _dev, _out_np, _run_linear
+from tests.test_gpu_exl3_linear import _assert_tile_close, _dev, _out_np, _run_linear
 from tests.test_gpu_exl3_moe import _assert_moe_close, _oracle_f32, _run
 from tests.test_gpu_marlin_moe import Layer as MarlinLayer
 from tests.test_gpu_marlin_moe import assert_close, dev, dev_act, from_f32, host_bits, routing
@@ -56,7 +58,7 @@ def test_prefill_full_shape_sampled_rows(ops, device, prefill_matrix, rows):
     assert np.isfinite(got).all()
     sample = [0, rows - 1]
     want = O.linear_out(x[sample], code, trellis, suh, svh, 8, 2, 28672, O.FP32)
-    _assert_fp32_close(got[sample], want, f"prefill M={rows}")
+    _assert_tile_close(got[sample], want, f"prefill M={rows}")
 
 
 # ---- EXL3 3-bit MoE layer at 2048 tokens --------------------------------------------
@@ -118,9 +120,11 @@ def test_moe_full_layer_2048_tokens(ops, device):
     perm = torch.randperm(rows, generator=torch.Generator().manual_seed(2051)).to(device)
     permuted = call(x[perm], ids[perm], weights[perm])
     assert torch.equal(permuted.view(torch.int16), out[perm].view(torch.int16))
+    # routed alone, a token's experts run on the small-M GEMV (another FP32
+    # summation order than the tile GEMM the full call uses): the MoE bar
     for r in (0, 1000):
         alone = call(x[r:r + 1], ids[r:r + 1], weights[r:r + 1])
-        assert torch.equal(alone.view(torch.int16), out[r:r + 1].view(torch.int16)), f"token {r}"
+        _assert_moe_close(_out_np(alone), _out_np(out[r:r + 1]).astype(np.float64), f"token {r}")
 
     # the oracle on the sampled tokens, with the four experts they use
     used = sorted({e for experts in sampled.values() for e in experts} | {routed})

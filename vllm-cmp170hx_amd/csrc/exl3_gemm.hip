@@ -5,30 +5,40 @@
 // GEMM runs on the matrix cores and applies the output transform itself:
 //  1. prefill_input: one workgroup per row forms t = H128(x * suh) over the
 //     whole row, picks a per-row power-of-two scale from the row maximum, and
-//     writes t as FP16 high and low parts (t * 2^e = hi + lo, ~22 bits).
-//  2. prefill_gemm: 256 x 256 output tiles, 16 wavefronts, four per SIMD
-//     (8 along M x 2 along N, 32 x 128 each = 1 x 4 v_mfma_f32_32x32x16_f16
-//     tiles).  Per K step of 32 inputs the workgroup decodes the 32 x 256
-//     weight slab (32 trellis tiles, one encoder lane per thread) straight into LDS as
-//     W^T [n][k] in FP16 (exact values) and stages the activation tiles;
-//     every wavefront accumulates hi * W and lo * W into one FP32
-//     accumulator.  The slab and tiles are double-buffered: step s + 1 is
-//     decoded and staged while the MFMAs of step s run (one barrier a step),
-//     with its trellis words and activations loaded two steps ahead.  The
-//     epilogue unscales each row (2^-e) and applies the output transform:
-//     H128 over each wavefront's 128-column band (one H128 block), times
-//     svh, rounded to the output dtype.
+//     writes t as FP16 high and low parts (t * 2^e = hi + lo, ~22 bits), in
+//     the k order of the MFMA operands: within every 32-input step, group g
+//     (8 halves) holds inputs {2g, 2g+1, 2g+8, 2g+9} of its two 16-input tile
+//     rows.  Row r: [high: padded_in halves][low: padded_in halves].
+//  2. the GEMM:
+//     * up to 4 bits per weight with a 16-byte aligned trellis: tile_gemm
+//       (exl3_tile.h), weights decoded in registers straight into MFMA B
+//       operands, 128 x 256 tiles, on the high parts only (each rotated
+//       input rounded once to FP16, as the reference's GPU kernels do);
+//     * other rates (and unaligned trellis bases): prefill_gemm, 256 x 256
+//       output tiles, 16 wavefronts, four per SIMD (8 along M x 2 along N,
+//       32 x 128 each = 1 x 4 v_mfma_f32_32x32x16_f16 tiles).  Per K step of
+//       32 inputs the workgroup decodes the 32 x 256 weight slab (32 trellis
+//       tiles, one encoder lane per thread) straight into LDS as W^T [n][k]
+//       in FP16 (exact values, k in the activations' order) and stages the
+//       activation tiles; every wavefront accumulates hi * W and lo * W into
+//       one FP32 accumulator.  The slab and tiles are double-buffered: step
+//       s + 1 is decoded and staged while the MFMAs of step s run (one
+//       barrier a step), with its trellis words and activations loaded two
+//       steps ahead.
+//     Both epilogues unscale each row (2^-e) and apply the output transform:
+//     H128 over each 128-column block, times svh, rounded to the output dtype.
 //
-// Workspace (FP32 elements): rows x padded_in floats holding the FP16 high
-// halves [rows][padded_in] then the low halves, and one int row exponent per
-// row after them.
+// Workspace (FP32 elements): rows x padded_in floats holding the FP16 rows
+// above, and one int row exponent per row after them.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <type_traits>
 
 #include "common.h"
 #include "exl3_codec.h"
 #include "exl3_internal.h"
+#include "exl3_tile.h"
 
 namespace exl3 {
 namespace {
@@ -50,11 +60,18 @@ constexpr int kLdsK = kBK + 8;      // LDS row stride in halves (80 bytes)
 // One workgroup (256 threads) per row.  Pass 1 finds the row maximum of
 // |t|, pass 2 recomputes t (the same operations, so the same values) and
 // writes the scaled high / low parts.
+// Half offset of input k within its 32-input step, in the operand order.
+__device__ __forceinline__ int64_t operand_order(int64_t k) {
+  const int w = int(k & 31);
+  const int g = (w & 7) >> 1;
+  const int slot = 4 * (w >> 4) + (w & 1) + 2 * ((w >> 3) & 1);
+  return (k & ~int64_t(31)) + g * 8 + slot;
+}
+
 __global__ __launch_bounds__(256) void prefill_input(const void* __restrict__ x, int x_dtype,
                                                      int64_t logical_in, int64_t padded_in,
                                                      const uint16_t* __restrict__ suh,
-                                                     _Float16* __restrict__ hi,
-                                                     _Float16* __restrict__ lo,
+                                                     _Float16* __restrict__ act,
                                                      int* __restrict__ row_exp) {
   __shared__ uint32_t row_max;
   const int64_t r = blockIdx.x;
@@ -86,26 +103,27 @@ __global__ __launch_bounds__(256) void prefill_input(const void* __restrict__ x,
   __syncthreads();
   const int e = scale_exponent(row_max);
   if (threadIdx.x == 0) row_exp[r] = e;
-  _Float16* h = hi + r * padded_in;
-  _Float16* l = lo + r * padded_in;
+  _Float16* h = act + r * 2 * padded_in;
+  _Float16* l = h + padded_in;
   for (int64_t b = wave; b < blocks; b += 4) {
     float v0, v1;
     form(b, v0, v1);
     const float t0 = ldexpf(v0, e);
     const float t1 = ldexpf(v1, e);
     const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
-    h[b * 128 + lane] = h0;
-    h[b * 128 + lane + 64] = h1;
-    l[b * 128 + lane] = _Float16(t0 - float(h0));
-    l[b * 128 + lane + 64] = _Float16(t1 - float(h1));
+    const int64_t k0 = operand_order(b * 128 + lane);
+    const int64_t k1 = operand_order(b * 128 + lane + 64);
+    h[k0] = h0;
+    h[k1] = h1;
+    l[k0] = _Float16(t0 - float(h0));
+    l[k1] = _Float16(t1 - float(h1));
   }
 }
 
 // ---- 2. decode-to-LDS MFMA GEMM -------------------------------------------------
 
 struct PrefillArgs {
-  const _Float16* hi;     // [rows][kp]
-  const _Float16* lo;     // [rows][kp]
+  const _Float16* act;    // [rows][high kp | low kp], operand order
   const int* row_exp;     // [rows]
   const uint8_t* trellis;
   const uint16_t* svh;    // [np]
@@ -149,8 +167,8 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
     const int vec = tid + kGemmThreads * v;
     st_off[v] = (vec >> 2) * kLdsK + 8 * (vec & 3);
     const int64_t src_row = min(row0 + (vec >> 2), a.rows - 1);
-    hi_src[v] = a.hi + src_row * a.kp + 8 * (vec & 3);
-    lo_src[v] = a.lo + src_row * a.kp + 8 * (vec & 3);
+    hi_src[v] = a.act + src_row * 2 * a.kp + 8 * (vec & 3);
+    lo_src[v] = hi_src[v] + a.kp;
   }
 
   // decode tasks: (tile row tr, tile column tc, encoder lane L), kTasks per thread
@@ -202,14 +220,14 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
     decode_words<kBitsX2, kCodebook>(task_l[i], words[slot][i], pair);
     if (!task_on[i]) pair[0] = pair[1] = pair[2] = pair[3] = 0u;
     const int L = task_l[i];
-    const int k = task_tr[i] * 16 + 2 * (L & 3);
+    // values 0-3 (tile rows 2q, 2q+1, 2q+8, 2q+9 of column n) sit at operand
+    // positions 8q + 4h .. + 3 of the step (h = tile row in the step), values
+    // 4-7 the same of column n + 8: one 8-byte store each
+    const int kb = 8 * (L & 3) + 4 * task_tr[i];
     const int n = task_tc[i] * 16 + (L >> 2);
-    // pair p = values (2p, 2p+1): k and k+1 of one column
     _Float16* w = w_lds[buf];
-    *reinterpret_cast<uint32_t*>(w + n * kLdsK + k) = pair[0];
-    *reinterpret_cast<uint32_t*>(w + n * kLdsK + k + 8) = pair[1];
-    *reinterpret_cast<uint32_t*>(w + (n + 8) * kLdsK + k) = pair[2];
-    *reinterpret_cast<uint32_t*>(w + (n + 8) * kLdsK + k + 8) = pair[3];
+    *reinterpret_cast<uint64_t*>(w + n * kLdsK + kb) = uint64_t(pair[0]) | (uint64_t(pair[1]) << 32);
+    *reinterpret_cast<uint64_t*>(w + (n + 8) * kLdsK + kb) = uint64_t(pair[2]) | (uint64_t(pair[3]) << 32);
   };
   auto stage = [&](int slot, int buf) {
 #pragma unroll
@@ -346,21 +364,57 @@ int launch_gemm(bool aligned, const PrefillArgs& a, hipStream_t stream) {
 
 }  // namespace
 
+namespace {
+
+template <int kBitsX2, int kCodebook>
+int launch_tile(const TileArgs& a, hipStream_t stream) {
+  const dim3 grid(unsigned((a.np + kTileCols - 1) / kTileCols), unsigned((a.rows + kTileRows - 1) / kTileRows));
+  hipLaunchKernelGGL((tile_gemm<kBitsX2, kCodebook, false>), grid, dim3(kTileThreads), 0, stream, a);
+  return vq::check_launch("exl3 tile_gemm");
+}
+
+}  // namespace
+
 int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trellis,
                    int64_t tiles_k, int64_t tiles_n, const uint16_t* suh, const uint16_t* svh,
                    int bits_x2, int codebook, int64_t logical_in, int64_t logical_out, void* out,
                    int out_dtype, float* workspace, hipStream_t stream) {
   const int64_t kp = tiles_k * 16;
   const int64_t np = tiles_n * 16;
-  if (rows > 65535 * int64_t(kBM)) return vq::fail("EXL3 linear has too many rows");
-  _Float16* hi = reinterpret_cast<_Float16*>(workspace);
-  _Float16* lo = hi + rows * kp;
+  if (rows > 65535 * int64_t(kTileRows)) return vq::fail("EXL3 linear has too many rows");
+  _Float16* act = reinterpret_cast<_Float16*>(workspace);
   int* row_exp = reinterpret_cast<int*>(workspace + rows * kp);
   hipLaunchKernelGGL(prefill_input, dim3(unsigned(rows)), dim3(256), 0, stream, x, x_dtype,
-                     logical_in, kp, suh, hi, lo, row_exp);
+                     logical_in, kp, suh, act, row_exp);
   if (int rc = vq::check_launch("exl3 prefill_input")) return rc;
-  PrefillArgs a{hi, lo, row_exp, trellis, svh, out, rows, kp, np, tiles_n, logical_out, out_dtype};
-  const bool aligned = (reinterpret_cast<uintptr_t>(trellis) & 3) == 0;
+  // the tile GEMM: up to 4 bits per weight, a 16-byte aligned trellis
+  // (LDS-DMA), 32-bit buffer offsets over the matrix and the activations
+  const uintptr_t base = reinterpret_cast<uintptr_t>(trellis);
+  if (tile_rate(bits_x2) && (base & 15) == 0 && tiles_k * tiles_n * 16 * bits_x2 <= INT_MAX &&
+      rows * 4 * kp <= INT_MAX) {
+    TileArgs t{};
+    t.act = reinterpret_cast<const uint8_t*>(act);
+    t.act_row_bytes = 4 * kp;
+    t.act_rows = rows;
+    t.row_exp = row_exp;
+    t.exp_stride = 1;
+    t.kp = kp;
+    t.np = np;
+    t.trellis = trellis;
+    t.svh = svh;
+    t.tiles_n = tiles_n;
+    t.rows = rows;
+    t.out = out;
+    t.out_dtype = out_dtype;
+    t.logical_out = logical_out;
+#define VQ_CASE(B, C) \
+    if (bits_x2 == B && codebook == C) return launch_tile<B, C>(t, stream);
+    VQ_CASE(2, 1) VQ_CASE(4, 1) VQ_CASE(6, 1) VQ_CASE(8, 1)
+    VQ_CASE(2, 2) VQ_CASE(3, 2) VQ_CASE(4, 2) VQ_CASE(5, 2) VQ_CASE(6, 2) VQ_CASE(7, 2) VQ_CASE(8, 2)
+#undef VQ_CASE
+  }
+  PrefillArgs a{act, row_exp, trellis, svh, out, rows, kp, np, tiles_n, logical_out, out_dtype};
+  const bool aligned = (base & 3) == 0;
   int rc = vq::kOk;
   bool done = false;
 #define VQ_CASE(B, C)                                        \

@@ -14,7 +14,11 @@
 //     output columns) over the whole K range, trellis streamed with
 //     coalesced buffer loads, decoded in registers, each decoded operand fed
 //     to v_mfma_f32_16x16x32_f16 for every 8-row sub-block of the task, then
-//     the output H128 and svh in the same kernel.
+//     the output H128 and svh in the same kernel.  Experts with at least
+//     48 routed rows (fixed rates up to 4 bits, 16-byte aligned matrices)
+//     run instead on the tile GEMM (exl3_tile.h: 128-row tasks x 256
+//     columns, FP16 high parts only), when their tasks make enough
+//     workgroups to fill the chip.
 //  3. moe_form (activation): clamp, SiLU(gate) * up * suh_down, H128 - the
 //     down projection's activations, in the same B-operand form.
 //  4. moe_gemv for the down projection.
@@ -27,6 +31,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <type_traits>
 
@@ -34,6 +39,7 @@
 #include "common.h"
 #include "exl3_codec.h"
 #include "exl3_internal.h"
+#include "exl3_tile.h"
 
 namespace exl3 {
 namespace {
@@ -98,73 +104,148 @@ struct MoeLayout {
 
 // ---- 1. route ------------------------------------------------------------------
 
+// An expert of a fixed-rate call whose routed rows reach this count, and
+// whose three matrices are 16-byte aligned (LDS-DMA), runs on the tile GEMM
+// in tasks of up to 128 rows; the others run on the GEMV in tasks of up to
+// task_rows rows.
+constexpr int kTileMinRows = 48;
+// Tile tasks run the whole K range each: a call uses them only when they
+// make at least this many workgroups in the narrower projection's launch.
+constexpr int64_t kMinTileBlocks = 128;
+// exl3_set_moe_tile_rows: the threshold in use (0 = kTileMinRows), which
+// also lifts the workgroup minimum (tests force the tile path with it)
+std::atomic<int> g_tile_rows_override{0};
+int tile_min_rows() {
+  const int forced = g_tile_rows_override.load();
+  return forced > 0 ? forced : kTileMinRows;
+}
+int tile_min_tasks(int automatic) { return g_tile_rows_override.load() > 0 ? 0 : automatic; }
+
+__device__ __forceinline__ bool tile_expert(const Routing& r, int e, int rows, int min_rows) {
+  if (rows < min_rows) return false;
+  const int64_t* p = r.ptrs + int64_t(e) * 9;
+  return ((p[0] | p[3] | p[6]) & 15) == 0;
+}
+
+// Table (int32, in the workspace): header {routed rows, GEMV tasks, tile
+// tasks, first tile task}, the routed assignments sorted by local expert,
+// then the tasks {expert, first sorted row, rows, 0}: GEMV tasks first, tile
+// tasks after them (every task has a row, so both fit in A entries).
+// tile_rows: the routed-row threshold of the tile GEMM (0: no tile tasks);
+// with fewer than min_tile_tasks tile tasks in all (too few workgroups to
+// fill the chip: each runs the whole K range), every expert takes the GEMV.
 __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int64_t assignments,
-                                                           int task_rows, int* table) {
+                                                           int task_rows, int tile_rows,
+                                                           int min_tile_tasks, int* table) {
   extern __shared__ int route_shared[];
   const int experts = int(routing.local_experts);
   int* count = route_shared;               // counts, then fill cursors
   int* row_begin = count + experts;
-  int* task_begin = row_begin + experts;   // experts + 1 entries
+  int* task_begin = row_begin + experts;   // GEMV tasks, experts + 1 entries
+  int* tile_begin = task_begin + experts + 1;  // tile tasks, experts + 1 entries
   __shared__ int scan_rows[kRouteThreads];
   __shared__ int scan_tasks[kRouteThreads];
+  __shared__ int scan_tiles[kRouteThreads];
+  __shared__ int tiles_in_all;
   const int tid = threadIdx.x;
   for (int e = tid; e < experts; e += kRouteThreads) count[e] = 0;
+  if (tid == 0) tiles_in_all = 0;
   __syncthreads();
   for (int64_t a = tid; a < assignments; a += kRouteThreads) {
     const int64_t e = local_expert(routing, a);
     if (e >= 0) atomicAdd(&count[e], 1);
   }
   __syncthreads();
-  // exclusive scan of (rows, tasks) over experts: each thread a contiguous run
+  // each thread a contiguous run of experts
   const int per = (experts + kRouteThreads - 1) / kRouteThreads;
   const int e0 = min(experts, tid * per);
   const int e1 = min(experts, e0 + per);
-  int rows = 0, tasks = 0;
+  if (tile_rows > 0) {
+    int mine = 0;
+    for (int e = e0; e < e1; ++e) {
+      if (tile_expert(routing, e, count[e], tile_rows)) mine += (count[e] + kTileRows - 1) / kTileRows;
+    }
+    if (mine > 0) atomicAdd(&tiles_in_all, mine);
+    __syncthreads();
+    if (tiles_in_all < min_tile_tasks) tile_rows = 0;
+  }
+  // exclusive scan of (rows, GEMV tasks, tile tasks) over experts
+  int rows = 0, tasks = 0, tile_tasks = 0;
   for (int e = e0; e < e1; ++e) {
-    rows += count[e];
-    tasks += (count[e] + task_rows - 1) / task_rows;
+    const int c = count[e];
+    rows += c;
+    if (tile_rows > 0 && tile_expert(routing, e, c, tile_rows)) {
+      tile_tasks += (c + kTileRows - 1) / kTileRows;
+    } else {
+      tasks += (c + task_rows - 1) / task_rows;
+    }
   }
   scan_rows[tid] = rows;
   scan_tasks[tid] = tasks;
+  scan_tiles[tid] = tile_tasks;
   __syncthreads();
   for (int d = 1; d < kRouteThreads; d <<= 1) {
     const int r = tid >= d ? scan_rows[tid - d] : 0;
     const int t = tid >= d ? scan_tasks[tid - d] : 0;
+    const int u = tid >= d ? scan_tiles[tid - d] : 0;
     __syncthreads();
     scan_rows[tid] += r;
     scan_tasks[tid] += t;
+    scan_tiles[tid] += u;
     __syncthreads();
   }
   int row_at = scan_rows[tid] - rows;
   int task_at = scan_tasks[tid] - tasks;
+  int tile_at = scan_tiles[tid] - tile_tasks;
   for (int e = e0; e < e1; ++e) {
     const int c = count[e];
+    const bool tile = tile_rows > 0 && tile_expert(routing, e, c, tile_rows);
     row_begin[e] = row_at;
     task_begin[e] = task_at;
+    tile_begin[e] = tile_at;
     count[e] = row_at;  // fill cursor
     row_at += c;
-    task_at += (c + task_rows - 1) / task_rows;
+    if (tile) {
+      tile_at += (c + kTileRows - 1) / kTileRows;
+    } else {
+      task_at += (c + task_rows - 1) / task_rows;
+    }
   }
   const int total_rows = scan_rows[kRouteThreads - 1];
   const int total_tasks = scan_tasks[kRouteThreads - 1];
+  const int total_tiles = scan_tiles[kRouteThreads - 1];
   if (tid == 0) {
     task_begin[experts] = total_tasks;
+    tile_begin[experts] = total_tiles;
     table[0] = total_rows;
     table[1] = total_tasks;
+    table[2] = total_tiles;
+    table[3] = total_tasks;
   }
   __syncthreads();
   int4* task_table = reinterpret_cast<int4*>(table + MoeLayout{0, 0, assignments}.tasks());
-  for (int t = tid; t < total_tasks; t += kRouteThreads) {
-    // last expert whose first task is at or before t (empty experts share
-    // their successor's start, so the search lands on the owner)
+  // task t of a list: the last expert whose first task is at or before t
+  // (experts without tasks of that list share their successor's start, so
+  // the search lands on the owner)
+  auto owner = [&](const int* begin, int t) {
     int lo = 0, hi = experts;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (task_begin[mid] <= t) lo = mid; else hi = mid;
+      if (begin[mid] <= t) lo = mid; else hi = mid;
     }
-    const int first = row_begin[lo] + (t - task_begin[lo]) * task_rows;
-    const int end = lo + 1 < experts ? row_begin[lo + 1] : total_rows;
-    task_table[t] = make_int4(lo, first, min(task_rows, end - first), 0);
+    return lo;
+  };
+  for (int t = tid; t < total_tasks; t += kRouteThreads) {
+    const int e = owner(task_begin, t);
+    const int first = row_begin[e] + (t - task_begin[e]) * task_rows;
+    const int end = e + 1 < experts ? row_begin[e + 1] : total_rows;
+    task_table[t] = make_int4(e, first, min(task_rows, end - first), 0);
+  }
+  for (int t = tid; t < total_tiles; t += kRouteThreads) {
+    const int e = owner(tile_begin, t);
+    const int first = row_begin[e] + (t - tile_begin[e]) * kTileRows;
+    const int end = e + 1 < experts ? row_begin[e + 1] : total_rows;
+    task_table[total_tasks + t] = make_int4(e, first, min(kTileRows, end - first), 0);
   }
   int* sorted = table + 4;
   for (int64_t a = tid; a < assignments; a += kRouteThreads) {
@@ -718,13 +799,49 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   const int task_rows = exl3::task_rows(fixed);
   const int64_t max_tasks =
       std::min<int64_t>(assignments, (assignments + task_rows - 1) / task_rows + local_experts);
-  if (any && max_tasks > 65535) return fail("EXL3 MoE has too many routed assignments");
+  // experts with enough rows run on the tile GEMM (fixed rates up to 4 bits)
+  const int tile_rows = exl3::tile_min_rows();
+  const bool tiles = fixed > 0 && exl3::tile_rate(fixed) && assignments >= tile_rows;
+  const int64_t max_tiles = tiles ? std::min<int64_t>(assignments, assignments / exl3::kTileRows +
+                                                                       assignments / tile_rows + 1)
+                                  : 0;
+  if (any && (max_tasks > 65535 || max_tiles > 65535)) {
+    return fail("EXL3 MoE has too many routed assignments");
+  }
   if (any) {
     int* table = reinterpret_cast<int*>(workspace + lay.ints());
+    // enough tile tasks for kMinTileBlocks workgroups in the narrower
+    // projection's launch
+    const int64_t narrow = std::min(lay.hpad, lay.ipad);
+    const int min_tile_tasks = int((exl3::kMinTileBlocks * exl3::kTileCols + narrow - 1) / narrow);
     hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads),
-                       size_t(3 * local_experts + 1) * sizeof(int), s, routing, assignments, task_rows,
-                       table);
+                       size_t(4 * local_experts + 2) * sizeof(int), s, routing, assignments, task_rows,
+                       tiles ? tile_rows : 0, exl3::tile_min_tasks(min_tile_tasks), table);
     if (int rc = check_launch("exl3 moe_route")) return rc;
+    auto tile = [&](int projection, int64_t kp, int64_t np, int64_t in_off, int64_t out_off) {
+      exl3::TileArgs t{};
+      t.act = reinterpret_cast<const uint8_t*>(workspace + in_off);
+      t.act_row_bytes = 4 * kp;
+      t.act_rows = assignments;
+      t.row_exp = reinterpret_cast<const int*>(workspace + lay.ints()) + lay.exps();
+      t.exp_stride = lay.kmax() / 128;
+      t.kp = kp;
+      t.np = np;
+      t.table = table;
+      t.task_offset = lay.tasks();
+      t.ptrs = packed_ptrs;
+      t.meta = packed_meta;
+      t.projection = projection;
+      t.moe_out = workspace + out_off;
+      const dim3 grid(unsigned((np + exl3::kTileCols - 1) / exl3::kTileCols), unsigned(max_tiles));
+      switch (fixed) {
+#define VQ_TILE(B) case B: hipLaunchKernelGGL((exl3::tile_gemm<B, 2, true>), grid, dim3(exl3::kTileThreads), 0, s, t); break;
+        VQ_TILE(2) VQ_TILE(3) VQ_TILE(4) VQ_TILE(5) VQ_TILE(6) VQ_TILE(7) VQ_TILE(8)
+#undef VQ_TILE
+        default: return fail("EXL3 MoE: no tile GEMM for this rate");
+      }
+      return check_launch("exl3 moe tile_gemm");
+    };
     const int want_bits = fixed == 0 ? int(bits_x2) : 0;
     auto gemv = [&](int projection, int64_t kp, int64_t np, int64_t in_off, int64_t out_off) {
       const dim3 grid(unsigned(np / 128), unsigned(max_tasks));
@@ -745,16 +862,29 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       hipLaunchKernelGGL(exl3::moe_form<false>, dim3(unsigned(form_h)), dim3(256), 0, s, routing, x,
                          x_dtype, hidden, intermediate_size, p, table, workspace, lay, swiglu_limit);
       if (int rc = check_launch("exl3 moe_form")) return rc;
-      if (int rc = gemv(p, lay.hpad, lay.ipad, lay.input(), p == 0 ? lay.gate() : lay.up())) return rc;
+      const int64_t out_off = p == 0 ? lay.gate() : lay.up();
+      if (int rc = gemv(p, lay.hpad, lay.ipad, lay.input(), out_off)) return rc;
+      if (tiles) {
+        if (int rc = tile(p, lay.hpad, lay.ipad, lay.input(), out_off)) return rc;
+      }
     }
     hipLaunchKernelGGL(exl3::moe_form<true>, dim3(unsigned(form_i)), dim3(256), 0, s, routing, x,
                        x_dtype, hidden, intermediate_size, 2, table, workspace, lay, swiglu_limit);
     if (int rc = check_launch("exl3 moe_form")) return rc;
     if (int rc = gemv(2, lay.ipad, lay.hpad, lay.act(), lay.input())) return rc;
+    if (tiles) {
+      if (int rc = tile(2, lay.ipad, lay.hpad, lay.act(), lay.input())) return rc;
+    }
   }
   const dim3 combine_grid(unsigned((hidden + 255) / 256), unsigned(std::min<int64_t>(rows, 65535)));
   hipLaunchKernelGGL(exl3::moe_combine, combine_grid, dim3(256), 0, s,
                      routing, workspace + lay.input(), topk_weights, rows, hidden, lay.hpad, out,
                      out_dtype, any);
   return check_launch("exl3 moe_combine");
+}
+
+extern "C" int exl3_set_moe_tile_rows(int rows) {
+  if (rows < 0) return vq::fail("EXL3 MoE tile threshold must be 0 (automatic) or positive");
+  exl3::g_tile_rows_override.store(rows);
+  return vq::kOk;
 }

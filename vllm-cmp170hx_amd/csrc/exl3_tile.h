@@ -1,0 +1,459 @@
+// EXL3 many-row GEMM for gfx950: decode in registers, activations through LDS.
+//
+// C[r][n] = sum_k A[r][k] W[k][n] for a tile of up to 128 rows x 256 output
+// columns, on v_mfma_f32_16x16x32_f16, then the output transform (unscale
+// the row, H128 over each 128-column block, times svh).  Serves the dense
+// linear above 32 rows (exl3_gemm.hip) and the MoE projections of
+// prefill-sized calls (exl3_moe.hip: the tile's rows are one expert's routed
+// assignments).
+//
+// Workgroup: 4 wavefronts (one per SIMD), two workgroups per CU.  Wavefront
+// w owns output columns [64 w, 64 w + 64) of the tile: four tile columns, two
+// pairs.  Per 32-input step (two tile rows) each lane decodes four encoder
+// lanes (two pairs x two tile rows) straight into MFMA B operands, with the
+// small-M kernel's lane map: lane (g, m) = (lane >> 4, lane & 15) decodes
+// encoder lane L = 4 (m & 7) + g of tile column (m >> 3) of a pair; values
+// 0-3 are B column m of the pair's first MFMA (tile column m & 7), values 4-7
+// of its second (tile column (m & 7) + 8), k slots {2g, 2g+1, 2g+8, 2g+9} of
+// the two tile rows.  The activations are stored in that k order (every
+// 32-input step: [g 0..3][8 halves]), so no weight ever moves between lanes
+// or through LDS.  The A operand of a 16-row block is then, for lane (g, m),
+// the 16 bytes of group g of row m: stored in LDS as [g][m] (1 KB per block),
+// read with one ds_read_b128 at 16 * lane, conflict-free.
+//
+// Activations: FP16 at a per-row power-of-two scale (the high part of the
+// activation buffer; its low part serves the small-M kernels), accumulated in
+// FP32: one rounding of each rotated input to FP16, as in the reference's
+// GPU kernels.
+//
+// Pipeline, per wavefront (one barrier a step):
+//   * trellis: LDS-DMA (buffer_load ... lds), 1 KB per step, into a ring of
+//     4 slots, issued 4 steps ahead; a step's ring words are read two steps
+//     before its MFMAs, and it is decoded (into registers) one step before;
+//   * activations: LDS-DMA of the tile's 8 row blocks per step, 2 per
+//     wavefront, into 3 buffers, issued 2 steps ahead; the
+//     operands of row block rb + 2 are read under the MFMAs of rb;
+//   * step s: issue the activation loads of s + 2, read the words of s + 2,
+//     issue the trellis load of s + 4, run the MFMAs of s with the decode of
+//     s + 1 between them (the VALU work of one step under the matrix work of
+//     the other), wait for this wavefront's loads of s + 1, barrier.
+//   Loads past the last step reload the last step (into a buffer or slot no
+//   one reads again), so the loop has no branch around a load and every wait
+//   count is a constant.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "common.h"
+#include "exl3_codec.h"
+#include "exl3_internal.h"
+
+namespace exl3 {
+
+constexpr int kTileWaves = 4;
+constexpr int kTileThreads = 64 * kTileWaves;
+constexpr int kTileCols = 64 * kTileWaves;          // 256
+constexpr int kTileRows = 128;
+constexpr int kTileBlocks = kTileRows / 16;         // 16-row blocks
+constexpr int kTileABufs = 3;
+constexpr int kTileRing = 4;
+constexpr int kTileADma = kTileBlocks / kTileWaves;  // 1 KB activation loads per wave and step
+constexpr int kTileRedStride = kTileCols + 4;       // epilogue row stride (floats)
+
+// The tile GEMM serves these rates (the trellis of one step of a wavefront
+// fits one 1 KB load).
+constexpr bool tile_rate(int64_t bits_x2) { return bits_x2 >= 2 && bits_x2 <= 8; }
+
+struct TileArgs {
+  // activation rows: row r at act + r * act_row_bytes, [high: kp halves]
+  // [low: kp halves], each 32-input step in the k order above
+  const uint8_t* act;
+  int64_t act_row_bytes;   // 4 * kp
+  int64_t act_rows;        // rows the activation buffer holds
+  const int* row_exp;      // scale exponent of row r at row_exp[r * exp_stride]
+  int64_t exp_stride;
+  int64_t kp;
+  int64_t np;
+  // dense: the matrix, rows, and the output
+  const uint8_t* trellis;
+  const uint16_t* svh;
+  int64_t tiles_n;
+  int64_t rows;
+  void* out;
+  int out_dtype;
+  int64_t logical_out;
+  // MoE: the route table (header, sorted assignments, tasks) and the
+  // projection of the experts' tables; FP32 outputs [assignment][np]
+  const int* table;
+  int64_t task_offset;     // int4 tasks at table + task_offset
+  const int64_t* ptrs;
+  const int64_t* meta;
+  int projection;
+  float* moe_out;
+};
+
+typedef __attribute__((address_space(3))) void* tile_lds_ptr_t;
+
+// f(std::integral_constant<int, i>) for i = 0 .. n - 1.
+template <int n, int i = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (i < n) {
+    f(std::integral_constant<int, i>{});
+    static_for<n, i + 1>(f);
+  }
+}
+
+// LDS reads the compiler does not see (a read it sees, of LDS that LDS-DMA
+// loads write, makes it wait for every such load in flight); a value is
+// ready after a tile_wait* that names it.
+template <int kOffset>
+__device__ __forceinline__ void tile_read16(half8_t& v, uint32_t address) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(address), "i"(kOffset));
+}
+template <int kOffset>
+__device__ __forceinline__ void tile_read4(uint32_t& v, uint32_t address) {
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(address), "i"(kOffset));
+}
+// At most n LDS reads still pending (they complete in order): a ready.
+template <int n>
+__device__ __forceinline__ void tile_wait(half8_t& a) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(n));
+}
+// Every LDS read done: a and the ring words ready.
+template <int kWords>
+__device__ __forceinline__ void tile_wait_last(half8_t& a, uint32_t (&w)[2][2][kWords]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a));
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) asm volatile("" : "+v"(w[p][h][i]));
+}
+template <int n, int kWords>
+__device__ __forceinline__ void tile_wait_words(uint32_t (&w)[2][2][kWords]) {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(n));
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) asm volatile("" : "+v"(w[p][h][i]));
+}
+
+template <int kBitsX2, int kCodebook, bool kMoe>
+__global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
+  static_assert(tile_rate(kBitsX2), "one 1 KB trellis load per step");
+  constexpr int kWords = LaneLoad<kBitsX2>::kWords;
+  constexpr int kTileBytes = 16 * kBitsX2;
+  constexpr int kRowChunk = 4 * kTileBytes;  // one tile row of a wavefront's four tile columns
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[kTileABufs][kTileBlocks][1024];
+  __shared__ __attribute__((aligned(16))) uint8_t t_lds[kTileWaves][kTileRing][1024];
+  __shared__ int row_id[kTileRows];
+  __shared__ int row_e[kTileRows];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = vq::uniform(tid >> 6);
+  const int g = lane >> 4;
+  const int m = lane & 15;
+  const int L = 4 * (m & 7) + g;
+  const int64_t col0 = int64_t(blockIdx.x) * kTileCols;
+
+  // ---- the tile's rows, matrix and scales ----
+  int nrows;
+  const uint8_t* trellis;
+  const uint16_t* svh;
+  int64_t tiles_n;
+  int first = 0;
+  if constexpr (kMoe) {
+    // tile tasks: table[2] of them from task table[3] on
+    const int task = blockIdx.y;
+    if (task >= a.table[2]) return;
+    const int4 tk = reinterpret_cast<const int4*>(a.table + a.task_offset)[a.table[3] + task];
+    const int expert = vq::uniform(tk.x);
+    first = vq::uniform(tk.y);
+    nrows = vq::uniform(tk.z);
+    const int64_t* ptrs = a.ptrs + expert * 9 + a.projection * 3;
+    const int64_t* meta = a.meta + expert * 12 + a.projection * 4;
+    trellis = reinterpret_cast<const uint8_t*>(vq::uniform(ptrs[0]));
+    svh = reinterpret_cast<const uint16_t*>(vq::uniform(ptrs[2]));
+    tiles_n = vq::uniform(meta[1]) / 16;
+    // an expert of another geometry or rate is never read: NaN rows
+    const bool bad = vq::uniform(meta[0]) != a.kp || vq::uniform(meta[1]) != a.np ||
+                     vq::uniform(meta[2]) != kBitsX2 || vq::uniform(meta[3]) != kCodebook;
+    if (bad) {
+      for (int r = wave; r < nrows; r += kTileWaves) {
+        float* dst = a.moe_out + int64_t(a.table[4 + first + r]) * a.np + col0;
+        for (int c = lane; c < kTileCols; c += 64) {
+          if (col0 + c < a.np) dst[c] = __builtin_nanf("");
+        }
+      }
+      return;
+    }
+  } else {
+    const int64_t row0 = int64_t(blockIdx.y) * kTileRows;
+    nrows = int(a.rows - row0 < kTileRows ? a.rows - row0 : kTileRows);
+    trellis = a.trellis;
+    svh = a.svh;
+    tiles_n = a.tiles_n;
+  }
+  if (tid < kTileRows) {
+    const int t = tid < nrows ? tid : nrows - 1;  // rows past the tile repeat its last row
+    int r;
+    if constexpr (kMoe) {
+      r = a.table[4 + first + t];
+    } else {
+      r = int(int64_t(blockIdx.y) * kTileRows + t);
+    }
+    row_id[tid] = r;
+    row_e[tid] = a.row_exp[int64_t(r) * a.exp_stride];
+  }
+  __syncthreads();
+
+  const int nblocks = (nrows + 15) >> 4;  // 16-row blocks with rows
+  const int steps = int(a.kp / 32);
+  const int last = steps - 1;
+  const int row_bytes = int(tiles_n * kTileBytes);
+  const int64_t tc0 = col0 / 16 + 4 * wave;  // this wavefront's first tile column
+  // columns past the matrix (a partial last tile) read tile column 0 again
+  // and are never stored
+  const int64_t tc_load = tc0 + 4 <= tiles_n ? tc0 : 0;
+
+  // ---- loads ----
+  // trellis: lane l copies 16 bytes of the step's two tile rows (lanes past
+  // them copy the first 16 bytes again, into the slot's unread tail)
+  const __amdgpu_buffer_rsrc_t t_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(trellis + tc_load * kTileBytes), 0, (steps * 2 - 1) * row_bytes + kRowChunk,
+      0x00020000);
+  const int t_voff = lane < 2 * kRowChunk / 16 ? (lane / (kRowChunk / 16)) * row_bytes +
+                                                     16 * (lane % (kRowChunk / 16))
+                                               : 0;
+  auto load_trellis = [&](int s) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(t_rsrc, (tile_lds_ptr_t)&t_lds[wave][s % kTileRing][0], 16,
+                                             t_voff, s * 2 * row_bytes, 0, 0);
+  };
+  // activations: this wavefront's row blocks rb = kTileADma * wave + i
+  // low part j / kTileBlocks, row block j % kTileBlocks); lane (g, m) copies
+  // group g of row 16 rb + m
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.act), 0, int(a.act_rows * a.act_row_bytes), 0x00020000);
+  int a_voff[kTileADma];
+#pragma unroll
+  for (int i = 0; i < kTileADma; ++i) {
+    const int rb = kTileADma * wave + i;
+    a_voff[i] = int(int64_t(row_id[16 * rb + m]) * a.act_row_bytes + 16 * g);
+  }
+  auto load_act = [&](int s) {
+    const int buf = s % kTileABufs;
+#pragma unroll
+    for (int i = 0; i < kTileADma; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (tile_lds_ptr_t)&a_lds[buf][kTileADma * wave + i][0],
+                                               16, a_voff[i], s * 64, 0, 0);
+    }
+  };
+
+  // ring words: tile column t = 2 p + (m >> 3) of tile row h of the slot
+  int word_off[2][2][kWords];
+  {
+    int idx[kWords];
+    lane_word_index<kBitsX2>(L, idx);
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < kWords; ++i)
+          word_off[p][h][i] = h * kRowChunk + (2 * p + (m >> 3)) * kTileBytes + 4 * idx[i];
+  }
+  f32x4_t acc[kTileBlocks][2][2];
+#pragma unroll
+  for (int rb = 0; rb < kTileBlocks; ++rb)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) acc[rb][p][0] = acc[rb][p][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // LDS reads in the loop go through tile_read* (outside the compiler's
+  // tracking of the LDS-DMA loads, which would make each read wait for
+  // every load in flight); tile_wait names the values it makes ready.
+  const uint32_t a_lane = vq::lds_address(&a_lds[0][0][0]) + 16 * lane;
+  const uint32_t t_base = vq::lds_address(&t_lds[wave][0][0]);
+  uint32_t word_addr[2][2][kWords];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) word_addr[p][h][i] = t_base + word_off[p][h][i];
+  uint32_t words[2][2][kWords];
+  auto read_words = [&](auto slot) {
+    constexpr int kSlot = decltype(slot)::value;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) tile_read4<kSlot * 1024>(words[p][h][i], word_addr[p][h][i]);
+  };
+
+  // decode of step words w into B operands of pair p: first / second MFMA
+  auto decode_pair = [&](const uint32_t (&w)[2][2][kWords], int p, half8_t (&b)[2][2]) {
+    uint32_t q0[4], q1[4];
+    decode_words<kBitsX2, kCodebook>(L, w[p][0], q0);
+    decode_words<kBitsX2, kCodebook>(L, w[p][1], q1);
+    b[p][0] = __builtin_bit_cast(half8_t, u32x4_t{q0[0], q0[1], q1[0], q1[1]});
+    b[p][1] = __builtin_bit_cast(half8_t, u32x4_t{q0[2], q0[3], q1[2], q1[3]});
+  };
+
+  // ---- prologue: T(0), T(1), A(0), T(2), A(1), T(3) in that order ----
+  asm volatile("" ::: "memory");
+  load_trellis(0);
+  load_trellis(min(1, last));
+  load_act(0);
+  load_trellis(min(2, last));
+  load_act(min(1, last));
+  load_trellis(min(3, last));
+  vq::wait_vmcnt<kTileADma + 2>();  // T(0), T(1) and A(0) of this wavefront landed
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  uint32_t wnext[2][2][kWords];     // the words of step s + 1 (decoded during step s)
+  read_words(std::integral_constant<int, 0>{});
+  tile_wait_words<0>(words);
+  half8_t b_cur[2][2];              // step s's B operands
+  decode_pair(words, 0, b_cur);
+  decode_pair(words, 1, b_cur);
+  read_words(std::integral_constant<int, 1>{});
+  tile_wait_words<0>(words);
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) wnext[p][h][i] = words[p][h][i];
+
+  // step s, its trellis in ring slot kSlot = s % 4 (the loop runs four steps
+  // an iteration: steps is a multiple of 4): the MFMAs of kRB row blocks of
+  // step s on b_cur, with the decode of step s + 1 scheduled between them,
+  // and the words of step s + 2 read
+  auto step = [&](int s, auto slot, auto row_blocks) {
+    constexpr int kSlot = decltype(slot)::value;
+    constexpr int kRB = decltype(row_blocks)::value;
+    load_act(min(s + 2, last));
+    // T(s + 2) landed: after it came A(s + 1), T(s + 3), A(s + 2)
+    vq::wait_vmcnt<2 * kTileADma + 1>();
+    read_words(std::integral_constant<int, (kSlot + 2) % kTileRing>{});  // (past the last step: unused)
+    // this step's slot (its words read two steps ago) takes step s + 4
+    load_trellis(min(s + 4, last));
+
+    half8_t b_next[2][2];
+    const uint32_t a_buf = a_lane + uint32_t(s % kTileABufs) * (kTileBlocks * 1024);
+    half8_t ah[kRB];
+    tile_read16<0 * 1024>(ah[0], a_buf);
+    tile_read16<1 * 1024>(ah[1], a_buf);
+    static_for<kRB>([&](auto rb_tag) {
+      constexpr int rb = decltype(rb_tag)::value;
+      if constexpr (rb + 1 < kRB) {
+        tile_wait<1>(ah[rb]);
+      } else {
+        tile_wait_last(ah[rb], words);
+      }
+      if constexpr (rb + 2 < kRB) tile_read16<(rb + 2) * 1024>(ah[rb + 2], a_buf);
+      if constexpr (rb == 0) {
+        decode_pair(wnext, 0, b_next);
+        decode_pair(wnext, 1, b_next);
+      }
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[rb][p][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[rb], b_cur[p][j], acc[rb][p][j], 0, 0, 0);
+    });
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      b_cur[p][0] = b_next[p][0];
+      b_cur[p][1] = b_next[p][1];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) wnext[p][h][i] = words[p][h][i];
+    }
+    // A(s + 1) of this wavefront landed: after it came T(s + 3), A(s + 2),
+    // T(s + 4); then every wavefront's (and every read of buffer s) is done
+    vq::wait_vmcnt<kTileADma + 2>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // Row blocks past the tile's rows hold copies of its last row: a tile of
+  // up to half the rows runs the half-height loop, any other the full one;
+  // neither branches around an MFMA.
+  auto run = [&](auto row_blocks) {
+    for (int s = 0; s < steps; s += kTileRing) {
+      step(s, std::integral_constant<int, 0>{}, row_blocks);
+      step(s + 1, std::integral_constant<int, 1>{}, row_blocks);
+      step(s + 2, std::integral_constant<int, 2>{}, row_blocks);
+      step(s + 3, std::integral_constant<int, 3>{}, row_blocks);
+    }
+  };
+  if (nblocks > kTileBlocks / 2) {
+    run(std::integral_constant<int, kTileBlocks>{});
+  } else {
+    run(std::integral_constant<int, kTileBlocks / 2>{});
+  }
+
+  // ---- epilogue ----
+  // the clamped loads past the last step may still be landing in the LDS
+  // the epilogue reuses
+  vq::wait_vmcnt<0>();
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(&a_lds[0][0][0]);  // [16][kTileRedStride]
+  static_assert(sizeof(a_lds) >= 16 * kTileRedStride * sizeof(float), "epilogue rows fit");
+#pragma unroll
+  for (int rb = 0; rb < kTileBlocks; ++rb) {
+    // lane (g, m) holds rows 4 g + i of the block, column m of each MFMA
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * g + i;
+      const int e = row_e[16 * rb + r];
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int col = 64 * wave + 32 * p + 16 * (m >> 3) + (m & 7) + 8 * j;
+          red[r * kTileRedStride + col] = ldexpf(acc[rb][p][j][i], -e);
+        }
+    }
+    __syncthreads();
+    // (row, 128-column block) tasks: H128 over the block, times svh
+    for (int task = wave; task < 32; task += kTileWaves) {
+      const int r = task >> 1;
+      const int blk = task & 1;
+      const int tr = 16 * rb + r;
+      const int64_t c0 = col0 + 128 * blk + lane;
+      float v0 = red[r * kTileRedStride + 128 * blk + lane];
+      float v1 = red[r * kTileRedStride + 128 * blk + lane + 64];
+      vq::h128_wave(v0, v1, lane);
+      if (tr < nrows) {
+        if constexpr (kMoe) {
+          if (c0 < a.np) {
+            float* dst = a.moe_out + int64_t(row_id[tr]) * a.np;
+            dst[c0] = v0 * vq::f16_to_f32(svh[c0]);
+            dst[c0 + 64] = v1 * vq::f16_to_f32(svh[c0 + 64]);
+          }
+        } else {
+          const int64_t row = int64_t(blockIdx.y) * kTileRows + tr;
+          if (c0 < a.logical_out) {
+            vq::store_act(a.out, a.out_dtype, row * a.logical_out + c0, v0 * vq::f16_to_f32(svh[c0]));
+          }
+          if (c0 + 64 < a.logical_out) {
+            vq::store_act(a.out, a.out_dtype, row * a.logical_out + c0 + 64,
+                          v1 * vq::f16_to_f32(svh[c0 + 64]));
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace exl3

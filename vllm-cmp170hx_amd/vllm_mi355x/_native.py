@@ -57,6 +57,7 @@ SIGNATURES = {
         c_vp, c_vp,                           # out, stream
     ]),
     "exl3_set_gemv_finish": (c_int, [c_int]),
+    "exl3_set_moe_tile_rows": (c_int, [c_int]),
     "exl3_set_gemv_blocks": (c_int, [c_int]),
     "exl3_set_gemv_groups": (c_int, [c_int]),
     "exl3_moe_workspace_size": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64]),
