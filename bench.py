@@ -484,18 +484,24 @@ def main() -> int:
     import torch
 
     torch.set_num_threads(os.cpu_count() or 1)
+
+    def calibration_copies():
+        if args.copy_mb:
+            src = torch.ones(args.copy_mb << 18, dtype=torch.float32, device="cuda:0")
+            dst = torch.empty_like(src)
+            for _ in range(10):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
+
     if args.only:
         run = {"prefill": gpu_exl3_prefill, "exl3_moe": gpu_exl3_moe, "marlin": gpu_marlin_moe}[args.only]
-        print(json.dumps({args.only: run(torch)}))
+        result = run(torch)
+        calibration_copies()
+        print(json.dumps({args.only: result}))
         return 0
     ms, steps, warm = gpu_gemv(args, torch)
-    if args.copy_mb:
-        src = torch.ones(args.copy_mb << 18, dtype=torch.float32, device="cuda:0")
-        dst = torch.empty_like(src)
-        for _ in range(10):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    calibration_copies()
     nbytes = gemv_bytes(K_IN, N_OUT, BITS_X2, ROWS)
     gbs = nbytes / (ms * 1e-3) / 1e9
     result = {

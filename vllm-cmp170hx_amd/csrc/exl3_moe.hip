@@ -259,37 +259,40 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
 // Half offset, within one assignment's [hi: k halves][lo: k halves], of
 // input k's high part: each 32-input step is [g 0..3][8 slots], slot order
 // {2g, 2g+1, 2g+8, 2g+9} of its two 16-input tile rows.
-__device__ __forceinline__ int64_t b_order(int64_t k) {
-  const int w = int(k & 31);
+__device__ __forceinline__ int b_order(int k) {
+  const int w = k & 31;
   const int g = (w & 7) >> 1;
   const int slot = 4 * (w >> 4) + (w & 1) + 2 * ((w >> 3) & 1);
-  return (k & ~int64_t(31)) + g * 8 + slot;
+  return (k & ~31) + g * 8 + slot;
 }
 
 // Writes one 128-input block of t (lane l holds inputs l, l + 64), scaled by
-// the assignment's power-of-two exponent, into its B-operand arrays.
-__device__ __forceinline__ void store_block(_Float16* dst, int64_t kp, int64_t block, float v0,
-                                            float v1, int e, int lane) {
+// the assignment's power-of-two exponent, into its B-operand arrays (offsets
+// within a row fit int32: kp is checked on the host).
+__device__ __forceinline__ void store_block(_Float16* dst, int kp, int block, float v0, float v1,
+                                            int e, int lane) {
   const float t0 = ldexpf(v0, e);
   const float t1 = ldexpf(v1, e);
   const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
-  const int64_t k0 = block * 128 + lane;
-  dst[b_order(k0)] = h0;
-  dst[kp + b_order(k0)] = _Float16(t0 - float(h0));
-  dst[b_order(k0 + 64)] = h1;
-  dst[kp + b_order(k0 + 64)] = _Float16(t1 - float(h1));
+  const int o0 = b_order(block * 128 + lane);
+  const int o1 = o0 + 64;  // input k + 64: two 32-input steps later
+  dst[o0] = h0;
+  dst[kp + o0] = _Float16(t0 - float(h0));
+  dst[o1] = h1;
+  dst[kp + o1] = _Float16(t1 - float(h1));
 }
 
 // kActivate false: gate/up input, t = H128(x[a / topk] * suh_projection);
 // true: down input from the gate/up results (already H128 * svh):
 // clamp, SiLU(g) * u * suh_down, H128, into the act region.
-// One workgroup per local assignment: pass 1 forms every 128-input block
-// (wavefront w takes blocks w, w + 4, ...) for the row maximum of |t|; pass 2
-// forms them again (the same operations, so the same values) and writes the
-// high / low parts at the row's one power-of-two scale, so the expert GEMV
-// sums the whole row before it unscales.  An expert whose matrix is not kp
-// rows long gets NaN operands (its suh is not read).
-template <bool kActivate>
+// One workgroup per local assignment: wavefront w forms blocks w, w + 4, ...
+// (the first kCache of them kept in registers, their loads issued together
+// at clamped block indices) for the row maximum of |t|, then writes the high
+// / low parts at the row's one power-of-two scale, so the expert GEMV sums
+// the whole row before it unscales; blocks past the register cache are
+// formed again (the same operations, so the same values).  An expert whose
+// matrix is not kp rows long gets NaN operands (its suh is not read).
+template <bool kActivate, int kCache>
 __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, int x_dtype,
                                                 int64_t hidden, int64_t intermediate, int projection,
                                                 const int* table, float* ws, MoeLayout lay,
@@ -349,7 +352,16 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   if (threadIdx.x == 0) row_max = 0u;
   __syncthreads();
   float mx = 0.0f;
-  for (int64_t b = wave; b < blocks; b += 4) {
+  float c0[kCache], c1[kCache];
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    form(min(int64_t(wave + 4 * i), blocks - 1), c0[i], c1[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    if (wave + 4 * i < blocks) mx = fmaxf(mx, fmaxf(fabsf(c0[i]), fabsf(c1[i])));
+  }
+  for (int64_t b = wave + 4 * kCache; b < blocks; b += 4) {
     float v0, v1;
     form(b, v0, v1);
     mx = fmaxf(mx, fmaxf(fabsf(v0), fabsf(v1)));
@@ -359,10 +371,14 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   __syncthreads();
   const int ex = scale_exponent(row_max);
   if (threadIdx.x == 0) exps[0] = ex;
-  for (int64_t b = wave; b < blocks; b += 4) {
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    if (wave + 4 * i < blocks) store_block(dst, int(kp), wave + 4 * i, c0[i], c1[i], ex, lane);
+  }
+  for (int64_t b = wave + 4 * kCache; b < blocks; b += 4) {
     float v0, v1;
     form(b, v0, v1);
-    store_block(dst, kp, b, v0, v1, ex, lane);
+    store_block(dst, int(kp), int(b), v0, v1, ex, lane);
   }
 }
 
@@ -687,12 +703,13 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
 
 // ---- 5. combine ------------------------------------------------------------------
 
-// One workgroup per (token, 256 columns): the token's routes (whether local,
-// the row of the down output, the routing weight) are read once into LDS;
-// each thread then sums its column over the local routes in route order, one
-// FMA each (the reference's order), with the loads of every route in flight
-// together (a route that is not local loads a valid row and is not added:
-// its own row may hold anything).
+// One workgroup per (token, 1024 columns): the token's routes (whether
+// local, the row of the down output, the routing weight) are read once into
+// LDS; each thread then sums its four columns over the local routes in route
+// order, one FMA each (the reference's order), with the 16-byte loads of
+// every route in flight together (a route that is not local loads a valid
+// row and is not added: its own row may hold anything).
+constexpr int kCombineCols = 4 * 256;
 __global__ __launch_bounds__(256) void moe_combine(Routing routing, const float* down,
                                                    const float* weights, int64_t rows,
                                                    int64_t hidden, int64_t hpad, void* out,
@@ -701,10 +718,11 @@ __global__ __launch_bounds__(256) void moe_combine(Routing routing, const float*
   __shared__ int64_t route_row[kRoutes];
   __shared__ float route_w[kRoutes];
   __shared__ int route_ok[kRoutes];
-  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  // columns c .. c + 3 (hpad is a multiple of 128: a row's 16-byte loads stay in it)
+  const int64_t c = int64_t(blockIdx.x) * kCombineCols + 4 * threadIdx.x;
   const bool mine = c < hidden;
   for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
-    float sum = 0.0f;
+    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (any_local) {
       for (int64_t k0 = 0; k0 < routing.topk; k0 += kRoutes) {
         const int n = int(routing.topk - k0 < kRoutes ? routing.topk - k0 : kRoutes);
@@ -719,14 +737,22 @@ __global__ __launch_bounds__(256) void moe_combine(Routing routing, const float*
         if (mine) {
 #pragma unroll 8
           for (int k = 0; k < n; ++k) {
-            const float v = down[route_row[k] + c];
-            sum = route_ok[k] ? fmaf(v, route_w[k], sum) : sum;
+            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(down + route_row[k] + c);
+            if (route_ok[k]) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) sum[i] = fmaf(v[i], route_w[k], sum[i]);
+            }
           }
         }
         __syncthreads();
       }
     }
-    if (mine) vq::store_act(out, out_dtype, r * hidden + c, sum);
+    if (mine) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (c + i < hidden) vq::store_act(out, out_dtype, r * hidden + c + i, sum[i]);
+      }
+    }
   }
 }
 
@@ -855,28 +881,38 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       }
       return check_launch("exl3 moe_gemv");
     };
-    // moe_form: one workgroup per assignment (the routed ones do work)
-    const int64_t form_h = assignments;
-    const int64_t form_i = assignments;
+    // moe_form: one workgroup per assignment (the routed ones do work), its
+    // register cache sized to the blocks a wavefront forms
+    auto form = [&](bool activate, int projection) {
+      const int64_t per_wave = ((activate ? lay.ipad : lay.hpad) / 128 + 3) / 4;
+      const dim3 grid{unsigned(assignments), 1u, 1u};
+#define VQ_FORM(A, C)                                                                              \
+  hipLaunchKernelGGL((exl3::moe_form<A, C>), grid, dim3(256), 0, s, routing, x, x_dtype, hidden, \
+                     intermediate_size, projection, table, workspace, lay, swiglu_limit)
+      if (activate) {
+        if (per_wave <= 4) VQ_FORM(true, 4); else if (per_wave <= 8) VQ_FORM(true, 8); else VQ_FORM(true, 16);
+      } else {
+        if (per_wave <= 4) VQ_FORM(false, 4); else if (per_wave <= 8) VQ_FORM(false, 8); else VQ_FORM(false, 16);
+      }
+#undef VQ_FORM
+      return check_launch("exl3 moe_form");
+    };
     for (int p = 0; p < 2; ++p) {
-      hipLaunchKernelGGL(exl3::moe_form<false>, dim3(unsigned(form_h)), dim3(256), 0, s, routing, x,
-                         x_dtype, hidden, intermediate_size, p, table, workspace, lay, swiglu_limit);
-      if (int rc = check_launch("exl3 moe_form")) return rc;
+      if (int rc = form(false, p)) return rc;
       const int64_t out_off = p == 0 ? lay.gate() : lay.up();
       if (int rc = gemv(p, lay.hpad, lay.ipad, lay.input(), out_off)) return rc;
       if (tiles) {
         if (int rc = tile(p, lay.hpad, lay.ipad, lay.input(), out_off)) return rc;
       }
     }
-    hipLaunchKernelGGL(exl3::moe_form<true>, dim3(unsigned(form_i)), dim3(256), 0, s, routing, x,
-                       x_dtype, hidden, intermediate_size, 2, table, workspace, lay, swiglu_limit);
-    if (int rc = check_launch("exl3 moe_form")) return rc;
+    if (int rc = form(true, 2)) return rc;
     if (int rc = gemv(2, lay.ipad, lay.hpad, lay.act(), lay.input())) return rc;
     if (tiles) {
       if (int rc = tile(2, lay.ipad, lay.hpad, lay.act(), lay.input())) return rc;
     }
   }
-  const dim3 combine_grid(unsigned((hidden + 255) / 256), unsigned(std::min<int64_t>(rows, 65535)));
+  const dim3 combine_grid(unsigned((hidden + exl3::kCombineCols - 1) / exl3::kCombineCols),
+                          unsigned(std::min<int64_t>(rows, 65535)));
   hipLaunchKernelGGL(exl3::moe_combine, combine_grid, dim3(256), 0, s,
                      routing, workspace + lay.input(), topk_weights, rows, hidden, lay.hpad, out,
                      out_dtype, any);

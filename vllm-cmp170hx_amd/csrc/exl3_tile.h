@@ -385,8 +385,9 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     asm volatile("" ::: "memory");
   };
   // Row blocks past the tile's rows hold copies of its last row: a tile of
-  // up to half the rows runs the half-height loop, any other the full one;
-  // neither branches around an MFMA.
+  // up to half the rows runs the half-height loop (an MoE task of up to a
+  // quarter, the quarter-height one), any other the full one; none branches
+  // around an MFMA.
   auto run = [&](auto row_blocks) {
     for (int s = 0; s < steps; s += kTileRing) {
       step(s, std::integral_constant<int, 0>{}, row_blocks);
@@ -397,8 +398,10 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   };
   if (nblocks > kTileBlocks / 2) {
     run(std::integral_constant<int, kTileBlocks>{});
-  } else {
+  } else if (!kMoe || nblocks > kTileBlocks / 4) {
     run(std::integral_constant<int, kTileBlocks / 2>{});
+  } else {
+    run(std::integral_constant<int, kTileBlocks / 4>{});  // MoE tasks of up to 32 rows
   }
 
   // ---- epilogue ----
