@@ -269,17 +269,22 @@ __device__ __forceinline__ int b_order(int k) {
 // Writes one 128-input block of t (lane l holds inputs l, l + 64), scaled by
 // the assignment's power-of-two exponent, into its B-operand arrays (offsets
 // within a row fit int32: kp is checked on the host).
-__device__ __forceinline__ void store_block(_Float16* dst, int kp, int block, float v0, float v1,
-                                            int e, int lane) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ void store_block(__amdgpu_buffer_rsrc_t dst, int kp, int block, float v0,
+                                            float v1, int e, int lane) {
   const float t0 = ldexpf(v0, e);
   const float t1 = ldexpf(v1, e);
   const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
-  const int o0 = b_order(block * 128 + lane);
-  const int o1 = o0 + 64;  // input k + 64: two 32-input steps later
-  dst[o0] = h0;
-  dst[kp + o0] = _Float16(t0 - float(h0));
-  dst[o1] = h1;
-  dst[kp + o1] = _Float16(t1 - float(h1));
+  const _Float16 l0 = _Float16(t0 - float(h0)), l1 = _Float16(t1 - float(h1));
+  const int o0 = 2 * b_order(block * 128 + lane);  // bytes
+  const int o1 = o0 + 128;  // input k + 64: two 32-input steps later
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, h0), dst, o0, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, l0), dst, o0, 2 * kp, 0);
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, h1), dst, o1, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, l1), dst, o1, 2 * kp, 0);
 }
 
 // kActivate false: gate/up input, t = H128(x[a / topk] * suh_projection);
@@ -307,32 +312,43 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   const int64_t e = local_expert(routing, a);
   const int64_t* ptrs = routing.ptrs + e * 9;
   int* exps = reinterpret_cast<int*>(ws + lay.ints()) + lay.exps() + a * (lay.kmax() / 128);
-  _Float16* dst = reinterpret_cast<_Float16*>(ws + (kActivate ? lay.act() : lay.input()) + a * kp);
+  const __amdgpu_buffer_rsrc_t dst =
+      make_rsrc(ws + (kActivate ? lay.act() : lay.input()) + a * kp, uint32_t(kp) * 4u);
   const bool bad = routing.meta[e * 12 + projection * 4] != kp;
   const uint16_t* suh = reinterpret_cast<const uint16_t*>(ptrs[projection * 3 + 1]);
-  auto form = [&](int64_t b, float& v0, float& v1) {
-    const int64_t k0 = b * 128 + lane;
-    const int64_t k1 = k0 + 64;
+  // Buffer resources over the row's inputs (32-bit offsets; loads past the
+  // end of x's row or of suh return zero, which forms zero).
+  const int in_len = int(kActivate ? intermediate : hidden);
+  const __amdgpu_buffer_rsrc_t suh_r = make_rsrc(suh, uint32_t(in_len) * 2u);
+  const __amdgpu_buffer_rsrc_t x_r =
+      make_rsrc(static_cast<const uint16_t*>(x) + (a / routing.topk) * hidden, uint32_t(hidden) * 2u);
+  const __amdgpu_buffer_rsrc_t g_r = make_rsrc(ws + lay.gate() + a * lay.ipad, uint32_t(lay.ipad) * 4u);
+  const __amdgpu_buffer_rsrc_t u_r = make_rsrc(ws + lay.up() + a * lay.ipad, uint32_t(lay.ipad) * 4u);
+  auto form = [&](int64_t block, float& v0, float& v1) {
+    const int k0 = int(block) * 128 + lane;
+    const int k1 = k0 + 64;
     if (bad) {
       v0 = v1 = __builtin_nanf("");
       return;
     }
     if constexpr (!kActivate) {
-      const uint16_t* row = static_cast<const uint16_t*>(x) + (a / routing.topk) * hidden;
-      const uint32_t x0 = row[k0 < hidden ? k0 : 0], x1 = row[k1 < hidden ? k1 : 0];
-      const uint32_t s0 = suh[k0 < hidden ? k0 : 0], s1 = suh[k1 < hidden ? k1 : 0];
-      v0 = k0 < hidden ? u16_act(uint16_t(x0), x_dtype) * vq::f16_to_f32(uint16_t(s0)) : 0.0f;
-      v1 = k1 < hidden ? u16_act(uint16_t(x1), x_dtype) * vq::f16_to_f32(uint16_t(s1)) : 0.0f;
+      const uint16_t x0 = __builtin_amdgcn_raw_buffer_load_b16(x_r, 2 * k0, 0, 0);
+      const uint16_t x1 = __builtin_amdgcn_raw_buffer_load_b16(x_r, 2 * k1, 0, 0);
+      const uint16_t s0 = __builtin_amdgcn_raw_buffer_load_b16(suh_r, 2 * k0, 0, 0);
+      const uint16_t s1 = __builtin_amdgcn_raw_buffer_load_b16(suh_r, 2 * k1, 0, 0);
+      v0 = u16_act(x0, x_dtype) * vq::f16_to_f32(s0);
+      v1 = u16_act(x1, x_dtype) * vq::f16_to_f32(s1);
     } else {
-      const float* g = ws + lay.gate() + a * lay.ipad;
-      const float* u = ws + lay.up() + a * lay.ipad;
-      const float gv[2] = {g[k0], g[k1]};
-      const float uv[2] = {u[k0], u[k1]};
-      const uint32_t sd[2] = {suh[k0 < intermediate ? k0 : 0], suh[k1 < intermediate ? k1 : 0]};
+      const float gv[2] = {__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g_r, 4 * k0, 0, 0)),
+                           __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g_r, 4 * k1, 0, 0))};
+      const float uv[2] = {__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(u_r, 4 * k0, 0, 0)),
+                           __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(u_r, 4 * k1, 0, 0))};
+      const uint16_t sd[2] = {__builtin_amdgcn_raw_buffer_load_b16(suh_r, 2 * k0, 0, 0),
+                              __builtin_amdgcn_raw_buffer_load_b16(suh_r, 2 * k1, 0, 0)};
       float v[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int64_t k = i ? k1 : k0;
+        const int k = i ? k1 : k0;
         v[i] = 0.0f;
         if (k < intermediate) {
           float gg = gv[i], uu = uv[i];
@@ -341,7 +357,7 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
             uu = fminf(fmaxf(uu, -limit), limit);
           }
           const float silu = gg / (1.0f + expf(-gg));
-          v[i] = (silu * uu) * vq::f16_to_f32(uint16_t(sd[i]));
+          v[i] = (silu * uu) * vq::f16_to_f32(sd[i]);
         }
       }
       v0 = v[0];
@@ -859,7 +875,9 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       t.meta = packed_meta;
       t.projection = projection;
       t.moe_out = workspace + out_off;
-      const dim3 grid(unsigned((np + exl3::kTileCols - 1) / exl3::kTileCols), unsigned(max_tiles));
+      t.col_tiles = int((np + exl3::kTileCols - 1) / exl3::kTileCols);
+      // (column tile, task) in one dimension, tasks padded to a multiple of 8
+      const dim3 grid(unsigned(t.col_tiles * ((max_tiles + 7) / 8 * 8)));
       switch (fixed) {
 #define VQ_TILE(B) case B: hipLaunchKernelGGL((exl3::tile_gemm<B, 2, true>), grid, dim3(exl3::kTileThreads), 0, s, t); break;
         VQ_TILE(2) VQ_TILE(3) VQ_TILE(4) VQ_TILE(5) VQ_TILE(6) VQ_TILE(7) VQ_TILE(8)

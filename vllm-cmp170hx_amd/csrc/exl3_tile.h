@@ -92,6 +92,7 @@ struct TileArgs {
   const int64_t* meta;
   int projection;
   float* moe_out;
+  int col_tiles;           // column tiles per task (the 1-D grid's inner size)
 };
 
 typedef __attribute__((address_space(3))) void* tile_lds_ptr_t;
@@ -145,14 +146,17 @@ __device__ __forceinline__ void tile_wait_words(uint32_t (&w)[2][2][kWords]) {
 
 template <int kBitsX2, int kCodebook, bool kMoe>
 __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
+  constexpr int kRows = kTileRows;
+  constexpr int kBlocks = kRows / 16;
+  constexpr int kADma = kBlocks / kTileWaves;
   static_assert(tile_rate(kBitsX2), "one 1 KB trellis load per step");
   constexpr int kWords = LaneLoad<kBitsX2>::kWords;
   constexpr int kTileBytes = 16 * kBitsX2;
   constexpr int kRowChunk = 4 * kTileBytes;  // one tile row of a wavefront's four tile columns
-  __shared__ __attribute__((aligned(16))) uint8_t a_lds[kTileABufs][kTileBlocks][1024];
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[kTileABufs][kBlocks][1024];
   __shared__ __attribute__((aligned(16))) uint8_t t_lds[kTileWaves][kTileRing][1024];
-  __shared__ int row_id[kTileRows];
-  __shared__ int row_e[kTileRows];
+  __shared__ int row_id[kRows];
+  __shared__ int row_e[kRows];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -160,7 +164,18 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   const int g = lane >> 4;
   const int m = lane & 15;
   const int L = 4 * (m & 7) + g;
-  const int64_t col0 = int64_t(blockIdx.x) * kTileCols;
+  // Dense: grid (column tile, row tile).  MoE: a 1-D grid; workgroups are
+  // dispatched to the 8 XCDs round-robin (workgroup p on XCD p % 8), and
+  // task t runs on XCD t % 8 with all its column tiles one after another,
+  // so that XCD's L2 fetches the task's activations once for all of them.
+  int64_t col_tile = blockIdx.x;
+  int moe_task = 0;
+  if constexpr (kMoe) {
+    const int local = int(blockIdx.x >> 3);
+    col_tile = local % a.col_tiles;
+    moe_task = (local / a.col_tiles) * 8 + int(blockIdx.x & 7);
+  }
+  const int64_t col0 = col_tile * kTileCols;
 
   // ---- the tile's rows, matrix and scales ----
   int nrows;
@@ -170,7 +185,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   int first = 0;
   if constexpr (kMoe) {
     // tile tasks: table[2] of them from task table[3] on
-    const int task = blockIdx.y;
+    const int task = moe_task;
     if (task >= a.table[2]) return;
     const int4 tk = reinterpret_cast<const int4*>(a.table + a.task_offset)[a.table[3] + task];
     const int expert = vq::uniform(tk.x);
@@ -194,19 +209,19 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
       return;
     }
   } else {
-    const int64_t row0 = int64_t(blockIdx.y) * kTileRows;
-    nrows = int(a.rows - row0 < kTileRows ? a.rows - row0 : kTileRows);
+    const int64_t row0 = int64_t(blockIdx.y) * kRows;
+    nrows = int(a.rows - row0 < kRows ? a.rows - row0 : kRows);
     trellis = a.trellis;
     svh = a.svh;
     tiles_n = a.tiles_n;
   }
-  if (tid < kTileRows) {
+  if (tid < kRows) {
     const int t = tid < nrows ? tid : nrows - 1;  // rows past the tile repeat its last row
     int r;
     if constexpr (kMoe) {
       r = a.table[4 + first + t];
     } else {
-      r = int(int64_t(blockIdx.y) * kTileRows + t);
+      r = int(int64_t(blockIdx.y) * kRows + t);
     }
     row_id[tid] = r;
     row_e[tid] = a.row_exp[int64_t(r) * a.exp_stride];
@@ -235,22 +250,22 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(t_rsrc, (tile_lds_ptr_t)&t_lds[wave][s % kTileRing][0], 16,
                                              t_voff, s * 2 * row_bytes, 0, 0);
   };
-  // activations: this wavefront's row blocks rb = kTileADma * wave + i
-  // low part j / kTileBlocks, row block j % kTileBlocks); lane (g, m) copies
+  // activations: this wavefront's row blocks rb = kADma * wave + i
+  // low part j / kBlocks, row block j % kBlocks); lane (g, m) copies
   // group g of row 16 rb + m
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(a.act), 0, int(a.act_rows * a.act_row_bytes), 0x00020000);
-  int a_voff[kTileADma];
+  int a_voff[kADma];
 #pragma unroll
-  for (int i = 0; i < kTileADma; ++i) {
-    const int rb = kTileADma * wave + i;
+  for (int i = 0; i < kADma; ++i) {
+    const int rb = kADma * wave + i;
     a_voff[i] = int(int64_t(row_id[16 * rb + m]) * a.act_row_bytes + 16 * g);
   }
   auto load_act = [&](int s) {
     const int buf = s % kTileABufs;
 #pragma unroll
-    for (int i = 0; i < kTileADma; ++i) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (tile_lds_ptr_t)&a_lds[buf][kTileADma * wave + i][0],
+    for (int i = 0; i < kADma; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (tile_lds_ptr_t)&a_lds[buf][kADma * wave + i][0],
                                                16, a_voff[i], s * 64, 0, 0);
     }
   };
@@ -268,9 +283,9 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
         for (int i = 0; i < kWords; ++i)
           word_off[p][h][i] = h * kRowChunk + (2 * p + (m >> 3)) * kTileBytes + 4 * idx[i];
   }
-  f32x4_t acc[kTileBlocks][2][2];
+  f32x4_t acc[kBlocks][2][2];
 #pragma unroll
-  for (int rb = 0; rb < kTileBlocks; ++rb)
+  for (int rb = 0; rb < kBlocks; ++rb)
 #pragma unroll
     for (int p = 0; p < 2; ++p) acc[rb][p][0] = acc[rb][p][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -314,7 +329,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   load_trellis(min(2, last));
   load_act(min(1, last));
   load_trellis(min(3, last));
-  vq::wait_vmcnt<kTileADma + 2>();  // T(0), T(1) and A(0) of this wavefront landed
+  vq::wait_vmcnt<kADma + 2>();  // T(0), T(1) and A(0) of this wavefront landed
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   uint32_t wnext[2][2][kWords];     // the words of step s + 1 (decoded during step s)
@@ -341,13 +356,13 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     constexpr int kRB = decltype(row_blocks)::value;
     load_act(min(s + 2, last));
     // T(s + 2) landed: after it came A(s + 1), T(s + 3), A(s + 2)
-    vq::wait_vmcnt<2 * kTileADma + 1>();
+    vq::wait_vmcnt<2 * kADma + 1>();
     read_words(std::integral_constant<int, (kSlot + 2) % kTileRing>{});  // (past the last step: unused)
     // this step's slot (its words read two steps ago) takes step s + 4
     load_trellis(min(s + 4, last));
 
     half8_t b_next[2][2];
-    const uint32_t a_buf = a_lane + uint32_t(s % kTileABufs) * (kTileBlocks * 1024);
+    const uint32_t a_buf = a_lane + uint32_t(s % kTileABufs) * (kBlocks * 1024);
     half8_t ah[kRB];
     tile_read16<0 * 1024>(ah[0], a_buf);
     tile_read16<1 * 1024>(ah[1], a_buf);
@@ -380,7 +395,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     }
     // A(s + 1) of this wavefront landed: after it came T(s + 3), A(s + 2),
     // T(s + 4); then every wavefront's (and every read of buffer s) is done
-    vq::wait_vmcnt<kTileADma + 2>();
+    vq::wait_vmcnt<kADma + 2>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
@@ -396,12 +411,12 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
       step(s + 3, std::integral_constant<int, 3>{}, row_blocks);
     }
   };
-  if (nblocks > kTileBlocks / 2) {
-    run(std::integral_constant<int, kTileBlocks>{});
-  } else if (!kMoe || nblocks > kTileBlocks / 4) {
-    run(std::integral_constant<int, kTileBlocks / 2>{});
+  if (nblocks > kBlocks / 2) {
+    run(std::integral_constant<int, kBlocks>{});
+  } else if (!kMoe || nblocks > kBlocks / 4) {
+    run(std::integral_constant<int, kBlocks / 2>{});
   } else {
-    run(std::integral_constant<int, kTileBlocks / 4>{});  // MoE tasks of up to 32 rows
+    run(std::integral_constant<int, kBlocks / 4>{});  // MoE tasks of up to 32 rows
   }
 
   // ---- epilogue ----
@@ -412,7 +427,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   float* red = reinterpret_cast<float*>(&a_lds[0][0][0]);  // [16][kTileRedStride]
   static_assert(sizeof(a_lds) >= 16 * kTileRedStride * sizeof(float), "epilogue rows fit");
 #pragma unroll
-  for (int rb = 0; rb < kTileBlocks; ++rb) {
+  for (int rb = 0; rb < kBlocks; ++rb) {
     // lane (g, m) holds rows 4 g + i of the block, column m of each MFMA
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -444,7 +459,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
             dst[c0 + 64] = v1 * vq::f16_to_f32(svh[c0 + 64]);
           }
         } else {
-          const int64_t row = int64_t(blockIdx.y) * kTileRows + tr;
+          const int64_t row = int64_t(blockIdx.y) * kRows + tr;
           if (c0 < a.logical_out) {
             vq::store_act(a.out, a.out_dtype, row * a.logical_out + c0, v0 * vq::f16_to_f32(svh[c0]));
           }
