@@ -380,6 +380,27 @@ int marlin_moe_align_permute(const int32_t* topk_ids, int64_t numel, int64_t num
                              int64_t cols, int64_t a_stride, void* out, int64_t out_stride,
                              void* stream);
 
+/*
+ * Split-cover MoE alignment: the routed rows sorted by expert (stable, by
+ * flat index) into four block lists of sizes 64, 48, 32 and 16, an expert
+ * with r rows getting cover[r][k] blocks of size k (cover: int32
+ * [cover_rows + 1][4] on the device, the cheapest cover by the caller's cost
+ * model; cover_rows >= numel).  Its rows fill its list-0 blocks, then its
+ * list-1 blocks, and so on; only its last block is padded (sentinel numel).
+ * List k: sorted ids (sorted_numel[k] >= numel + size_k * E entries), expert
+ * per block (eids_numel[k] >= (numel + size_k * E) / size_k; -1 past the
+ * list), ntpp[k] = its padded row count.  Deterministic (no atomic decides a
+ * position).  One workgroup; at most 1820 experts.  Replaces split_align
+ * (vllm_sm80/kernels/marlin_moe/split_align.py:173-224 and its five Triton
+ * kernels, split_align.py:45-170).
+ */
+int moe_split_align(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
+                    const int32_t* expert_map, const int32_t* cover, int64_t cover_rows,
+                    int32_t* sorted64, int32_t* sorted48, int32_t* sorted32, int32_t* sorted16,
+                    const int64_t* sorted_numel, int32_t* eids64, int32_t* eids48,
+                    int32_t* eids32, int32_t* eids16, const int64_t* eids_numel, int32_t* ntpp,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

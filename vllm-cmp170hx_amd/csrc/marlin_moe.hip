@@ -1033,6 +1033,67 @@ __device__ __forceinline__ int block_inclusive_scan(int v, int* wave_tot) {
   return v + before;
 }
 
+// Rounds of 1024 rows in ascending flat order: each wavefront ranks its rows
+// per expert with ballots, and a row's rank within its expert counts the
+// expert's rows of earlier rounds and earlier wavefronts (cursor[] starts at
+// zero; wcnt[16][experts] when wave_counts, else the 16 wavefronts take turns
+// at the cursors).  place(i, e, rank) for every routed row: the rank is its
+// position in the stable (flat index) order of its expert's rows.
+template <typename Place>
+__device__ __forceinline__ void rank_rows(const int32_t* ids, int64_t numel, int experts,
+                                          const int32_t* expert_map, int* count, int* wcnt,
+                                          int wave_counts, Place&& place) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int id_bits = experts > 1 ? 32 - __builtin_clz(unsigned(experts - 1)) : 1;
+  for (int64_t base = 0; base < numel; base += kAlignThreads) {
+    const int64_t i = base + tid;
+    const int e = i < numel ? routed_expert(ids, expert_map, i, experts) : -1;
+    // lanes of this wavefront routed to the same expert: one ballot per bit
+    // of the expert id (no data exchange between lanes)
+    uint64_t same = __ballot(e >= 0);
+    for (int bit = 0; bit < id_bits; ++bit) {
+      const bool set = (e >> bit) & 1;
+      const uint64_t m = __ballot(set);
+      same &= set ? m : ~m;
+    }
+    const int rank = __builtin_popcountll(same & ((uint64_t(1) << lane) - 1));
+    const int n_same = __builtin_popcountll(same);
+    const bool leader = e >= 0 && rank == 0;
+    int dest = -1;  // rank within the expert
+    if (wave_counts) {
+      if (leader) wcnt[wave * experts + e] = n_same;
+      __syncthreads();
+      if (e >= 0) {
+        int before = count[e];
+        for (int w = 0; w < wave; ++w) before += wcnt[w * experts + e];
+        dest = before + rank;
+      }
+      __syncthreads();
+      for (int x = tid; x < experts; x += kAlignThreads) {
+        int add = 0;
+        for (int w = 0; w < kAlignThreads / 64; ++w) {
+          add += wcnt[w * experts + x];
+          wcnt[w * experts + x] = 0;
+        }
+        count[x] += add;
+      }
+      __syncthreads();
+    } else {
+      for (int turn = 0; turn < kAlignThreads / 64; ++turn) {
+        if (wave == turn && e >= 0) {
+          const int cursor = count[e];
+          dest = cursor + rank;
+          if (leader) count[e] = cursor + n_same;
+        }
+        __syncthreads();
+      }
+    }
+    if (dest >= 0) place(i, e, dest);
+  }
+}
+
 // One workgroup: counts, padded exclusive scan, expert per block, then the
 // routed rows placed in ascending flat order inside each expert: rounds of
 // 1024 rows; each wavefront ranks its rows per expert with ballots, and a row
@@ -1049,8 +1110,6 @@ __device__ __forceinline__ void align_block(
   int* wcnt = start + experts;        // [16][experts] when wave_counts
   __shared__ int wave_tot[kAlignThreads / 64];
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
   for (int e = tid; e < experts; e += kAlignThreads) count[e] = 0;
   if (wave_counts) {
     for (int i = tid; i < 16 * experts; i += kAlignThreads) wcnt[i] = 0;
@@ -1092,52 +1151,10 @@ __device__ __forceinline__ void align_block(
   }
   for (int64_t i = tid; i < sorted_size; i += kAlignThreads) sorted[i] = int32_t(numel);
   __syncthreads();
-  const int id_bits = experts > 1 ? 32 - __builtin_clz(unsigned(experts - 1)) : 1;
-  for (int64_t base = 0; base < numel; base += kAlignThreads) {
-    const int64_t i = base + tid;
-    const int e = i < numel ? routed_expert(ids, expert_map, i, experts) : -1;
-    // lanes of this wavefront routed to the same expert: one ballot per bit
-    // of the expert id (no data exchange between lanes)
-    uint64_t same = __ballot(e >= 0);
-    for (int bit = 0; bit < id_bits; ++bit) {
-      const bool set = (e >> bit) & 1;
-      const uint64_t m = __ballot(set);
-      same &= set ? m : ~m;
-    }
-    const int rank = __builtin_popcountll(same & ((uint64_t(1) << lane) - 1));
-    const int n_same = __builtin_popcountll(same);
-    const bool leader = e >= 0 && rank == 0;
-    int64_t dest = -1;
-    if (wave_counts) {
-      if (leader) wcnt[wave * experts + e] = n_same;
-      __syncthreads();
-      if (e >= 0) {
-        int before = count[e];
-        for (int w = 0; w < wave; ++w) before += wcnt[w * experts + e];
-        dest = int64_t(start[e]) + before + rank;
-      }
-      __syncthreads();
-      for (int x = tid; x < experts; x += kAlignThreads) {
-        int add = 0;
-        for (int w = 0; w < kAlignThreads / 64; ++w) {
-          add += wcnt[w * experts + x];
-          wcnt[w * experts + x] = 0;
-        }
-        count[x] += add;
-      }
-      __syncthreads();
-    } else {
-      for (int turn = 0; turn < kAlignThreads / 64; ++turn) {
-        if (wave == turn && e >= 0) {
-          const int cursor = count[e];
-          dest = int64_t(start[e]) + cursor + rank;
-          if (leader) count[e] = cursor + n_same;
-        }
-        __syncthreads();
-      }
-    }
-    if (dest >= 0 && dest < sorted_size) sorted[dest] = int32_t(i);
-  }
+  rank_rows(ids, numel, experts, expert_map, count, wcnt, wave_counts, [&](int64_t i, int e, int rank) {
+    const int64_t dest = int64_t(start[e]) + rank;
+    if (dest < sorted_size) sorted[dest] = int32_t(i);
+  });
 }
 
 __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
@@ -1145,6 +1162,98 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp,
     int wave_counts) {
   align_block(ids, numel, experts, bs, expert_map, sorted, sorted_size, eids, blocks, ntpp, wave_counts);
+}
+
+// ---- split-cover alignment (marlin_moe/split_align.py:173-224's layout) ----------------
+
+// Block sizes of the split lists, largest first.
+constexpr int kSplitSizes[4] = {64, 48, 32, 16};
+
+struct SplitLists {
+  int32_t* sorted[4];   // list k: sorted row ids (sentinel numel on padding)
+  int32_t* eids[4];     // list k: expert of each block (-1 past the list)
+  int64_t sorted_numel[4];
+  int64_t eids_numel[4];
+  int32_t* ntpp;        // [4]: rows (padded) of each list
+};
+
+// One workgroup.  An expert with r routed rows is covered by cover[r][k]
+// blocks of size kSplitSizes[k] (the cheapest cover, a table built on the
+// host); its rows, in stable flat order, fill list 0's blocks, then list 1's,
+// and so on, so only its last block holds padding.  Lists are laid out
+// expert after expert (exclusive scans over experts per list).
+__global__ __launch_bounds__(kAlignThreads) void moe_split_align_kernel(
+    const int32_t* ids, int64_t numel, int experts, const int32_t* expert_map, const int32_t* cover,
+    SplitLists out, int wave_counts) {
+  extern __shared__ int align_shared[];
+  int* count = align_shared;            // experts: counts, then cursors
+  int* off = count + experts;           // [4][experts]: list offsets (rows)
+  int* lo = off + 4 * experts;          // [4][experts]: first rank of each list
+  int* wcnt = lo + 4 * experts;         // [16][experts] when wave_counts
+  __shared__ int wave_tot[kAlignThreads / 64];
+  __shared__ int totals[4];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < experts; e += kAlignThreads) count[e] = 0;
+  if (wave_counts) {
+    for (int i = tid; i < 16 * experts; i += kAlignThreads) wcnt[i] = 0;
+  }
+  __syncthreads();
+  for (int64_t i = tid; i < numel; i += kAlignThreads) {
+    const int e = routed_expert(ids, expert_map, i, experts);
+    if (e >= 0) atomicAdd(&count[e], 1);
+  }
+  __syncthreads();
+  const int per = (experts + kAlignThreads - 1) / kAlignThreads;
+  const int e0 = min(experts, tid * per);
+  const int e1 = min(experts, e0 + per);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    int run = 0;
+    for (int e = e0; e < e1; ++e) run += cover[count[e] * 4 + k] * kSplitSizes[k];
+    const int incl = block_inclusive_scan(run, wave_tot);
+    int at = incl - run;
+    for (int e = e0; e < e1; ++e) {
+      off[k * experts + e] = at;
+      at += cover[count[e] * 4 + k] * kSplitSizes[k];
+    }
+    if (tid == kAlignThreads - 1) totals[k] = incl;
+    __syncthreads();
+  }
+  for (int e = e0; e < e1; ++e) {
+    int at = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lo[k * experts + e] = at;
+      at += cover[count[e] * 4 + k] * kSplitSizes[k];
+    }
+    count[e] = 0;  // cursor
+  }
+  if (tid < 4) out.ntpp[tid] = totals[tid];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int bs = kSplitSizes[k];
+    const int total = totals[k];
+    for (int64_t b = tid; b < out.eids_numel[k]; b += kAlignThreads) {
+      int owner = -1;
+      if (b < total / bs) {
+        int lo_e = 0, hi_e = experts;  // last expert whose first block is at or before b
+        while (hi_e - lo_e > 1) {
+          const int mid = (lo_e + hi_e) >> 1;
+          if (off[k * experts + mid] / bs <= b) lo_e = mid; else hi_e = mid;
+        }
+        owner = lo_e;
+      }
+      out.eids[k][b] = owner;
+    }
+    for (int64_t i = tid; i < total; i += kAlignThreads) out.sorted[k][i] = int32_t(numel);
+  }
+  __syncthreads();
+  rank_rows(ids, numel, experts, expert_map, count, wcnt, wave_counts, [&](int64_t i, int e, int rank) {
+    int k = 3;
+    while (k > 0 && rank < lo[k * experts + e]) --k;
+    out.sorted[k][off[k * experts + e] + rank - lo[k * experts + e]] = int32_t(i);
+  });
 }
 
 // The alignment (workgroup 0) and the activations' k permutation (the other
@@ -1522,6 +1631,41 @@ extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int6
                      numel, int(num_experts), int(block_size), expert_map, sorted, sorted_numel,
                      expert_ids, expert_ids_numel, ntpp, wave_counts);
   return check_launch("moe_align_block_size");
+}
+
+extern "C" int moe_split_align(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
+                               const int32_t* expert_map, const int32_t* cover, int64_t cover_rows,
+                               int32_t* sorted64, int32_t* sorted48, int32_t* sorted32, int32_t* sorted16,
+                               const int64_t* sorted_numel, int32_t* eids64, int32_t* eids48,
+                               int32_t* eids32, int32_t* eids16, const int64_t* eids_numel,
+                               int32_t* ntpp, void* stream) {
+  using namespace vq;
+  if (numel < 0 || numel > INT_MAX) return fail("split_align: numel out of range");
+  if (num_experts <= 0 || num_experts > 8192) return fail("split_align: 1 <= num_experts <= 8192");
+  if (cover_rows < numel) return fail("split_align buffers too small");
+  if (9 * num_experts * int64_t(sizeof(int)) > 65536) return fail("split_align: at most 1820 experts");
+  marlin::SplitLists lists{};
+  int32_t* sorted[4] = {sorted64, sorted48, sorted32, sorted16};
+  int32_t* eids[4] = {eids64, eids48, eids32, eids16};
+  for (int k = 0; k < 4; ++k) {
+    const int64_t bs = marlin::kSplitSizes[k];
+    // the reference's buffers: numel + bs E rows, (numel + bs E) / bs + 1 blocks
+    if (sorted_numel[k] < numel + bs * num_experts || eids_numel[k] < (numel + bs * num_experts) / bs) {
+      return fail("split_align buffers too small");
+    }
+    if (numel + bs * num_experts > INT_MAX) return fail("split_align: padded total must fit int32");
+    lists.sorted[k] = sorted[k];
+    lists.eids[k] = eids[k];
+    lists.sorted_numel[k] = sorted_numel[k];
+    lists.eids_numel[k] = eids_numel[k];
+  }
+  lists.ntpp = ntpp;
+  const int wave_counts = num_experts <= 640 ? 1 : 0;
+  const size_t lds = size_t(9 + (wave_counts ? 16 : 0)) * size_t(num_experts) * sizeof(int);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(marlin::moe_split_align_kernel, dim3(1), dim3(marlin::kAlignThreads), lds, s, topk_ids,
+                     numel, int(num_experts), expert_map, cover, lists, wave_counts);
+  return check_launch("moe_split_align");
 }
 
 extern "C" int marlin_moe_align_permute(const int32_t* topk_ids, int64_t numel, int64_t num_experts,

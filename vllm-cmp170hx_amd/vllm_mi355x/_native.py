@@ -103,6 +103,12 @@ SIGNATURES = {
     "moe_sum_add": (c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "moe_align_block_size": (c_int, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64,
                                      c_vp, c_vp]),
+    "moe_split_align": (c_int, [
+        c_vp, c_i64, c_i64, c_vp, c_vp, c_i64,  # topk_ids, numel, num_experts, expert_map, cover, rows
+        c_vp, c_vp, c_vp, c_vp, c_vp,            # sorted lists 64 / 48 / 32 / 16, sorted_numel[4]
+        c_vp, c_vp, c_vp, c_vp, c_vp,            # expert-id lists, eids_numel[4]
+        c_vp, c_vp,                              # ntpp[4], stream
+    ]),
 }
 
 _lib = None

@@ -21,6 +21,7 @@ import math
 import torch
 
 from . import _C
+from . import split_align as split_align_mod
 from ..moe.align import align_sizes, kernel_moe_align_block_size
 from ..moe.routing import moe_sum
 
@@ -106,9 +107,12 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
     experts (id out of range, or mapped to -1) add nothing.
 
     path: None (automatic), "staged" (activations staged in LDS per
-    workgroup, any block size and K split) or "direct" (k-permuted
+    workgroup, any block size and K split), "direct" (k-permuted
     activations, SwiGLU fused into w13; blocks of at most 32 tokens, K split
-    1).  Both give the same sums."""
+    1) or "split" (the staged kernels over the split-cover block lists of
+    split_align: one w13 and one w2 launch per list, as the reference's
+    prefill.run, marlin_moe/prefill.py:381-447).  All give the same sums: a
+    row's sums depend only on its own activations, expert and K split."""
     M, K = hidden_states.shape
     E = w1.size(0)
     N = w2.size(1) * 16
@@ -136,6 +140,9 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
     bs = block_size or choose_block_size(M, topk, E)
     if path is None:
         direct = ksplit in (None, 1) and direct_applies(M, topk, K, N, E, bs)
+    elif path == "split":
+        return _split_path(hidden_states, w1, w2, w1_scale, w2_scale, topk_weights, local, out,
+                           limit, E, ksplit, workspace)
     elif path in ("direct", "staged"):
         direct = path == "direct"
         if direct and (ksplit not in (None, 1) or bs > 32 or (2 * N) % 256 != 0 or K % 32 != 0):
@@ -175,5 +182,44 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
     _C.act(buf["part"], local.view(-1), ks, slots, N, limit, buf["h"])
     _C.gemm(buf["h"], w2, w2_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], tw, 1, slots,
             N, K, bs, _C.MODE_TOPK, 1, out=buf["c3"])
+    moe_sum(buf["c3"].view(M, topk, K), out, local, E)
+    return out
+
+
+def _split_path(hidden_states, w1, w2, w1_scale, w2_scale, topk_weights, local, out, limit, E,
+                ksplit, workspace):
+    """The staged kernels over the split-cover lists (prefill.py:381-447's
+    run): every routed row is computed once, in the block list its expert's
+    cover puts it in."""
+    M, K = hidden_states.shape
+    N = w2.size(1) * 16
+    topk = local.size(1)
+    slots = M * topk
+    ws = workspace if workspace is not None else {}
+    key = ("split", slots, E, hidden_states.device)
+    sbuf = ws.get(key)
+    if sbuf is None:
+        sbuf = split_align_mod.buffers(slots, E, hidden_states.device)
+        ws[key] = sbuf
+    lists = split_align_mod.split_align(local, E, sbuf)
+    ks = ksplit or choose_w13_ksplit(min(slots, E), 2 * N, K, 64)
+    shapes = {"part": (ks * slots * 2 * N,), "h": (slots, N), "c3": (slots, K)}
+    buf = {}
+    for name, shape in shapes.items():
+        dtype = torch.float32 if name == "part" else hidden_states.dtype
+        numel = math.prod(shape)
+        t = ws.get(name)
+        if t is None or t.numel() < numel or t.dtype != dtype:
+            t = torch.empty(numel, dtype=dtype, device=hidden_states.device)
+            ws[name] = t
+        buf[name] = t.view(-1)[:numel].view(shape)
+    tw = topk_weights.to(torch.float32).contiguous().view(-1)
+    for bs, sorted_ids, expert_ids, ntpp in lists:
+        _C.gemm(hidden_states, w1, w1_scale, sorted_ids, expert_ids, ntpp, None, topk, slots, K,
+                2 * N, bs, _C.MODE_PARTIAL, ks, part=buf["part"])
+    _C.act(buf["part"], local.view(-1), ks, slots, N, limit, buf["h"])
+    for bs, sorted_ids, expert_ids, ntpp in lists:
+        _C.gemm(buf["h"], w2, w2_scale, sorted_ids, expert_ids, ntpp, tw, 1, slots, N, K, bs,
+                _C.MODE_TOPK, 1, out=buf["c3"])
     moe_sum(buf["c3"].view(M, topk, K), out, local, E)
     return out
