@@ -381,6 +381,28 @@ int marlin_moe_align_permute(const int32_t* topk_ids, int64_t numel, int64_t num
                              void* stream);
 
 /*
+ * MoE router with the block alignment: logits = x W^T in FP32 (bf16 or fp16
+ * x [M][K] with row stride x_stride, weight [E][K] contiguous; products
+ * exact, summed in one fixed order on the matrix cores), then per row the
+ * top-k experts by key, ties to the lower expert: scoring 1 = sigmoid +
+ * bias (score 0.5 tanh(0.5 l) + 0.5, key score + bias[e]), 0 = softmax
+ * (key = score = exp(l - max) / sum); weights = the selected scores,
+ * divided by (their sum + 1e-20) when renormalize, times scale; rows with
+ * is_padding[m] != 0 (optional uint8 [M]) route to -1.  Then the
+ * moe_align_block_size alignment of the ids (same outputs and sizes).
+ * logits fp32 [M][E], topk_weights fp32 / topk_ids int32 [M][topk].  Two
+ * launches; K % 128 == 0, E <= 1024, topk <= 64.  Replaces moe_route
+ * (vllm_sm80/kernels/moe/route.py:994-1084: router GEMV, sigmoid/bias
+ * top-k, alignment), with softmax scoring added for routers that use it.
+ */
+int moe_route(const void* x, int x_dtype, int64_t M, int64_t K, int64_t x_stride,
+              const void* weight, const float* bias, int64_t num_experts, int64_t topk,
+              int scoring, int renormalize, float scale, int64_t block_size,
+              const uint8_t* is_padding, float* logits, float* topk_weights, int32_t* topk_ids,
+              int32_t* sorted, int64_t sorted_numel, int32_t* expert_ids,
+              int64_t expert_ids_numel, int32_t* ntpp, void* stream);
+
+/*
  * Split-cover MoE alignment: the routed rows sorted by expert (stable, by
  * flat index) into four block lists of sizes 64, 48, 32 and 16, an expert
  * with r rows getting cover[r][k] blocks of size k (cover: int32

@@ -1164,6 +1164,155 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   align_block(ids, numel, experts, bs, expert_map, sorted, sorted_size, eids, blocks, ntpp, wave_counts);
 }
 
+// ---- router: logits, top-k, alignment (vllm_sm80/kernels/moe/route.py) ------------------
+
+typedef short bf16raw8_t __attribute__((ext_vector_type(8)));
+
+// logits[m][e] = sum_k x[m][k] W[e][k] in FP32 (bf16 or fp16 products are
+// exact in FP32).  Workgroup = 16 experts x 16 rows: its four wavefronts
+// take a quarter of K each on v_mfma_f32_16x16x32 (A = 16 rows x 32 k, B =
+// 32 k x 16 experts, every lane 8 consecutive k of its row / expert), and the
+// quarters are added in wavefront order: one fixed order, so the logits are
+// bitwise reproducible and independent of M.  Rows past M and experts past
+// E read a valid row and are not stored.
+template <bool kBF16>
+__global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* x, int64_t x_stride,
+                                                           const uint16_t* w, int64_t M, int64_t K,
+                                                           int64_t E, float* logits) {
+  __shared__ f32x4_t red[3][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t e0 = int64_t(blockIdx.x) * 16;
+  const int64_t m0 = int64_t(blockIdx.y) * 16;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int64_t row = min(m0 + r, M - 1);
+  const int64_t ex = min(e0 + r, E - 1);
+  const int64_t kq = K / 4;
+  const uint16_t* xa = x + row * x_stride + wave * kq + 8 * g;
+  const uint16_t* wb = w + ex * K + wave * kq + 8 * g;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t k = 0; k < kq; k += 32) {
+    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa + k);
+    const u32x4_t b = *reinterpret_cast<const u32x4_t*>(wb + k);
+    acc = mfma<kBF16>(b, a, acc);  // C[e][m]: lane holds experts 4g..4g+3 of row r
+  }
+  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const f32x4_t o = red[q][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] += o[i];
+    }
+    const int64_t m = m0 + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t e = e0 + 4 * g + i;
+      if (m < M && e < E) logits[m * E + e] = acc[i];
+    }
+  }
+}
+
+// An FP32 key as a signed integer of the same order.
+__device__ __forceinline__ int32_t monotone(float v) {
+  const int32_t b = __builtin_bit_cast(int32_t, v);
+  return b ^ ((b >> 31) & 0x7fffffff);
+}
+
+constexpr int kRouteMaxExperts = 1024;
+
+// One workgroup: wavefront w routes rows w, w + 16, ...: scores of every
+// expert (sigmoid: 0.5 tanh(0.5 l) + 0.5, the key adding the bias; softmax:
+// exp(l - max) / sum, the key the probability), top-k by the packed
+// (monotone(key) << 32 | E - 1 - e) maximum (the lower expert wins an exact
+// tie), weights = the selected scores, renormalized (/ (sum + 1e-20)) if
+// asked, times `scale`; padding rows (is_padding != 0) route to -1.  Then
+// the block alignment of the ids, in the same workgroup.
+__global__ __launch_bounds__(kAlignThreads) void route_select_align_kernel(
+    const float* logits, const float* bias, int64_t M, int E, int topk, int sigmoid, int renorm,
+    float scale, const uint8_t* is_padding, float* topk_w, int32_t* topk_ids, int bs,
+    int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp,
+    int wave_counts) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  constexpr int kPer = kRouteMaxExperts / 64;
+  for (int64_t m = wave; m < M; m += kAlignThreads / 64) {
+    const float* lrow = logits + m * E;
+    float score[kPer];
+    int64_t packed[kPer];
+    float mx = -INFINITY;
+    if (!sigmoid) {
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) mx = fmaxf(mx, lrow[e]);
+      }
+      mx = vq::wave_max(mx, lane);
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane + 64 * j;
+      score[j] = 0.0f;
+      if (e < E) score[j] = sigmoid ? 0.5f * tanhf(0.5f * lrow[e]) + 0.5f : expf(lrow[e] - mx);
+      sum += score[j];
+    }
+    if (!sigmoid) {
+      // the softmax denominator: a fixed-order sum (per lane in expert
+      // order, then the butterfly)
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) sum += __shfl_xor(sum, d);
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) score[j] = score[j] / sum;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane + 64 * j;
+      const float key = sigmoid ? score[j] + bias[e < E ? e : 0] : score[j];
+      packed[j] = e < E ? (int64_t(monotone(key)) << 32) | int64_t(E - 1 - e) : INT64_MIN;
+    }
+    float sel_w = 0.0f;
+    int sel_e = -1;
+    float total = 0.0f;
+    for (int k = 0; k < topk; ++k) {
+      int64_t best = INT64_MIN;
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) best = packed[j] > best ? packed[j] : best;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) {
+        const int64_t o = __shfl_xor(best, d);
+        best = o > best ? o : best;
+      }
+      const int e = E - 1 - int(best & 0xffffffff);
+      float v_own = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        if (j == e / 64) v_own = score[j];
+        if (packed[j] == best) packed[j] = INT64_MIN;
+      }
+      const float chosen = __shfl(v_own, e % 64);
+      total += chosen;
+      if (lane == k) {
+        sel_w = chosen;
+        sel_e = e;
+      }
+    }
+    if (lane < topk) {
+      float wgt = renorm ? sel_w / (total + 1e-20f) : sel_w;
+      wgt *= scale;
+      const bool pad = is_padding != nullptr && is_padding[m] != 0;
+      topk_w[m * topk + lane] = wgt;
+      topk_ids[m * topk + lane] = pad ? -1 : sel_e;
+    }
+  }
+  // the ids are read back by this workgroup's alignment
+  __threadfence();
+  __syncthreads();
+  align_block(topk_ids, M * topk, E, bs, nullptr, sorted, sorted_size, eids, blocks, ntpp, wave_counts);
+}
+
 // ---- split-cover alignment (marlin_moe/split_align.py:173-224's layout) ----------------
 
 // Block sizes of the split lists, largest first.
@@ -1666,6 +1815,50 @@ extern "C" int moe_split_align(const int32_t* topk_ids, int64_t numel, int64_t n
   hipLaunchKernelGGL(marlin::moe_split_align_kernel, dim3(1), dim3(marlin::kAlignThreads), lds, s, topk_ids,
                      numel, int(num_experts), expert_map, cover, lists, wave_counts);
   return check_launch("moe_split_align");
+}
+
+extern "C" int moe_route(const void* x, int x_dtype, int64_t M, int64_t K, int64_t x_stride,
+                         const void* weight, const float* bias, int64_t num_experts, int64_t topk,
+                         int scoring, int renormalize, float scale, int64_t block_size,
+                         const uint8_t* is_padding, float* logits, float* topk_weights,
+                         int32_t* topk_ids, int32_t* sorted, int64_t sorted_numel,
+                         int32_t* expert_ids, int64_t expert_ids_numel, int32_t* ntpp,
+                         void* stream) {
+  using namespace vq;
+  if (x_dtype != kBF16 && x_dtype != kFP16) return fail("moe_route: bf16 or fp16 x and weight");
+  if (M <= 0 || M > (int64_t(1) << 24)) return fail("moe_route: 1 <= M <= 2^24 rows");
+  if (K <= 0 || K % 128 != 0 || K > (int64_t(1) << 24)) return fail("moe_route: K % 128 == 0");
+  if (x_stride < K || x_stride % 8 != 0) return fail("moe_route: x rows 16-byte aligned, stride >= K");
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (reinterpret_cast<uintptr_t>(weight) & 15) != 0) {
+    return fail("moe_route: 16-byte aligned x and weight");
+  }
+  if (num_experts <= 0 || num_experts > marlin::kRouteMaxExperts) return fail("moe_route: 1 <= E <= 1024");
+  if (topk <= 0 || topk > num_experts || topk > 64) return fail("moe_route: 1 <= topk <= min(E, 64)");
+  if (scoring != 0 && scoring != 1) return fail("moe_route: scoring 0 (softmax) or 1 (sigmoid + bias)");
+  if (scoring == 1 && bias == nullptr) return fail("moe_route: sigmoid scoring needs the bias");
+  int wave_counts = 0;
+  size_t lds = 0;
+  if (int rc = marlin::align_checks(M * topk, num_experts, block_size, sorted_numel, expert_ids_numel,
+                                    wave_counts, lds)) {
+    return rc;
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(unsigned((num_experts + 15) / 16), unsigned((M + 15) / 16));
+  if (x_dtype == kBF16) {
+    hipLaunchKernelGGL(marlin::route_logits_kernel<true>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(weight),
+                       M, K, num_experts, logits);
+  } else {
+    hipLaunchKernelGGL(marlin::route_logits_kernel<false>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(weight),
+                       M, K, num_experts, logits);
+  }
+  if (int rc = check_launch("moe_route logits")) return rc;
+  hipLaunchKernelGGL(marlin::route_select_align_kernel, dim3(1), dim3(marlin::kAlignThreads), lds, s,
+                     logits, bias, M, int(num_experts), int(topk), scoring, renormalize, scale,
+                     is_padding, topk_weights, topk_ids, int(block_size), sorted, sorted_numel,
+                     expert_ids, expert_ids_numel, ntpp, wave_counts);
+  return check_launch("moe_route select_align");
 }
 
 extern "C" int marlin_moe_align_permute(const int32_t* topk_ids, int64_t numel, int64_t num_experts,

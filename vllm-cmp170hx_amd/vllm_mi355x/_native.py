@@ -103,6 +103,14 @@ SIGNATURES = {
     "moe_sum_add": (c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "moe_align_block_size": (c_int, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64,
                                      c_vp, c_vp]),
+    "moe_route": (c_int, [
+        c_vp, c_int, c_i64, c_i64, c_i64,        # x, x_dtype, M, K, x_stride
+        c_vp, c_vp, c_i64, c_i64,                # weight, bias, num_experts, topk
+        c_int, c_int, ctypes.c_float, c_i64,     # scoring, renormalize, scale, block_size
+        c_vp, c_vp, c_vp, c_vp,                  # is_padding, logits, topk_weights, topk_ids
+        c_vp, c_i64, c_vp, c_i64, c_vp,          # sorted, numel, expert_ids, numel, ntpp
+        c_vp,                                    # stream
+    ]),
     "moe_split_align": (c_int, [
         c_vp, c_i64, c_i64, c_vp, c_vp, c_i64,  # topk_ids, numel, num_experts, expert_map, cover, rows
         c_vp, c_vp, c_vp, c_vp, c_vp,            # sorted lists 64 / 48 / 32 / 16, sorted_numel[4]
