@@ -173,3 +173,11 @@ def test_reference_loader_accepts_the_marlin_library():
         "topk_weights moe_block_size top_k mul_topk_weights b_type_id size_m size_n "
         "size_k use_atomic_add use_fp32_reduce is_zp_float thread_k thread_n "
         "blocks_per_sm c_tmp redo")
+
+
+def test_moe_launch_rows_keeps_offsets_in_32_bits():
+    from vllm_mi355x.kernels.exl3 import ops
+    rows = ops.moe_launch_rows(7168, 2048, 9)
+    assert rows == (2 ** 31 - 1) // (4 * 7168 * 9)
+    assert rows * 9 * 7168 * 4 <= 2 ** 31 - 1 < (rows + 1) * 9 * 7168 * 4
+    assert ops.moe_launch_rows(100, 300, 8) == (2 ** 31 - 1) // (4 * 384 * 8)

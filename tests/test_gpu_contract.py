@@ -299,3 +299,34 @@ def test_moe_expert_trellis_at_2_byte_offsets(ops, device, bits_x2):
     expected = O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map, intermediate,
                          out_dtype=code)
     _assert_moe_close(_out_np(out), _oracle_f32(expected, code), "unaligned expert trellis")
+
+
+def test_moe_out_row_chunks_match_one_call(device):
+    """ops.moe_out / moe_out_v2 in row chunks (forced small here; automatic
+    above the 32-bit workspace offset limit) give the single call's outputs
+    bitwise: the calls are small enough to stay on the GEMV, whose tokens
+    are independent."""
+    from vllm_mi355x.kernels.exl3 import ops
+    ops.ensure_extension()
+    rng = np.random.default_rng(81)
+    hidden, intermediate, experts, topk, rows = 256, 128, 4, 2, 11
+    layer = Layer(rng, experts, hidden, intermediate, [(6, 2)], device, scales="sign")
+    ids = _dev(np.stack([rng.permutation(experts)[:topk] for _ in range(rows)]), device)
+    weights = _dev(rng.random((rows, topk)).astype(np.float32), device)
+    emap = _dev(np.arange(experts, dtype=np.int64), device)
+    _, _, x = _acts(rng, rows, hidden, "bf16", device)
+    ws = torch.empty(ops.moe_workspace_size(rows, hidden, intermediate, topk, experts),
+                     dtype=torch.float32, device=device)
+    for v2 in (False, True):
+        outs = []
+        for chunk in (None, 3):
+            out = torch.empty_like(x)
+            if v2:
+                ops.moe_out_v2(x, ids, weights, layer.ptrs, layer.meta, emap, intermediate, 6, out, ws,
+                               row_chunk=chunk)
+            else:
+                ops.moe_out(x, ids, weights, layer.ptrs, layer.meta, emap, intermediate, out, ws,
+                            row_chunk=chunk)
+            outs.append(out)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), f"v2={v2}"

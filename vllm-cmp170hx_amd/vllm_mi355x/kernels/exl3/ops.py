@@ -164,23 +164,49 @@ def moe_workspace_size_v2(max_rows: int, hidden_size: int, intermediate_size: in
                                                    local_experts)
 
 
+def moe_launch_rows(hidden: int, intermediate_size: int, topk: int) -> int:
+    """Most rows one MoE launch takes: its workspace rows (rows * topk
+    assignments of the padded hidden / intermediate width, FP32) are
+    addressed with 32-bit byte offsets, so larger calls run in row chunks
+    (the reference chunks its calls the same way, quant.py:1898-1910)."""
+    kmax = max(-(-hidden // 128) * 128, -(-intermediate_size // 128) * 128)
+    return max(1, (2 ** 31 - 1) // (4 * kmax * max(1, topk)))
+
+
+def _chunked_moe(op, x, topk_ids, topk_weights, args, out, workspace, tail, row_chunk):
+    rows = x.shape[0]
+    chunk = row_chunk or moe_launch_rows(x.shape[1], args[3], topk_ids.shape[1])
+    if rows <= chunk:
+        op(x, topk_ids, topk_weights, *args, out, workspace, *tail)
+        return
+    for r0 in range(0, rows, chunk):
+        r1 = min(rows, r0 + chunk)
+        op(x[r0:r1], topk_ids[r0:r1], topk_weights[r0:r1], *args, out[r0:r1], workspace, *tail)
+
+
 def moe_out(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
-            intermediate_size: int, out, workspace, swiglu_limit: float = 0.0) -> None:
+            intermediate_size: int, out, workspace, swiglu_limit: float = 0.0,
+            row_chunk: int | None = None) -> None:
     """Routed experts; swiglu_limit > 0 clamps the FP32 gate from above and
-    up on both sides before SiLU(gate) * up (reference ops.py:585-616)."""
+    up on both sides before SiLU(gate) * up (reference ops.py:585-616).
+    Calls above moe_launch_rows rows (or ``row_chunk``) run in row chunks,
+    the workspace sized for one chunk."""
     ensure_extension()
-    torch.ops._exl3_C.moe_out(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
-                              intermediate_size, out, workspace, swiglu_limit)
+    _chunked_moe(torch.ops._exl3_C.moe_out, x, topk_ids, topk_weights,
+                 (packed_ptrs, packed_meta, expert_map, intermediate_size), out, workspace,
+                 (swiglu_limit,), row_chunk)
 
 
 def moe_out_v2(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
                intermediate_size: int, bits_x2: int, out, workspace,
-               swiglu_limit: float = 0.0) -> None:
+               swiglu_limit: float = 0.0, row_chunk: int | None = None) -> None:
     """moe_out for a layer whose routed matrices all have rate bits_x2
-    (mul1), with the decode specialized for that rate."""
+    (mul1), with the decode specialized for that rate (row chunks as
+    moe_out)."""
     ensure_extension()
-    torch.ops._exl3_C.moe_out_v2(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
-                                 intermediate_size, bits_x2, out, workspace, swiglu_limit)
+    _chunked_moe(torch.ops._exl3_C.moe_out_v2, x, topk_ids, topk_weights,
+                 (packed_ptrs, packed_meta, expert_map, intermediate_size, bits_x2), out, workspace,
+                 (swiglu_limit,), row_chunk)
 
 
 def ple_decode_out(packed_rows, global_ids, head_bias, head_offsets, head_vocab_sizes,
