@@ -266,7 +266,10 @@ int exl3_ple_decode_out(const void* packed_rows, int64_t rows, int64_t words,
  * a_stride elements (a_stride % 8 == 0), at least ceil(n_slots / top_k)
  * rows; block_size a multiple of 8 up to 64.  part needs ksplit * n_slots *
  * N floats (mode PARTIAL); out rows of out_stride elements (STORE / TOPK,
- * ksplit 1).  Rows of unrouted slots are left untouched.
+ * ksplit 1).  Rows of unrouted slots are left untouched.  sorted == NULL
+ * (and ntpp NULL): identity routing, block b is slot b alone and
+ * expert_ids[b] its local expert (expert_ids_numel >= n_slots): one token's
+ * slots need no alignment launch.
  * Replaces _ampere_marlin_C::decode_gemm_orig / decode_gemm_v2
  * (csrc/ampere_marlin/decode_orig.cu:361-390, decode_v2.cu:395-399) and
  * prefill_tile_gemm (csrc/ampere_marlin/prefill_tiles.cu:12-26, upstream

@@ -239,13 +239,15 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
   const bool tile_ok = tile < (g.N >> 6);
   const int b = blockIdx.y;
   const int ks = blockIdx.z;
-  if (int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
+  if (g.sorted && int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
   // (a vector load: the kernel writes memory the compiler cannot tell apart)
   const int e = vq::uniform(g.eids[b]);
   if (e < 0 || e >= g.experts) return;
   if (tid < kMaxBlock) {
     int slot = -1;
-    if (tid < g.bs) {
+    if (!g.sorted) {
+      slot = tid == 0 ? b : -1;  // identity routing: block b is slot b alone
+    } else if (tid < g.bs) {
       const int sid = g.sorted[int64_t(b) * g.bs + tid];
       if (sid >= 0 && sid < g.n_slots) slot = sid;
     }
@@ -537,13 +539,15 @@ __global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direc
   }
   const int b = blockIdx.y;
   const int ks = blockIdx.z;
-  if (int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
+  if (g.sorted && int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
   // (a vector load: the kernel writes memory the compiler cannot tell apart)
   const int e = vq::uniform(g.eids[b]);
   if (e < 0 || e >= g.experts) return;
   if (tid < kMaxBlock) {
     int slot = -1;
-    if (tid < g.bs) {
+    if (!g.sorted) {
+      slot = tid == 0 ? b : -1;  // identity routing: block b is slot b alone
+    } else if (tid < g.bs) {
       const int sid = g.sorted[int64_t(b) * g.bs + tid];
       if (sid >= 0 && sid < g.n_slots) slot = sid;
     }
@@ -1523,8 +1527,16 @@ int prepare_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
   if (!aligned16(a) || !aligned16(w) || !aligned16(scales)) {
     return fail("a, w and s must be 16-byte aligned");
   }
-  // every routed block holds at least one slot, and routed blocks come first
-  blocks = std::min(std::min<int64_t>(sorted_numel / block_size, expert_ids_numel), n_slots);
+  // every routed block holds at least one slot, and routed blocks come first;
+  // without sorted ids (identity routing), block b is slot b and
+  // expert_ids[b] its local expert
+  if (!sorted) {
+    if (expert_ids_numel < n_slots) return fail("identity routing: one expert id per slot");
+    blocks = n_slots;
+  } else {
+    if (!ntpp) return fail("routing: num_tokens_post_pad required with sorted ids");
+    blocks = std::min(std::min<int64_t>(sorted_numel / block_size, expert_ids_numel), n_slots);
+  }
   if (blocks > 65535) return fail("too many aligned blocks");
   const int64_t groups = K / 128;
   if (ksplit <= 0 || groups % ksplit != 0 || ksplit > 65535) {

@@ -68,7 +68,9 @@ def _on(t: torch.Tensor, device: torch.device, name: str) -> None:
 
 def gemm(a, w, s, sorted_ids, expert_ids, ntpp, topk_w, top_k, n_slots, K, N, block_size, mode,
          ksplit, part=None, out=None) -> None:
-    """marlin_moe_gemm on torch tensors (checks of decode_orig.cu:361-375)."""
+    """marlin_moe_gemm on torch tensors (checks of decode_orig.cu:361-375).
+    sorted_ids = ntpp = None: identity routing, block b is slot b alone and
+    expert_ids[b] its local expert (one expert id per slot)."""
     _require(a.dtype in _DTYPE_CODES and a.dim() == 2 and a.stride(1) == 1,
              "a: bf16 or fp16, unit inner stride")
     _require(s.dtype == a.dtype, "scales must have the activation dtype")
@@ -78,11 +80,15 @@ def gemm(a, w, s, sorted_ids, expert_ids, ntpp, topk_w, top_k, n_slots, K, N, bl
              "w: int32 [E, K/16, 2N]")
     _require(s.dim() == 3 and s.size(0) == w.size(0) and s.size(1) * 128 == K and s.size(2) == N,
              "s: [E, K/128, N]")
-    _require(sorted_ids.dtype == torch.int32 and expert_ids.dtype == torch.int32
-             and ntpp.dtype == torch.int32, "routing dtypes")
+    identity = sorted_ids is None
+    _require(identity == (ntpp is None), "sorted ids and num_tokens_post_pad come together")
+    _require(expert_ids.dtype == torch.int32 and expert_ids.is_contiguous() and
+             (identity or (sorted_ids.dtype == torch.int32 and ntpp.dtype == torch.int32)),
+             "routing dtypes")
     for t, name in ((w, "w"), (s, "s"), (sorted_ids, "sorted"), (expert_ids, "eids"),
                     (ntpp, "ntpp")):
-        _on(t, a.device, name)
+        if t is not None:
+            _on(t, a.device, name)
     if topk_w is not None:
         _require(topk_w.dtype == torch.float32 and topk_w.is_contiguous(), "topk weights fp32")
         _on(topk_w, a.device, "topk_w")
@@ -97,8 +103,9 @@ def gemm(a, w, s, sorted_ids, expert_ids, ntpp, topk_w, top_k, n_slots, K, N, bl
     with torch.cuda.device(a.device):
         status = lib.marlin_moe_gemm(
             a.data_ptr(), _DTYPE_CODES[a.dtype], a.size(0), a.stride(0), w.data_ptr(),
-            s.data_ptr(), w.size(0), sorted_ids.data_ptr(), sorted_ids.numel(),
-            expert_ids.data_ptr(), expert_ids.numel(), ntpp.data_ptr(),
+            s.data_ptr(), w.size(0), 0 if identity else sorted_ids.data_ptr(),
+            0 if identity else sorted_ids.numel(),
+            expert_ids.data_ptr(), expert_ids.numel(), 0 if identity else ntpp.data_ptr(),
             0 if topk_w is None else topk_w.data_ptr(), int(top_k), int(n_slots), int(K), int(N),
             int(block_size), int(mode), int(ksplit),
             0 if part is None else part.data_ptr(), 0 if part is None else part.numel(),

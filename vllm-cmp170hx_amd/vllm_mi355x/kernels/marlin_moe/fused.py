@@ -175,12 +175,18 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
                        slots, N, K, bs, _C.MODE_TOPK, 1, out=buf["c3"])
         moe_sum(buf["c3"].view(M, topk, K), out, local, E)
         return out
-    kernel_moe_align_block_size(local, E, bs, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
-                                None)
-    _C.gemm(hidden_states, w1, w1_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], None,
+    if M == 1 and path is None:
+        # one token: its top-k slots route to distinct experts, so each slot
+        # is its own block (identity routing, no alignment launch)
+        sorted_ids, expert_ids, ntpp = None, local.view(-1), None
+    else:
+        kernel_moe_align_block_size(local, E, bs, buf["sorted"], buf["expert_ids"], buf["ntpp"],
+                                    None, None)
+        sorted_ids, expert_ids, ntpp = buf["sorted"], buf["expert_ids"], buf["ntpp"]
+    _C.gemm(hidden_states, w1, w1_scale, sorted_ids, expert_ids, ntpp, None,
             topk, slots, K, 2 * N, bs, _C.MODE_PARTIAL, ks, part=buf["part"])
     _C.act(buf["part"], local.view(-1), ks, slots, N, limit, buf["h"])
-    _C.gemm(buf["h"], w2, w2_scale, buf["sorted"], buf["expert_ids"], buf["ntpp"], tw, 1, slots,
+    _C.gemm(buf["h"], w2, w2_scale, sorted_ids, expert_ids, ntpp, tw, 1, slots,
             N, K, bs, _C.MODE_TOPK, 1, out=buf["c3"])
     moe_sum(buf["c3"].view(M, topk, K), out, local, E)
     return out
