@@ -842,23 +842,32 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   const int64_t max_tasks =
       std::min<int64_t>(assignments, (assignments + task_rows - 1) / task_rows + local_experts);
   // experts with enough rows run on the tile GEMM (fixed rates up to 4 bits)
+  // Experts with enough rows run on the tile GEMM (fixed rates up to 4
+  // bits).  Tile tasks = sum over those experts of ceil(rows / 128), at most
+  // assignments / tile_rows for a threshold up to 64 rows; when that bound
+  // is under the workgroup minimum (enough tasks for kMinTileBlocks
+  // workgroups in the narrower projection) no call can have tile tasks and
+  // the tile launches are left out.
   const int tile_rows = exl3::tile_min_rows();
-  const bool tiles = fixed > 0 && exl3::tile_rate(fixed) && assignments >= tile_rows;
-  const int64_t max_tiles = tiles ? std::min<int64_t>(assignments, assignments / exl3::kTileRows +
-                                                                       assignments / tile_rows + 1)
-                                  : 0;
+  const int64_t narrow = std::min(lay.hpad, lay.ipad);
+  const int min_tile_tasks = exl3::tile_min_tasks(
+      int((exl3::kMinTileBlocks * exl3::kTileCols + narrow - 1) / narrow));
+  int64_t max_tiles = 0;
+  if (fixed > 0 && exl3::tile_rate(fixed) && assignments >= tile_rows) {
+    max_tiles = tile_rows <= 64 ? assignments / tile_rows
+                                : assignments / exl3::kTileRows + assignments / tile_rows + 1;
+    max_tiles = std::min<int64_t>(max_tiles, assignments);
+    if (max_tiles < min_tile_tasks) max_tiles = 0;
+  }
+  const bool tiles = max_tiles > 0;
   if (any && (max_tasks > 65535 || max_tiles > 65535)) {
     return fail("EXL3 MoE has too many routed assignments");
   }
   if (any) {
     int* table = reinterpret_cast<int*>(workspace + lay.ints());
-    // enough tile tasks for kMinTileBlocks workgroups in the narrower
-    // projection's launch
-    const int64_t narrow = std::min(lay.hpad, lay.ipad);
-    const int min_tile_tasks = int((exl3::kMinTileBlocks * exl3::kTileCols + narrow - 1) / narrow);
     hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads),
                        size_t(4 * local_experts + 2) * sizeof(int), s, routing, assignments, task_rows,
-                       tiles ? tile_rows : 0, exl3::tile_min_tasks(min_tile_tasks), table);
+                       tiles ? tile_rows : 0, min_tile_tasks, table);
     if (int rc = check_launch("exl3 moe_route")) return rc;
     auto tile = [&](int projection, int64_t kp, int64_t np, int64_t in_off, int64_t out_off) {
       exl3::TileArgs t{};
@@ -876,8 +885,12 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       t.projection = projection;
       t.moe_out = workspace + out_off;
       t.col_tiles = int((np + exl3::kTileCols - 1) / exl3::kTileCols);
-      // (column tile, task) in one dimension, tasks padded to a multiple of 8
-      const dim3 grid(unsigned(t.col_tiles * ((max_tiles + 7) / 8 * 8)));
+      // per XCD: up to ceil(max_tiles / 8) tasks in groups of task_group,
+      // each group task_group x col_tiles workgroups
+      const int64_t per_xcd = (max_tiles + 7) / 8;
+      t.task_group = int(std::min<int64_t>(8, per_xcd));
+      const int64_t groups = (per_xcd + t.task_group - 1) / t.task_group;
+      const dim3 grid{unsigned(8 * groups * t.task_group * t.col_tiles), 1u, 1u};
       switch (fixed) {
 #define VQ_TILE(B) case B: hipLaunchKernelGGL((exl3::tile_gemm<B, 2, true>), grid, dim3(exl3::kTileThreads), 0, s, t); break;
         VQ_TILE(2) VQ_TILE(3) VQ_TILE(4) VQ_TILE(5) VQ_TILE(6) VQ_TILE(7) VQ_TILE(8)

@@ -92,7 +92,8 @@ struct TileArgs {
   const int64_t* meta;
   int projection;
   float* moe_out;
-  int col_tiles;           // column tiles per task (the 1-D grid's inner size)
+  int col_tiles;           // column tiles per task
+  int task_group;          // tasks per group in an XCD's order (1..8)
 };
 
 typedef __attribute__((address_space(3))) void* tile_lds_ptr_t;
@@ -165,15 +166,26 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   const int m = lane & 15;
   const int L = 4 * (m & 7) + g;
   // Dense: grid (column tile, row tile).  MoE: a 1-D grid; workgroups are
-  // dispatched to the 8 XCDs round-robin (workgroup p on XCD p % 8), and
-  // task t runs on XCD t % 8 with all its column tiles one after another,
-  // so that XCD's L2 fetches the task's activations once for all of them.
+  // dispatched to the 8 XCDs round-robin (workgroup p on XCD p % 8, its
+  // p / 8-th).  XCD x runs the contiguous task range [x P, x P + P),
+  // P = ceil(tasks / 8): the tasks of one expert share an XCD.  Within it,
+  // groups of task_group tasks run column-major (column tile 0 of each task
+  // of the group, then column tile 1, ...), so the workgroups resident at
+  // once on the XCD hold a few tasks x a few column tiles at the same K
+  // steps, and its L2 fetches each activation tile and each weight stripe
+  // once for all of them.
   int64_t col_tile = blockIdx.x;
   int moe_task = 0;
   if constexpr (kMoe) {
     const int local = int(blockIdx.x >> 3);
-    col_tile = local % a.col_tiles;
-    moe_task = (local / a.col_tiles) * 8 + int(blockIdx.x & 7);
+    const int span = a.task_group * a.col_tiles;
+    const int group = local / span;
+    const int in_group = local - group * span;
+    col_tile = in_group / a.task_group;
+    const int idx = group * a.task_group + (in_group - int(col_tile) * a.task_group);
+    const int per_xcd = (vq::uniform(a.table[2]) + 7) >> 3;
+    if (idx >= per_xcd) return;
+    moe_task = int(blockIdx.x & 7) * per_xcd + idx;
   }
   const int64_t col0 = col_tile * kTileCols;
 
