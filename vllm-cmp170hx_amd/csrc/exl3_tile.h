@@ -28,12 +28,12 @@
 //
 // Pipeline, per wavefront (one barrier a step):
 //   * trellis: LDS-DMA (buffer_load ... lds), 1 KB per step, into a ring of
-//     4 slots, issued 4 steps ahead; a step's ring words are read two steps
-//     before its MFMAs, and it is decoded (into registers) one step before;
+//     4 slots, issued 4 steps ahead; a step's ring words are read and
+//     decoded (into registers) one step before its MFMAs;
 //   * activations: LDS-DMA of the tile's 8 row blocks per step, 2 per
 //     wavefront, into 3 buffers, issued 2 steps ahead; the
 //     operands of row block rb + 2 are read under the MFMAs of rb;
-//   * step s: issue the activation loads of s + 2, read the words of s + 2,
+//   * step s: issue the activation loads of s + 2, read the words of s + 1,
 //     issue the trellis load of s + 4, run the MFMAs of s with the decode of
 //     s + 1 between them (the VALU work of one step under the matrix work of
 //     the other), wait for this wavefront's loads of s + 1, barrier.
@@ -127,6 +127,17 @@ __device__ __forceinline__ void tile_wait(half8_t& a) {
 template <int kWords>
 __device__ __forceinline__ void tile_wait_last(half8_t& a, uint32_t (&w)[2][2][kWords]) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a));
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) asm volatile("" : "+v"(w[p][h][i]));
+}
+// At most n LDS reads pending: a and the ring words (read before a) ready.
+template <int n, int kWords>
+__device__ __forceinline__ void tile_wait(half8_t& a, uint32_t (&w)[2][2][kWords]) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(n));
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -344,33 +355,25 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   vq::wait_vmcnt<kADma + 2>();  // T(0), T(1) and A(0) of this wavefront landed
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  uint32_t wnext[2][2][kWords];     // the words of step s + 1 (decoded during step s)
   read_words(std::integral_constant<int, 0>{});
   tile_wait_words<0>(words);
   half8_t b_cur[2][2];              // step s's B operands
   decode_pair(words, 0, b_cur);
   decode_pair(words, 1, b_cur);
-  read_words(std::integral_constant<int, 1>{});
-  tile_wait_words<0>(words);
-#pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < kWords; ++i) wnext[p][h][i] = words[p][h][i];
 
   // step s, its trellis in ring slot kSlot = s % 4 (the loop runs four steps
   // an iteration: steps is a multiple of 4): the MFMAs of kRB row blocks of
-  // step s on b_cur, with the decode of step s + 1 scheduled between them,
-  // and the words of step s + 2 read
+  // step s on b_cur, with the words of step s + 1 read and decoded between
+  // them
   auto step = [&](int s, auto slot, auto row_blocks) {
     constexpr int kSlot = decltype(slot)::value;
     constexpr int kRB = decltype(row_blocks)::value;
     load_act(min(s + 2, last));
-    // T(s + 2) landed: after it came A(s + 1), T(s + 3), A(s + 2)
-    vq::wait_vmcnt<2 * kADma + 1>();
-    read_words(std::integral_constant<int, (kSlot + 2) % kTileRing>{});  // (past the last step: unused)
-    // this step's slot (its words read two steps ago) takes step s + 4
+    // T(s + 1) landed: after it came A(s), T(s + 2), A(s + 1), T(s + 3),
+    // A(s + 2)
+    vq::wait_vmcnt<3 * kADma + 2>();
+    read_words(std::integral_constant<int, (kSlot + 1) % kTileRing>{});  // (past the last step: unused)
+    // this step's slot (its words read and decoded a step ago) takes step s + 4
     load_trellis(min(s + 4, last));
 
     half8_t b_next[2][2];
@@ -380,15 +383,17 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     tile_read16<1 * 1024>(ah[1], a_buf);
     static_for<kRB>([&](auto rb_tag) {
       constexpr int rb = decltype(rb_tag)::value;
-      if constexpr (rb + 1 < kRB) {
+      if constexpr (rb == 0) {
+        tile_wait<1>(ah[rb], words);  // (the words were read before ah[0])
+      } else if constexpr (rb + 1 < kRB) {
         tile_wait<1>(ah[rb]);
       } else {
         tile_wait_last(ah[rb], words);
       }
       if constexpr (rb + 2 < kRB) tile_read16<(rb + 2) * 1024>(ah[rb + 2], a_buf);
       if constexpr (rb == 0) {
-        decode_pair(wnext, 0, b_next);
-        decode_pair(wnext, 1, b_next);
+        decode_pair(words, 0, b_next);
+        decode_pair(words, 1, b_next);
       }
 #pragma unroll
       for (int p = 0; p < 2; ++p)
@@ -400,10 +405,6 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     for (int p = 0; p < 2; ++p) {
       b_cur[p][0] = b_next[p][0];
       b_cur[p][1] = b_next[p][1];
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < kWords; ++i) wnext[p][h][i] = words[p][h][i];
     }
     // A(s + 1) of this wavefront landed: after it came T(s + 3), A(s + 2),
     // T(s + 4); then every wavefront's (and every read of buffer s) is done
@@ -436,6 +437,14 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   // the epilogue reuses
   vq::wait_vmcnt<0>();
   __syncthreads();
+  // Every task of a wavefront is in its 128-column block wave & 1: its two
+  // svh values are loaded once, here.  (Loads and stores share one in-order
+  // counter, so a load waited for after an output store also waits for the
+  // store's completion: a load per task would serialize the stores.)
+  const int blk = wave & 1;
+  const int64_t c0 = col0 + 128 * blk + lane;
+  const float svh0 = c0 < a.np ? vq::f16_to_f32(svh[c0]) : 0.0f;
+  const float svh1 = c0 + 64 < a.np ? vq::f16_to_f32(svh[c0 + 64]) : 0.0f;
   float* red = reinterpret_cast<float*>(&a_lds[0][0][0]);  // [16][kTileRedStride]
   static_assert(sizeof(a_lds) >= 16 * kTileRedStride * sizeof(float), "epilogue rows fit");
 #pragma unroll
@@ -455,11 +464,12 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     }
     __syncthreads();
     // (row, 128-column block) tasks: H128 over the block, times svh
-    for (int task = wave; task < 32; task += kTileWaves) {
+    static_assert(kTileWaves % 2 == 0, "task & 1 == wave & 1");
+#pragma unroll
+    for (int t = 0; t < 32 / kTileWaves; ++t) {
+      const int task = wave + kTileWaves * t;
       const int r = task >> 1;
-      const int blk = task & 1;
       const int tr = 16 * rb + r;
-      const int64_t c0 = col0 + 128 * blk + lane;
       float v0 = red[r * kTileRedStride + 128 * blk + lane];
       float v1 = red[r * kTileRedStride + 128 * blk + lane + 64];
       vq::h128_wave(v0, v1, lane);
@@ -467,17 +477,16 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
         if constexpr (kMoe) {
           if (c0 < a.np) {
             float* dst = a.moe_out + int64_t(row_id[tr]) * a.np;
-            dst[c0] = v0 * vq::f16_to_f32(svh[c0]);
-            dst[c0 + 64] = v1 * vq::f16_to_f32(svh[c0 + 64]);
+            dst[c0] = v0 * svh0;
+            dst[c0 + 64] = v1 * svh1;
           }
         } else {
           const int64_t row = int64_t(blockIdx.y) * kRows + tr;
           if (c0 < a.logical_out) {
-            vq::store_act(a.out, a.out_dtype, row * a.logical_out + c0, v0 * vq::f16_to_f32(svh[c0]));
+            vq::store_act(a.out, a.out_dtype, row * a.logical_out + c0, v0 * svh0);
           }
           if (c0 + 64 < a.logical_out) {
-            vq::store_act(a.out, a.out_dtype, row * a.logical_out + c0 + 64,
-                          v1 * vq::f16_to_f32(svh[c0 + 64]));
+            vq::store_act(a.out, a.out_dtype, row * a.logical_out + c0 + 64, v1 * svh1);
           }
         }
       }
