@@ -297,15 +297,19 @@ __device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int 
     red[(part * a.rows + r) * 128 + col] = v;
   }
   __syncthreads();
+  // svh loaded before the first output store (a load waited for after a
+  // store also waits for the store: loads and stores share one counter)
+  const int64_t c0 = base + lane;
+  const int64_t c1 = c0 + 64;
+  const float svh0 = vq::f16_to_f32(a.svh[c0]);
+  const float svh1 = vq::f16_to_f32(a.svh[c1]);
   for (int r = wave; r < a.rows && wave < 4; r += 4) {
     float v0 = red[r * 128 + lane] + red[(a.rows + r) * 128 + lane];
     float v1 = red[r * 128 + lane + 64] + red[(a.rows + r) * 128 + lane + 64];
     vq::h128_wave(v0, v1, lane);
-    const int64_t c0 = base + lane;
-    const int64_t c1 = c0 + 64;
     void* out = a.out;
-    if (c0 < a.logical_out) vq::store_act(out, a.out_dtype, r * a.out_stride + c0, v0 * vq::f16_to_f32(a.svh[c0]));
-    if (c1 < a.logical_out) vq::store_act(out, a.out_dtype, r * a.out_stride + c1, v1 * vq::f16_to_f32(a.svh[c1]));
+    if (c0 < a.logical_out) vq::store_act(out, a.out_dtype, r * a.out_stride + c0, v0 * svh0);
+    if (c1 < a.logical_out) vq::store_act(out, a.out_dtype, r * a.out_stride + c1, v1 * svh1);
   }
 }
 

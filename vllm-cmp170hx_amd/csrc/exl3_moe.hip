@@ -705,15 +705,29 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
     }
   }
   __syncthreads();
-  for (int r = wave; r < nrows; r += 4) {
-    float v0 = red[r][lane];
-    float v1 = red[r][lane + 64];
-    vq::h128_wave(v0, v1, lane);
-    const int64_t c0 = 128 * int64_t(blockIdx.x) + lane;
-    const int64_t a = sorted[first + r];
-    float* dst = ws + out_offset + a * np;
-    dst[c0] = v0 * vq::f16_to_f32(svh[c0]);
-    dst[c0 + 64] = v1 * vq::f16_to_f32(svh[c0 + 64]);
+  // The rows' assignments and the block's svh are loaded before the first
+  // output store: loads and stores share one in-order counter, so a load
+  // waited for after a store also waits for the store to complete.
+  const int64_t c0 = 128 * int64_t(blockIdx.x) + lane;
+  const float svh0 = vq::f16_to_f32(svh[c0]);
+  const float svh1 = vq::f16_to_f32(svh[c0 + 64]);
+  int row_a[kRows / 4];
+#pragma unroll
+  for (int i = 0; i < kRows / 4; ++i) {
+    const int r = wave + 4 * i;
+    row_a[i] = r < nrows ? sorted[first + r] : 0;
+  }
+#pragma unroll
+  for (int i = 0; i < kRows / 4; ++i) {
+    const int r = wave + 4 * i;
+    if (r < nrows) {
+      float v0 = red[r][lane];
+      float v1 = red[r][lane + 64];
+      vq::h128_wave(v0, v1, lane);
+      float* dst = ws + out_offset + int64_t(row_a[i]) * np;
+      dst[c0] = v0 * svh0;
+      dst[c0 + 64] = v1 * svh1;
+    }
   }
 }
 

@@ -408,6 +408,14 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
     }
     if (!tile_ok) return;
 
+    // the router weights before the first store (loads and stores share one
+    // in-order counter: a load waited for after a store waits for it too)
+    float wts[kNs];
+#pragma unroll
+    for (int sb = 0; sb < kNs; ++sb) {
+      const int slot = s_slot[16 * sb + col];
+      wts[sb] = kMode == kTopk && slot >= 0 ? round_act<kBF16>(g.topk_w[slot]) : 0.0f;
+    }
     // C fragment: lane holds columns 16 j + 4 q .. +3 of token 16 sb + col
 #pragma unroll
     for (int sb = 0; sb < kNs; ++sb) {
@@ -422,7 +430,7 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
         } else {
           float x[4] = {v[0], v[1], v[2], v[3]};
           if constexpr (kMode == kTopk) {
-            const float w = round_act<kBF16>(g.topk_w[slot]);
+            const float w = wts[sb];
 #pragma unroll
             for (int u = 0; u < 4; ++u) x[u] = round_act<kBF16>(x[u]) * w;  // exact product
           }
@@ -829,6 +837,14 @@ __global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direc
       }
       return;
     }
+    // the router weights before the first store (loads and stores share one
+    // in-order counter: a load waited for after a store waits for it too)
+    float wts[kNs];
+#pragma unroll
+    for (int sb = 0; sb < kNs; ++sb) {
+      const int slot = s_slot[16 * sb + col];
+      wts[sb] = kMode == kTopk && slot >= 0 ? round_act<kBF16>(g.topk_w[slot]) : 0.0f;
+    }
 #pragma unroll
     for (int x = 0; x < kDirectTiles; ++x) {
       if (!tile_ok[x]) continue;
@@ -845,7 +861,7 @@ __global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direc
           } else {
             float y[4] = {v[0], v[1], v[2], v[3]};
             if constexpr (kMode == kTopk) {
-              const float w = round_act<kBF16>(g.topk_w[slot]);
+              const float w = wts[sb];
 #pragma unroll
               for (int u = 0; u < 4; ++u) y[u] = round_act<kBF16>(y[u]) * w;  // exact product
             }
@@ -966,18 +982,42 @@ __global__ __launch_bounds__(kThreads) void moe_sum_kernel(const uint16_t* in, i
   float acc[kVec];
 #pragma unroll
   for (int u = 0; u < kVec; ++u) acc[u] = 0.0f;
-  for (int k = 0; k < topk; ++k) {
-    if (ids) {
-      const int id = ids[t * topk + k];
-      if (id < 0 || id >= experts) continue;
-    }
-    const uint16_t* row = in + (t * topk + k) * hidden + c;
-    if constexpr (kVec == 8) {
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(row);
+  // eight slots at a time: their ids, then their rows' loads all in flight,
+  // then the sums in slot order
+  constexpr int kBatch = 8;
+  for (int k0 = 0; k0 < topk; k0 += kBatch) {
+    bool use[kBatch];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc[u] += act_f32<kBF16>(uint16_t(v[u >> 1] >> (16 * (u & 1))));
+    for (int i = 0; i < kBatch; ++i) {
+      const int k = k0 + i;
+      bool ok = k < topk;
+      if (ok && ids) {
+        const int id = ids[t * topk + k];
+        ok = id >= 0 && id < experts;
+      }
+      use[i] = ok;
+    }
+    if constexpr (kVec == 8) {
+      u32x4_t v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        v[i] = use[i] ? *reinterpret_cast<const u32x4_t*>(in + (t * topk + k0 + i) * hidden + c)
+                      : u32x4_t{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        if (!use[i]) continue;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u] += act_f32<kBF16>(uint16_t(v[i][u >> 1] >> (16 * (u & 1))));
+      }
     } else {
-      acc[0] += act_f32<kBF16>(row[0]);
+      uint16_t v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) v[i] = use[i] ? in[(t * topk + k0 + i) * hidden + c] : uint16_t(0);
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        if (use[i]) acc[0] += act_f32<kBF16>(v[i]);
+      }
     }
   }
   if (shared) {
