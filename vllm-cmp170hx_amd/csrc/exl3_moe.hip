@@ -266,37 +266,81 @@ __device__ __forceinline__ int b_order(int k) {
   return (k & ~31) + g * 8 + slot;
 }
 
-// Writes one 128-input block of t (lane l holds inputs l, l + 64), scaled by
-// the assignment's power-of-two exponent, into its B-operand arrays (offsets
-// within a row fit int32: kp is checked on the host).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
 }
 
-__device__ __forceinline__ void store_block(__amdgpu_buffer_rsrc_t dst, int kp, int block, float v0,
-                                            float v1, int e, int lane) {
-  const float t0 = ldexpf(v0, e);
-  const float t1 = ldexpf(v1, e);
-  const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
-  const _Float16 l0 = _Float16(t0 - float(h0)), l1 = _Float16(t1 - float(h1));
-  const int o0 = 2 * b_order(block * 128 + lane);  // bytes
-  const int o1 = o0 + 128;  // input k + 64: two 32-input steps later
-  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, h0), dst, o0, 0, 0);
-  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, l0), dst, o0, 2 * kp, 0);
-  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, h1), dst, o1, 0, 0);
-  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, l1), dst, o1, 2 * kp, 0);
+// H128 of the blocks a wavefront holds as 16-lane rows: lane (q, l) of row
+// q holds elements 8 l .. 8 l + 7 of its block in v[0..7].  The butterfly
+// distances 1, 2, 4 pair elements of one lane, 8, 16, 32, 64 the lanes l ^ 1,
+// 2, 4, 8 of the row (DPP): every element gets the same additions, in the
+// same order of distances, as h128_wave (lower lo + hi, upper lo - hi, FP32
+// round to nearest), then the scale.
+__device__ __forceinline__ void h128_rows(float (&v)[8], int l) {
+  // every sum rounded on its own: no product of the caller fused into the
+  // first additions
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int d = 1; d < 8; d <<= 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if ((j & d) == 0) {
+        const float lo = v[j], hi = v[j | d];
+        v[j] = lo + hi;
+        v[j | d] = lo - hi;
+      }
+    }
+  }
+  auto cross = [&](auto dist) {
+    constexpr int d = decltype(dist)::value;
+    const bool upper = (l & d) != 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float o = vq::xor_lanes<d>(v[j], l);
+      v[j] = o + (upper ? -v[j] : v[j]);
+    }
+  };
+  cross(std::integral_constant<int, 1>{});
+  cross(std::integral_constant<int, 2>{});
+  cross(std::integral_constant<int, 4>{});
+  cross(std::integral_constant<int, 8>{});
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] *= vq::kH128Scale;
+}
+
+// Writes inputs k0 .. k0 + 7 (k0 % 8 == 0) of t, scaled by the row's
+// power-of-two exponent, into the row's B-operand arrays: in b_order, inputs
+// 2i and 2i + 1 of the eight are adjacent halves (one dword store each) at
+// (k0 & ~31) + 8 i + 4 ((k0 >> 4) & 1) + 2 ((k0 >> 3) & 1).
+__device__ __forceinline__ void store8(__amdgpu_buffer_rsrc_t dst, int kp, int k0, const float (&v)[8],
+                                       int e) {
+  const int base = (k0 & ~31) + 4 * ((k0 >> 4) & 1) + 2 * ((k0 >> 3) & 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float t0 = ldexpf(v[2 * i], e);
+    const float t1 = ldexpf(v[2 * i + 1], e);
+    const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
+    const _Float16 l0 = _Float16(t0 - float(h0)), l1 = _Float16(t1 - float(h1));
+    const uint32_t hw = uint32_t(__builtin_bit_cast(uint16_t, h0)) | (uint32_t(__builtin_bit_cast(uint16_t, h1)) << 16);
+    const uint32_t lw = uint32_t(__builtin_bit_cast(uint16_t, l0)) | (uint32_t(__builtin_bit_cast(uint16_t, l1)) << 16);
+    const int o = 2 * (base + 8 * i);  // bytes
+    __builtin_amdgcn_raw_buffer_store_b32(hw, dst, o, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(lw, dst, o, 2 * kp, 0);
+  }
 }
 
 // kActivate false: gate/up input, t = H128(x[a / topk] * suh_projection);
 // true: down input from the gate/up results (already H128 * svh):
 // clamp, SiLU(g) * u * suh_down, H128, into the act region.
-// One workgroup per local assignment: wavefront w forms blocks w, w + 4, ...
-// (the first kCache of them kept in registers, their loads issued together
-// at clamped block indices) for the row maximum of |t|, then writes the high
-// / low parts at the row's one power-of-two scale, so the expert GEMV sums
-// the whole row before it unscales; blocks past the register cache are
-// formed again (the same operations, so the same values).  An expert whose
-// matrix is not kp rows long gets NaN operands (its suh is not read).
+// One workgroup per local assignment.  A wavefront forms four blocks at a
+// time (block group G: blocks 4 G .. 4 G + 3, one per 16-lane row, eight
+// inputs a lane); wavefront w takes groups w, w + 4, ... (the first kCache
+// of them kept in registers, their loads issued together at clamped group
+// indices) for the row maximum of |t|, then writes the high / low parts at
+// the row's one power-of-two scale, so the expert GEMV sums the whole row
+// before it unscales; groups past the register cache are formed again (the
+// same operations, so the same values).  An expert whose matrix is not kp
+// rows long gets NaN operands (its suh is not read).
 template <bool kActivate, int kCache>
 __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, int x_dtype,
                                                 int64_t hidden, int64_t intermediate, int projection,
@@ -305,8 +349,11 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   __shared__ uint32_t row_max;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int q = lane >> 4;   // the lane's block within a group
+  const int l = lane & 15;   // its eight inputs within the block: 8 l ..
   const int64_t kp = kActivate ? lay.ipad : lay.hpad;
   const int64_t blocks = kp / 128;
+  const int64_t groups = (blocks + 3) / 4;
   if (int64_t(blockIdx.x) >= int64_t(table[0])) return;
   const int64_t a = table[4 + blockIdx.x];
   const int64_t e = local_expert(routing, a);
@@ -324,63 +371,91 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
       make_rsrc(static_cast<const uint16_t*>(x) + (a / routing.topk) * hidden, uint32_t(hidden) * 2u);
   const __amdgpu_buffer_rsrc_t g_r = make_rsrc(ws + lay.gate() + a * lay.ipad, uint32_t(lay.ipad) * 4u);
   const __amdgpu_buffer_rsrc_t u_r = make_rsrc(ws + lay.up() + a * lay.ipad, uint32_t(lay.ipad) * 4u);
-  auto form = [&](int64_t block, float& v0, float& v1) {
-    const int k0 = int(block) * 128 + lane;
-    const int k1 = k0 + 64;
+  // the first input of the lane's eight in group G (clamped to the last block)
+  auto first_k = [&](int64_t G) { return int(min(4 * G + q, blocks - 1)) * 128 + 8 * l; };
+  // eight 16-bit inputs k0 .. k0 + 7 of a buffer of len valid ones: one
+  // 16-byte load, or, for the chunk that reaches past len, 2-byte loads
+  // (a buffer load partly past the end returns zero as a whole; each 2-byte
+  // load past it returns zero)
+  auto load8 = [&](__amdgpu_buffer_rsrc_t r, int k0, int len, uint16_t (&h)[8]) {
+    if (k0 + 8 <= len) {
+      const u32x4_t w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, 2 * k0, 0, 0));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = uint16_t(w[j >> 1] >> (16 * (j & 1)));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = __builtin_amdgcn_raw_buffer_load_b16(r, 2 * (k0 + j), 0, 0);
+    }
+  };
+  auto form = [&](int64_t G, float (&v)[8]) {
+    const int k0 = first_k(G);
     if (bad) {
-      v0 = v1 = __builtin_nanf("");
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = __builtin_nanf("");
       return;
     }
     if constexpr (!kActivate) {
-      const uint16_t x0 = __builtin_amdgcn_raw_buffer_load_b16(x_r, 2 * k0, 0, 0);
-      const uint16_t x1 = __builtin_amdgcn_raw_buffer_load_b16(x_r, 2 * k1, 0, 0);
-      const uint16_t s0 = __builtin_amdgcn_raw_buffer_load_b16(suh_r, 2 * k0, 0, 0);
-      const uint16_t s1 = __builtin_amdgcn_raw_buffer_load_b16(suh_r, 2 * k1, 0, 0);
-      v0 = u16_act(x0, x_dtype) * vq::f16_to_f32(s0);
-      v1 = u16_act(x1, x_dtype) * vq::f16_to_f32(s1);
-    } else {
-      const float gv[2] = {__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g_r, 4 * k0, 0, 0)),
-                           __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g_r, 4 * k1, 0, 0))};
-      const float uv[2] = {__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(u_r, 4 * k0, 0, 0)),
-                           __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(u_r, 4 * k1, 0, 0))};
-      const uint16_t sd[2] = {__builtin_amdgcn_raw_buffer_load_b16(suh_r, 2 * k0, 0, 0),
-                              __builtin_amdgcn_raw_buffer_load_b16(suh_r, 2 * k1, 0, 0)};
-      float v[2];
+      uint16_t xh[8], sh[8];
+      load8(x_r, k0, in_len, xh);
+      load8(suh_r, k0, in_len, sh);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int k = i ? k1 : k0;
-        v[i] = 0.0f;
-        if (k < intermediate) {
-          float gg = gv[i], uu = uv[i];
+      for (int j = 0; j < 8; ++j) v[j] = u16_act(xh[j], x_dtype) * vq::f16_to_f32(sh[j]);
+    } else {
+      float gv[8], uv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4_t gq = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(g_r, 4 * k0 + 16 * h, 0, 0));
+        const u32x4_t uq = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(u_r, 4 * k0 + 16 * h, 0, 0));
+        // each element to a scalar before the bit cast: a bit cast of a
+        // vector element expression is emitted as a read of element 0
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t gw = gq[i], uw = uq[i];
+          gv[4 * h + i] = __builtin_bit_cast(float, gw);
+          uv[4 * h + i] = __builtin_bit_cast(float, uw);
+        }
+      }
+      uint16_t sd[8];
+      load8(suh_r, k0, in_len, sd);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[j] = 0.0f;
+        if (k0 + j < intermediate) {
+          float gg = gv[j], uu = uv[j];
           if (limit > 0.0f) {
             gg = fminf(gg, limit);
             uu = fminf(fmaxf(uu, -limit), limit);
           }
           const float silu = gg / (1.0f + expf(-gg));
-          v[i] = (silu * uu) * vq::f16_to_f32(sd[i]);
+          v[j] = (silu * uu) * vq::f16_to_f32(sd[j]);
         }
       }
-      v0 = v[0];
-      v1 = v[1];
     }
-    vq::h128_wave(v0, v1, lane);
+    h128_rows(v, l);
   };
+  auto live = [&](int64_t G) { return 4 * G + q < blocks; };
   if (threadIdx.x == 0) row_max = 0u;
   __syncthreads();
   float mx = 0.0f;
-  float c0[kCache], c1[kCache];
+  float c[kCache][8];
 #pragma unroll
   for (int i = 0; i < kCache; ++i) {
-    form(min(int64_t(wave + 4 * i), blocks - 1), c0[i], c1[i]);
+    form(min(int64_t(wave + 4 * i), groups - 1), c[i]);
   }
 #pragma unroll
   for (int i = 0; i < kCache; ++i) {
-    if (wave + 4 * i < blocks) mx = fmaxf(mx, fmaxf(fabsf(c0[i]), fabsf(c1[i])));
+    if (wave + 4 * i < groups && live(wave + 4 * i)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(c[i][j]));
+    }
   }
-  for (int64_t b = wave + 4 * kCache; b < blocks; b += 4) {
-    float v0, v1;
-    form(b, v0, v1);
-    mx = fmaxf(mx, fmaxf(fabsf(v0), fabsf(v1)));
+  for (int64_t G = wave + 4 * kCache; G < groups; G += 4) {
+    float v[8];
+    form(G, v);
+    if (live(G)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+    }
   }
   mx = vq::wave_max(mx, lane);
   if (lane == 0) atomicMax(&row_max, __builtin_bit_cast(uint32_t, mx));
@@ -389,12 +464,12 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   if (threadIdx.x == 0) exps[0] = ex;
 #pragma unroll
   for (int i = 0; i < kCache; ++i) {
-    if (wave + 4 * i < blocks) store_block(dst, int(kp), wave + 4 * i, c0[i], c1[i], ex, lane);
+    if (wave + 4 * i < groups && live(wave + 4 * i)) store8(dst, int(kp), first_k(wave + 4 * i), c[i], ex);
   }
-  for (int64_t b = wave + 4 * kCache; b < blocks; b += 4) {
-    float v0, v1;
-    form(b, v0, v1);
-    store_block(dst, int(kp), int(b), v0, v1, ex, lane);
+  for (int64_t G = wave + 4 * kCache; G < groups; G += 4) {
+    float v[8];
+    form(G, v);
+    if (live(G)) store8(dst, int(kp), first_k(G), v, ex);
   }
 }
 
@@ -927,17 +1002,18 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       return check_launch("exl3 moe_gemv");
     };
     // moe_form: one workgroup per assignment (the routed ones do work), its
-    // register cache sized to the blocks a wavefront forms
+    // register cache sized to the 4-block groups a wavefront forms
     auto form = [&](bool activate, int projection) {
-      const int64_t per_wave = ((activate ? lay.ipad : lay.hpad) / 128 + 3) / 4;
+      const int64_t groups = ((activate ? lay.ipad : lay.hpad) / 128 + 3) / 4;
+      const int64_t per_wave = (groups + 3) / 4;
       const dim3 grid{unsigned(assignments), 1u, 1u};
 #define VQ_FORM(A, C)                                                                              \
   hipLaunchKernelGGL((exl3::moe_form<A, C>), grid, dim3(256), 0, s, routing, x, x_dtype, hidden, \
                      intermediate_size, projection, table, workspace, lay, swiglu_limit)
       if (activate) {
-        if (per_wave <= 4) VQ_FORM(true, 4); else if (per_wave <= 8) VQ_FORM(true, 8); else VQ_FORM(true, 16);
+        if (per_wave <= 1) VQ_FORM(true, 1); else if (per_wave <= 2) VQ_FORM(true, 2); else VQ_FORM(true, 4);
       } else {
-        if (per_wave <= 4) VQ_FORM(false, 4); else if (per_wave <= 8) VQ_FORM(false, 8); else VQ_FORM(false, 16);
+        if (per_wave <= 1) VQ_FORM(false, 1); else if (per_wave <= 2) VQ_FORM(false, 2); else VQ_FORM(false, 4);
       }
 #undef VQ_FORM
       return check_launch("exl3 moe_form");
