@@ -128,9 +128,11 @@ __device__ __forceinline__ bool tile_expert(const Routing& r, int e, int rows, i
 }
 
 // Table (int32, in the workspace): header {routed rows, GEMV tasks, tile
-// tasks, first tile task}, the routed assignments sorted by local expert,
-// then the tasks {expert, first sorted row, rows, 0}: GEMV tasks first, tile
-// tasks after them (every task has a row, so both fit in A entries).
+// tasks, first tile task}, the routed assignments sorted by local expert
+// (the GEMV experts' rows first, then the tile experts' rows, each part in
+// expert order), then the tasks {expert, first sorted row, rows, 0}: GEMV
+// tasks first, tile tasks after them (every task has a row, so both fit in
+// A entries).
 // tile_rows: the routed-row threshold of the tile GEMM (0: no tile tasks);
 // with fewer than min_tile_tasks tile tasks in all (too few workgroups to
 // fill the chip: each runs the whole K range), every expert takes the GEMV.
@@ -143,7 +145,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
   int* row_begin = count + experts;
   int* task_begin = row_begin + experts;   // GEMV tasks, experts + 1 entries
   int* tile_begin = task_begin + experts + 1;  // tile tasks, experts + 1 entries
-  __shared__ int scan_rows[kRouteThreads];
+  __shared__ int scan_rows[kRouteThreads];   // GEMV experts' rows
+  __shared__ int scan_trows[kRouteThreads];  // tile experts' rows
   __shared__ int scan_tasks[kRouteThreads];
   __shared__ int scan_tiles[kRouteThreads];
   __shared__ int tiles_in_all;
@@ -169,49 +172,56 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
     __syncthreads();
     if (tiles_in_all < min_tile_tasks) tile_rows = 0;
   }
-  // exclusive scan of (rows, GEMV tasks, tile tasks) over experts
-  int rows = 0, tasks = 0, tile_tasks = 0;
+  // exclusive scan of (GEMV rows, tile rows, GEMV tasks, tile tasks) over
+  // experts
+  int rows = 0, trows = 0, tasks = 0, tile_tasks = 0;
   for (int e = e0; e < e1; ++e) {
     const int c = count[e];
-    rows += c;
     if (tile_rows > 0 && tile_expert(routing, e, c, tile_rows)) {
+      trows += c;
       tile_tasks += (c + kTileRows - 1) / kTileRows;
     } else {
+      rows += c;
       tasks += (c + task_rows - 1) / task_rows;
     }
   }
   scan_rows[tid] = rows;
+  scan_trows[tid] = trows;
   scan_tasks[tid] = tasks;
   scan_tiles[tid] = tile_tasks;
   __syncthreads();
   for (int d = 1; d < kRouteThreads; d <<= 1) {
     const int r = tid >= d ? scan_rows[tid - d] : 0;
+    const int q = tid >= d ? scan_trows[tid - d] : 0;
     const int t = tid >= d ? scan_tasks[tid - d] : 0;
     const int u = tid >= d ? scan_tiles[tid - d] : 0;
     __syncthreads();
     scan_rows[tid] += r;
+    scan_trows[tid] += q;
     scan_tasks[tid] += t;
     scan_tiles[tid] += u;
     __syncthreads();
   }
+  const int gemv_rows = scan_rows[kRouteThreads - 1];
   int row_at = scan_rows[tid] - rows;
+  int trow_at = gemv_rows + scan_trows[tid] - trows;
   int task_at = scan_tasks[tid] - tasks;
   int tile_at = scan_tiles[tid] - tile_tasks;
   for (int e = e0; e < e1; ++e) {
     const int c = count[e];
     const bool tile = tile_rows > 0 && tile_expert(routing, e, c, tile_rows);
-    row_begin[e] = row_at;
+    row_begin[e] = tile ? trow_at : row_at;
     task_begin[e] = task_at;
     tile_begin[e] = tile_at;
-    count[e] = row_at;  // fill cursor
-    row_at += c;
     if (tile) {
+      trow_at += c;
       tile_at += (c + kTileRows - 1) / kTileRows;
     } else {
+      row_at += c;
       task_at += (c + task_rows - 1) / task_rows;
     }
   }
-  const int total_rows = scan_rows[kRouteThreads - 1];
+  const int total_rows = gemv_rows + scan_trows[kRouteThreads - 1];
   const int total_tasks = scan_tasks[kRouteThreads - 1];
   const int total_tiles = scan_tiles[kRouteThreads - 1];
   if (tid == 0) {
@@ -238,15 +248,18 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
   for (int t = tid; t < total_tasks; t += kRouteThreads) {
     const int e = owner(task_begin, t);
     const int first = row_begin[e] + (t - task_begin[e]) * task_rows;
-    const int end = e + 1 < experts ? row_begin[e + 1] : total_rows;
+    const int end = row_begin[e] + count[e];
     task_table[t] = make_int4(e, first, min(task_rows, end - first), 0);
   }
   for (int t = tid; t < total_tiles; t += kRouteThreads) {
     const int e = owner(tile_begin, t);
     const int first = row_begin[e] + (t - tile_begin[e]) * kTileRows;
-    const int end = e + 1 < experts ? row_begin[e + 1] : total_rows;
+    const int end = row_begin[e] + count[e];
     task_table[total_tasks + t] = make_int4(e, first, min(kTileRows, end - first), 0);
   }
+  __syncthreads();
+  for (int e = e0; e < e1; ++e) count[e] = row_begin[e];  // fill cursors
+  __syncthreads();
   int* sorted = table + 4;
   for (int64_t a = tid; a < assignments; a += kRouteThreads) {
     const int64_t e = local_expert(routing, a);
@@ -311,9 +324,10 @@ __device__ __forceinline__ void h128_rows(float (&v)[8], int l) {
 // Writes inputs k0 .. k0 + 7 (k0 % 8 == 0) of t, scaled by the row's
 // power-of-two exponent, into the row's B-operand arrays: in b_order, inputs
 // 2i and 2i + 1 of the eight are adjacent halves (one dword store each) at
-// (k0 & ~31) + 8 i + 4 ((k0 >> 4) & 1) + 2 ((k0 >> 3) & 1).
+// (k0 & ~31) + 8 i + 4 ((k0 >> 4) & 1) + 2 ((k0 >> 3) & 1).  The low parts
+// only when `lo` (rows of tile experts use the high parts alone).
 __device__ __forceinline__ void store8(__amdgpu_buffer_rsrc_t dst, int kp, int k0, const float (&v)[8],
-                                       int e) {
+                                       int e, bool lo) {
   const int base = (k0 & ~31) + 4 * ((k0 >> 4) & 1) + 2 * ((k0 >> 3) & 1);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -325,7 +339,7 @@ __device__ __forceinline__ void store8(__amdgpu_buffer_rsrc_t dst, int kp, int k
     const uint32_t lw = uint32_t(__builtin_bit_cast(uint16_t, l0)) | (uint32_t(__builtin_bit_cast(uint16_t, l1)) << 16);
     const int o = 2 * (base + 8 * i);  // bytes
     __builtin_amdgcn_raw_buffer_store_b32(hw, dst, o, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b32(lw, dst, o, 2 * kp, 0);
+    if (lo) __builtin_amdgcn_raw_buffer_store_b32(lw, dst, o, 2 * kp, 0);
   }
 }
 
@@ -358,6 +372,10 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   const int64_t a = table[4 + blockIdx.x];
   const int64_t e = local_expert(routing, a);
   const int64_t* ptrs = routing.ptrs + e * 9;
+  // the tile experts' rows (sorted rows from the first tile task's first
+  // on) feed only the tile GEMM, which reads the high parts
+  const bool lo = table[2] == 0 ||
+                  int(blockIdx.x) < reinterpret_cast<const int4*>(table + lay.tasks())[table[3]].y;
   int* exps = reinterpret_cast<int*>(ws + lay.ints()) + lay.exps() + a * (lay.kmax() / 128);
   const __amdgpu_buffer_rsrc_t dst =
       make_rsrc(ws + (kActivate ? lay.act() : lay.input()) + a * kp, uint32_t(kp) * 4u);
@@ -464,12 +482,12 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   if (threadIdx.x == 0) exps[0] = ex;
 #pragma unroll
   for (int i = 0; i < kCache; ++i) {
-    if (wave + 4 * i < groups && live(wave + 4 * i)) store8(dst, int(kp), first_k(wave + 4 * i), c[i], ex);
+    if (wave + 4 * i < groups && live(wave + 4 * i)) store8(dst, int(kp), first_k(wave + 4 * i), c[i], ex, lo);
   }
   for (int64_t G = wave + 4 * kCache; G < groups; G += 4) {
     float v[8];
     form(G, v);
-    if (live(G)) store8(dst, int(kp), first_k(G), v, ex);
+    if (live(G)) store8(dst, int(kp), first_k(G), v, ex, lo);
   }
 }
 
