@@ -632,34 +632,40 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
   // the wavefront's two tiles of tile row 0
   const uint8_t* chunk = trellis + 2 * (4 * int64_t(blockIdx.x) + wave) * tile_bytes;
 
-  // B-operand staging of a block: chunk c = tid + 256 i (i < kChunks) is 16
-  // bytes (step, g, column) = (c / (4 kCols), c / kCols % 4, c % kCols);
-  // columns of rows past the task read its last row again (their MFMA
-  // columns are never used)
+  // B-operand staging of a block for the first kNs 8-row sub-blocks (kc =
+  // 16 kNs columns: rows 0 .. 8 kNs - 1, high and low parts): chunk c = tid +
+  // 256 i (i < kc / 16) is 16 bytes (step, g, column) = (c / (4 kc), c / kc
+  // % 4, c % kc), kept at that column of the kCols-wide LDS layout; columns
+  // of rows past the task read its last row again (their MFMA columns are
+  // never used).  Tasks of fewer rows stage (and read) fewer columns.
   //    The B operands are read through a buffer over the input region
   //    (32-bit byte offsets: the region is A x kp floats, checked on the host).
   const __amdgpu_buffer_rsrc_t st_buf = __builtin_amdgcn_make_buffer_rsrc(
       ws + in_offset, 0, int(lay.assignments * kp * 4), 0x00020000);
-  uint32_t st_off[kChunks];
+  auto stage_offsets = [&](auto ns_tag, uint32_t (&off)[kChunks]) {
+    constexpr int kc = 16 * decltype(ns_tag)::value;
 #pragma unroll
-  for (int i = 0; i < kChunks; ++i) {
-    const int c = tid + 256 * i;
-    const int col = c % kCols;
-    const int64_t a = sorted[first + min(col >> 1, nrows - 1)];
-    st_off[i] = uint32_t((a * 2 * kp + (col & 1) * kp + (c / (4 * kCols)) * 32 + (c / kCols % 4) * 8) * 2);
-  }
-  auto stage = [&](int kb, u32x4_t (&v)[kChunks]) {
+    for (int i = 0; i < kc / 16; ++i) {
+      const int c = tid + 256 * i;
+      const int col = c % kc;
+      const int64_t a = sorted[first + min(col >> 1, nrows - 1)];
+      off[i] = uint32_t((a * 2 * kp + (col & 1) * kp + (c / (4 * kc)) * 32 + (c / kc % 4) * 8) * 2);
+    }
+  };
+  auto stage = [&](auto ns_tag, const uint32_t (&off)[kChunks], int kb, u32x4_t (&v)[kChunks]) {
+    constexpr int kc = 16 * decltype(ns_tag)::value;
 #pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      v[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(st_buf, int(st_off[i]),
+    for (int i = 0; i < kc / 16; ++i) {
+      v[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(st_buf, int(off[i]),
                                                                                int(kb * 256), 0));
     }
   };
-  auto put = [&](int buf, const u32x4_t (&v)[kChunks]) {
+  auto put = [&](auto ns_tag, int buf, const u32x4_t (&v)[kChunks]) {
+    constexpr int kc = 16 * decltype(ns_tag)::value;
 #pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
+    for (int i = 0; i < kc / 16; ++i) {
       const int c = tid + 256 * i;
-      *reinterpret_cast<u32x4_t*>(&bop[buf][c / (4 * kCols)][c / kCols % 4][c % kCols][0]) = v[i];
+      *reinterpret_cast<u32x4_t*>(&bop[buf][c / (4 * kc)][c / kc % 4][c % kc][0]) = v[i];
     }
   };
   if (tid < kRows) {
@@ -705,13 +711,16 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
 #pragma unroll
   for (int sb = 0; sb < kSub; ++sb) acc1[sb] = acc2[sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto stream = [&](auto aligned_tag) {
+  auto stream = [&](auto aligned_tag, auto ns_tag) {
+    constexpr int kNs = decltype(ns_tag)::value;  // sub-blocks staged and read
+    uint32_t st_off[kChunks];
+    stage_offsets(ns_tag, st_off);
     // prologue: block 0's B operands, the first kDepth steps of trellis
     u32x4_t sv[kChunks];
-    stage(0, sv);
+    stage(ns_tag, st_off, 0, sv);
   #pragma unroll
     for (int i = 0; i < kDepth; ++i) load_step(aligned_tag, i, min(i, steps - 1));
-    put(0, sv);
+    put(ns_tag, 0, sv);
     __syncthreads();
 
     // one 128-input block (4 steps) per iteration, branch-free around the
@@ -726,7 +735,7 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
           const int buf = int(kb & 1);
           if (i == 0) {
             progress_priority(s, steps);
-            stage(min(kb + 1, kblocks - 1), sv);
+            stage(ns_tag, st_off, min(kb + 1, kblocks - 1), sv);
           }
           uint32_t q0[4], q1[4];
           if constexpr (kFixed) {
@@ -746,35 +755,50 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
           }
           const u32x4_t a1 = {q0[0], q0[1], q1[0], q1[1]};
           const u32x4_t a2 = {q0[2], q0[3], q1[2], q1[3]};
-          // every sub-block's B operand in one batch of LDS reads (the staged
-          // columns past the task hold its last row: valid data), then the
-          // MFMAs of the task's sub-blocks
+          // the staged sub-blocks' B operands in one batch of LDS reads (the
+          // staged columns past the task hold its last row: valid data),
+          // then the MFMAs of the task's sub-blocks
           half8_t b[kSub];
   #pragma unroll
-          for (int sb = 0; sb < kSub; ++sb) b[sb] = *reinterpret_cast<const half8_t*>(&bop[buf][s & 3][g][16 * sb + m][0]);
+          for (int sb = 0; sb < kNs; ++sb) b[sb] = *reinterpret_cast<const half8_t*>(&bop[buf][s & 3][g][16 * sb + m][0]);
   #pragma unroll
-          for (int sb = 0; sb < kSub; ++sb) {
+          for (int sb = 0; sb < kNs; ++sb) {
             if (sb < nsub) {
               acc1[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1), b[sb], acc1[sb], 0, 0, 0);
               acc2[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a2), b[sb], acc2[sb], 0, 0, 0);
             }
           }
           if (i == 3) {
-            put(buf ^ 1, sv);
+            put(ns_tag, buf ^ 1, sv);
             __syncthreads();
           }
         }
       }
     }
   };
+  // the loop for the fewest staged sub-blocks (1, 2 or kSub) that hold the
+  // task's rows
+  auto run = [&](auto aligned_tag) {
+    if constexpr (kSub >= 4) {
+      if (nsub <= 1) {
+        stream(aligned_tag, std::integral_constant<int, 1>{});
+      } else if (nsub <= 2) {
+        stream(aligned_tag, std::integral_constant<int, 2>{});
+      } else {
+        stream(aligned_tag, std::integral_constant<int, kSub>{});
+      }
+    } else {
+      stream(aligned_tag, std::integral_constant<int, kSub>{});
+    }
+  };
   if constexpr (kFixed) {
     if (aligned) {
-      stream(std::true_type{});
+      run(std::true_type{});
     } else {
-      stream(std::false_type{});
+      run(std::false_type{});
     }
   } else {
-    stream(std::true_type{});  // the run-time decode reads the tiles itself
+    run(std::true_type{});  // the run-time decode reads the tiles itself
   }
 
   // epilogue: high + low parts (adjacent lanes) unscaled per row, the rows'
