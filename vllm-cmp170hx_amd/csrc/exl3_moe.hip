@@ -4,12 +4,13 @@
 //
 // Launch sequence on the caller's stream (as the reference's run_moe_out):
 //  1. moe_route: one workgroup groups the local assignments by local expert
-//     (counts, scan, sorted list) and cuts each expert's rows into tasks of
-//     at most 32 rows (8 for the run-time-format decode: the per-expert
-//     token sort).
+//     (counts, scan, sorted list: the GEMV experts' rows, then the tile
+//     experts' rows) and cuts each expert's rows into tasks of at most 32
+//     rows (8 for the run-time-format decode: the per-expert token sort).
 //  2. per projection (gate, up): moe_form builds t = H128(x[a / topk] * suh)
 //     of every local assignment, as FP16 high/low parts in MFMA B-operand
-//     order with one power-of-two scale per assignment row; moe_gemv runs
+//     order with one power-of-two scale per assignment row (the high parts
+//     alone for the tile experts' rows); moe_gemv runs
 //     every task against its expert's matrix: one workgroup = (task, 128
 //     output columns) over the whole K range, trellis streamed with
 //     coalesced buffer loads, decoded in registers, each decoded operand fed
