@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <type_traits>
 
 namespace vq {
 
@@ -55,6 +56,40 @@ __device__ __forceinline__ void store_act(void* p, int dtype, int64_t i, float v
     static_cast<_Float16*>(p)[i] = _Float16(v);
   } else {
     static_cast<float*>(p)[i] = v;
+  }
+}
+
+// Elements i .. i + 7 of an activation-dtype array, of which the first
+// `valid` exist: 16-byte stores when all eight exist and the address allows
+// them, else one store per element (the same roundings either way).
+__device__ __forceinline__ void store8_act(void* p, int dtype, int64_t i, const float (&v)[8], int64_t valid) {
+  if (dtype == kFP32) {
+    float* q = static_cast<float*>(p) + i;
+    if (valid >= 8 && (reinterpret_cast<uintptr_t>(q) & 15) == 0) {
+      typedef float f4_t __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<f4_t*>(q) = f4_t{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f4_t*>(q + 4) = f4_t{v[4], v[5], v[6], v[7]};
+      return;
+    }
+  } else {
+    uint16_t* q = static_cast<uint16_t*>(p) + i;
+    if (valid >= 8 && (reinterpret_cast<uintptr_t>(q) & 15) == 0) {
+      typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint16_t h0 = dtype == kBF16 ? f32_to_bf16(v[2 * k]) : __builtin_bit_cast(uint16_t, _Float16(v[2 * k]));
+        const uint16_t h1 =
+            dtype == kBF16 ? f32_to_bf16(v[2 * k + 1]) : __builtin_bit_cast(uint16_t, _Float16(v[2 * k + 1]));
+        w[k] = uint32_t(h0) | (uint32_t(h1) << 16);
+      }
+      *reinterpret_cast<u4_t*>(q) = u4_t{w[0], w[1], w[2], w[3]};
+      return;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k < valid) store_act(p, dtype, i + k, v[k]);
   }
 }
 
@@ -137,6 +172,45 @@ __device__ __forceinline__ void h128_wave(float& v0, float& v1, int lane) {
   const float hi = v0 - v1;
   v0 = lo * kH128Scale;
   v1 = hi * kH128Scale;
+}
+
+// H128 of four 128-value blocks held as 16-lane rows: lane (q, l), q =
+// lane >> 4, l = lane & 15, holds elements 8 l .. 8 l + 7 of row q's block
+// in v[0..7].  The butterfly distances 1, 2, 4 pair elements of one lane, 8,
+// 16, 32, 64 the lanes l ^ 1, 2, 4, 8 of the row (DPP): every element gets
+// the same additions, in the same order of distances, as h128_wave (lower
+// lo + hi, upper lo - hi, FP32 round to nearest), then the scale.  Every
+// lane must be active.
+__device__ __forceinline__ void h128_rows(float (&v)[8], int l) {
+  // every sum rounded on its own: no product of the caller fused into the
+  // first additions
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int d = 1; d < 8; d <<= 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if ((j & d) == 0) {
+        const float lo = v[j], hi = v[j | d];
+        v[j] = lo + hi;
+        v[j | d] = lo - hi;
+      }
+    }
+  }
+  auto cross = [&](auto dist) {
+    constexpr int d = decltype(dist)::value;
+    const bool upper = (l & d) != 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float o = xor_lanes<d>(v[j], l);
+      v[j] = o + (upper ? -v[j] : v[j]);
+    }
+  };
+  cross(std::integral_constant<int, 1>{});
+  cross(std::integral_constant<int, 2>{});
+  cross(std::integral_constant<int, 4>{});
+  cross(std::integral_constant<int, 8>{});
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] *= kH128Scale;
 }
 
 // s_waitcnt with only vmcnt <= n (the other counters unconstrained), and a

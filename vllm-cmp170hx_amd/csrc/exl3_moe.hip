@@ -284,44 +284,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
 }
 
-// H128 of the blocks a wavefront holds as 16-lane rows: lane (q, l) of row
-// q holds elements 8 l .. 8 l + 7 of its block in v[0..7].  The butterfly
-// distances 1, 2, 4 pair elements of one lane, 8, 16, 32, 64 the lanes l ^ 1,
-// 2, 4, 8 of the row (DPP): every element gets the same additions, in the
-// same order of distances, as h128_wave (lower lo + hi, upper lo - hi, FP32
-// round to nearest), then the scale.
-__device__ __forceinline__ void h128_rows(float (&v)[8], int l) {
-  // every sum rounded on its own: no product of the caller fused into the
-  // first additions
-#pragma clang fp contract(off)
-#pragma unroll
-  for (int d = 1; d < 8; d <<= 1) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if ((j & d) == 0) {
-        const float lo = v[j], hi = v[j | d];
-        v[j] = lo + hi;
-        v[j | d] = lo - hi;
-      }
-    }
-  }
-  auto cross = [&](auto dist) {
-    constexpr int d = decltype(dist)::value;
-    const bool upper = (l & d) != 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float o = vq::xor_lanes<d>(v[j], l);
-      v[j] = o + (upper ? -v[j] : v[j]);
-    }
-  };
-  cross(std::integral_constant<int, 1>{});
-  cross(std::integral_constant<int, 2>{});
-  cross(std::integral_constant<int, 4>{});
-  cross(std::integral_constant<int, 8>{});
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] *= vq::kH128Scale;
-}
-
 // Writes inputs k0 .. k0 + 7 (k0 % 8 == 0) of t, scaled by the row's
 // power-of-two exponent, into the row's B-operand arrays: in b_order, inputs
 // 2i and 2i + 1 of the eight are adjacent halves (one dword store each) at
@@ -450,7 +412,7 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
         }
       }
     }
-    h128_rows(v, l);
+    vq::h128_rows(v, l);
   };
   auto live = [&](int64_t G) { return 4 * G + q < blocks; };
   if (threadIdx.x == 0) row_max = 0u;

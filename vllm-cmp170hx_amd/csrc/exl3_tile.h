@@ -437,14 +437,20 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   // the epilogue reuses
   vq::wait_vmcnt<0>();
   __syncthreads();
-  // Every task of a wavefront is in its 128-column block wave & 1: its two
-  // svh values are loaded once, here.  (Loads and stores share one in-order
-  // counter, so a load waited for after an output store also waits for the
-  // store's completion: a load per task would serialize the stores.)
+  // Wavefront w finishes 128-column block blk = w & 1 of the tile: in each
+  // row block, rows 8 (w >> 1) + 4 b + q (b = 0, 1), one per 16-lane row q
+  // = lane >> 4, lane l = lane & 15 holding the block's columns 8 l .. 8 l +
+  // 7, so the output H128 runs in registers and DPP (h128_rows) and each
+  // lane stores its eight outputs together.  The lane's eight svh values are
+  // loaded once, here (loads and stores share one in-order counter: a load
+  // waited for after an output store also waits for the store).
   const int blk = wave & 1;
-  const int64_t c0 = col0 + 128 * blk + lane;
-  const float svh0 = c0 < a.np ? vq::f16_to_f32(svh[c0]) : 0.0f;
-  const float svh1 = c0 + 64 < a.np ? vq::f16_to_f32(svh[c0 + 64]) : 0.0f;
+  const int q = lane >> 4;
+  const int l = lane & 15;
+  const int64_t c0 = col0 + 128 * blk + 8 * l;  // the lane's first column
+  float sv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sv[j] = c0 + j < a.np ? vq::f16_to_f32(svh[c0 + j]) : 0.0f;
   float* red = reinterpret_cast<float*>(&a_lds[0][0][0]);  // [16][kTileRedStride]
   static_assert(sizeof(a_lds) >= 16 * kTileRedStride * sizeof(float), "epilogue rows fit");
 #pragma unroll
@@ -463,31 +469,29 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
         }
     }
     __syncthreads();
-    // (row, 128-column block) tasks: H128 over the block, times svh
-    static_assert(kTileWaves % 2 == 0, "task & 1 == wave & 1");
 #pragma unroll
-    for (int t = 0; t < 32 / kTileWaves; ++t) {
-      const int task = wave + kTileWaves * t;
-      const int r = task >> 1;
+    for (int b = 0; b < 2; ++b) {
+      const int r = 8 * (wave >> 1) + 4 * b + q;
       const int tr = 16 * rb + r;
-      float v0 = red[r * kTileRedStride + 128 * blk + lane];
-      float v1 = red[r * kTileRedStride + 128 * blk + lane + 64];
-      vq::h128_wave(v0, v1, lane);
+      const float* src = red + r * kTileRedStride + 128 * blk + 8 * l;
+      const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(src);
+      const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(src + 4);
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float y0 = x0[j], y1 = x1[j];
+        v[j] = y0;
+        v[4 + j] = y1;
+      }
+      vq::h128_rows(v, l);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] *= sv[j];
       if (tr < nrows) {
         if constexpr (kMoe) {
-          if (c0 < a.np) {
-            float* dst = a.moe_out + int64_t(row_id[tr]) * a.np;
-            dst[c0] = v0 * svh0;
-            dst[c0 + 64] = v1 * svh1;
-          }
+          vq::store8_act(a.moe_out, vq::kFP32, int64_t(row_id[tr]) * a.np + c0, v, a.np - c0);
         } else {
           const int64_t row = int64_t(blockIdx.y) * kRows + tr;
-          if (c0 < a.logical_out) {
-            vq::store_act(a.out, a.out_dtype, row * a.logical_out + c0, v0 * svh0);
-          }
-          if (c0 + 64 < a.logical_out) {
-            vq::store_act(a.out, a.out_dtype, row * a.logical_out + c0 + 64, v1 * svh1);
-          }
+          vq::store8_act(a.out, a.out_dtype, row * a.logical_out + c0, v, a.logical_out - c0);
         }
       }
     }
