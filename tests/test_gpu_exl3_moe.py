@@ -407,6 +407,32 @@ def test_moe_tile_path_matches_oracle_and_gemv(ops, device, tile_rows, bits_x2, 
     assert torch.equal(tiled.view(torch.int16), again.view(torch.int16))
 
 
+@pytest.mark.parametrize("path", ["gemv", "tile"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_moe_ragged_logical_sizes_match_oracle(ops, device, tile_rows, path, dtype):
+    """Logical hidden / intermediate sizes that end inside an 8-input chunk
+    (300 and 250, padded to 384 and 256): the forming kernels read the last
+    chunk of x, suh and the gate / up results one element at a time, and the
+    padded inputs past the logical size form zero; on the GEMV path and on
+    the tile path (whose down projection also has a partial 256-column
+    tile), against the oracle."""
+    print(f"moe ragged sizes path={path} {dtype}", flush=True)
+    rng = np.random.default_rng(4242 if path == "gemv" else 4243)
+    hidden, intermediate, experts, topk, rows = 300, 250, 5, 3, 40
+    layer = Layer(rng, experts, hidden, intermediate, [(6, 2)], device, scales="sign")
+    ids = np.stack([rng.permutation(experts)[:topk] for _ in range(rows)])
+    weights = rng.random((rows, topk)).astype(np.float32)
+    expert_map = np.arange(experts, dtype=np.int64)
+    x_host, code, x = _acts(rng, rows, hidden, dtype, device)
+    args = (_dev(ids, device), _dev(weights, device), layer, _dev(expert_map, device), intermediate)
+    tile_rows(1 if path == "tile" else 1 << 30)
+    out = _run(ops, x, *args, bits_x2=6)
+    expected = O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map, intermediate,
+                         out_dtype=code)
+    bar = TILE_ABS_RMS if path == "tile" else GEMV_ABS_RMS
+    _assert_moe_close(_out_np(out), _oracle_f32(expected, code), f"ragged {path}", bar)
+
+
 def test_moe_tile_path_clamp_geometry_and_alignment(ops, device, tile_rows):
     """The tile path with the SwiGLU clamp, an expert of the wrong geometry
     (NaN rows, never read) and expert matrices at 2-byte offsets (routed to
