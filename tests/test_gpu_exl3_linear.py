@@ -312,6 +312,30 @@ def test_prefill_matches_oracle(ops, device, rows, bits_x2, codebook):
     check(got[sample], want, f"prefill rows={rows}")
 
 
+@pytest.mark.parametrize("rows", [40, 300])
+def test_prefill_16bit_outputs_are_the_rounded_fp32_outputs(ops, device, rows):
+    """The many-row path computes each output in FP32 and rounds it once to
+    the output dtype, storing eight columns together where the address
+    allows and one at a time otherwise (a width of n - 5 leaves rows at
+    every 16-byte phase and a partial last group): its BF16 / FP16 outputs
+    are the round-to-nearest-even of its FP32 outputs, bit for bit."""
+    print(f"prefill 16-bit outputs rows={rows}", flush=True)
+    rng = np.random.default_rng(6100 + rows)
+    k, n = 1024, 2048 + 128
+    trellis, suh, svh = random_matrix(rng, k, n, 8, scales="test")
+    logical_in, logical_out = k - 3, n - 5
+    x, code = random_acts(rng, rows, logical_in, "fp16")
+    f32 = _run_linear(ops, device, trellis, suh, svh, x, code, 8, 2, logical_out,
+                      torch.float32).cpu().numpy()
+    assert np.isfinite(f32).all()
+    f16 = _run_linear(ops, device, trellis, suh, svh, x, code, 8, 2, logical_out, torch.float16)
+    assert np.array_equal(f16.cpu().numpy().view(np.uint16), f32.astype(np.float16).view(np.uint16))
+    bf = _run_linear(ops, device, trellis, suh, svh, x, code, 8, 2, logical_out, torch.bfloat16)
+    u = f32.view(np.uint32).astype(np.uint64)
+    want = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)  # RNE, finite values
+    assert np.array_equal(bf.view(torch.int16).cpu().numpy().view(np.uint16), want)
+
+
 def test_prefill_benchmark_shape(ops, device):
     """8192 x 28672 at 4 bits, 512 fp16 rows: sampled rows against the oracle."""
     print("prefill 8192x28672 M=512", flush=True)
