@@ -150,15 +150,16 @@ __device__ __forceinline__ float wave_max(float v, int lane) {
 // order; the lower element becomes lo + hi and the upper one lo - hi (FP32
 // round to nearest), then both are scaled by 1/sqrt(128).  The same
 // operations in the same order as the reference (reference.cu:107-122,
-// codec.cuh:186-209), so the transform is bit-identical to it.  (The upper
-// lane's partner - v is computed as partner + (-v): the same rounding.)
+// codec.cuh:186-209), so the transform is bit-identical to it.  (A lane's
+// partner +- v is one FMA, partner + v * (+-1): the product is exact, so it
+// rounds as the sum does.)
 template <int d>
 __device__ __forceinline__ void h128_stage(float& v0, float& v1, int lane) {
   const float o0 = xor_lanes<d>(v0, lane);
   const float o1 = xor_lanes<d>(v1, lane);
-  const bool upper = (lane & d) != 0;
-  v0 = o0 + (upper ? -v0 : v0);
-  v1 = o1 + (upper ? -v1 : v1);
+  const float sgn = (lane & d) != 0 ? -1.0f : 1.0f;
+  v0 = __builtin_fmaf(v0, sgn, o0);
+  v1 = __builtin_fmaf(v1, sgn, o1);
 }
 
 __device__ __forceinline__ void h128_wave(float& v0, float& v1, int lane) {
@@ -196,13 +197,14 @@ __device__ __forceinline__ void h128_rows(float (&v)[8], int l) {
       }
     }
   }
+  // partner +- v as partner + v * (+-1) in one FMA (exact product)
   auto cross = [&](auto dist) {
     constexpr int d = decltype(dist)::value;
-    const bool upper = (l & d) != 0;
+    const float sgn = (l & d) != 0 ? -1.0f : 1.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float o = xor_lanes<d>(v[j], l);
-      v[j] = o + (upper ? -v[j] : v[j]);
+      v[j] = __builtin_fmaf(v[j], sgn, o);
     }
   };
   cross(std::integral_constant<int, 1>{});
