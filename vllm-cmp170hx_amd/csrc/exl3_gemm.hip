@@ -314,13 +314,14 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm(PrefillArgs a) {
       float v[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[j] = ldexpf(acc[i][j][r], -e);
+      // partner +- v as partner + v * (+-1): one FMA, exact product
       auto lane_stage = [&](auto d_tag) {
         constexpr int d = decltype(d_tag)::value;
-        const bool upper = (lane & d) != 0;
+        const float sgn = (lane & d) != 0 ? -1.0f : 1.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float o = vq::xor_lanes<d>(v[j], lane);
-          v[j] = o + (upper ? -v[j] : v[j]);
+          v[j] = __builtin_fmaf(v[j], sgn, o);
         }
       };
       lane_stage(std::integral_constant<int, 1>{});
