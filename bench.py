@@ -14,7 +14,7 @@ HIP graph of back-to-back calls, timed with HIP events on the stream they
 run on, after at least MIN_WARMUP_CALLS untimed calls (~0.2 s of the same
 work, whatever --warmup asks: a shorter run still measures the GPU coming
 up to its sustained clock, ~2.5% below the steady rate; the JSON line's
-"warmup" is the count actually run).
+"warmup" is the count actually run; --min-warmup 0 for counter runs).
 
 value = algorithmic bytes per step / time per step, in GB/s, where the bytes
 are the packed weights + suh/svh + activations + output
@@ -141,7 +141,7 @@ def gpu_gemv(args, torch):
         t, suh, svh = mats[i % COPIES]
         ops.linear_out(x, t, suh, svh, BITS_X2, CODEBOOK, K_IN, N_OUT, out, ws)
 
-    ms, steps, warm = time_graph(torch, call, GRAPH_CALLS, max(args.warmup, MIN_WARMUP_CALLS), args.steps)
+    ms, steps, warm = time_graph(torch, call, GRAPH_CALLS, max(args.warmup, args.min_warmup), args.steps)
     del mats
     return ms, steps, warm
 
@@ -468,6 +468,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=1200)
     parser.add_argument("--warmup", type=int, default=120)
+    parser.add_argument("--min-warmup", type=int, default=MIN_WARMUP_CALLS,
+                        help="least untimed GEMV calls before the timed ones (counter runs: 0)")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-extras", action="store_true",
