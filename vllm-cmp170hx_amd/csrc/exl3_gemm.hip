@@ -8,7 +8,9 @@
 //     writes t as FP16 high and low parts (t * 2^e = hi + lo, ~22 bits), in
 //     the k order of the MFMA operands: within every 32-input step, group g
 //     (8 halves) holds inputs {2g, 2g+1, 2g+8, 2g+9} of its two 16-input tile
-//     rows.  Row r: [high: padded_in halves][low: padded_in halves].
+//     rows.  Row r: [high: padded_in halves][low: padded_in halves]; the
+//     low parts are written only when prefill_gemm is the GEMM that reads
+//     them.
 //  2. the GEMM:
 //     * up to 4 bits per weight with a 16-byte aligned trellis: tile_gemm
 //       (exl3_tile.h), weights decoded in registers straight into MFMA B
@@ -57,9 +59,15 @@ constexpr int kLdsK = kBK + 8;      // LDS row stride in halves (80 bytes)
 
 // ---- 1. activations ----------------------------------------------------------
 
-// One workgroup (256 threads) per row.  Pass 1 finds the row maximum of
-// |t|, pass 2 recomputes t (the same operations, so the same values) and
-// writes the scaled high / low parts.
+// One workgroup (256 threads) per row.  A wavefront forms four 128-input
+// blocks at a time (group G: blocks 4 G .. 4 G + 3, one per 16-lane row,
+// eight consecutive inputs a lane, H128 in registers and DPP); wavefront w
+// takes groups w, w + 4, ..., the first kCache of them kept in registers.
+// Pass 1 finds the row maximum of |t|, pass 2 writes the scaled high parts
+// (and the low parts when `lo`: the GEMM reading them is not the tile
+// GEMM) as dword pairs; groups past the register cache are formed again
+// (the same operations, so the same values).  Inputs past logical_in form
+// +0, as the reference's zero padding.
 // Half offset of input k within its 32-input step, in the operand order.
 __device__ __forceinline__ int64_t operand_order(int64_t k) {
   const int w = int(k & 31);
@@ -68,35 +76,70 @@ __device__ __forceinline__ int64_t operand_order(int64_t k) {
   return (k & ~int64_t(31)) + g * 8 + slot;
 }
 
+template <int kCache>
 __global__ __launch_bounds__(256) void prefill_input(const void* __restrict__ x, int x_dtype,
                                                      int64_t logical_in, int64_t padded_in,
                                                      const uint16_t* __restrict__ suh,
                                                      _Float16* __restrict__ act,
-                                                     int* __restrict__ row_exp) {
+                                                     int* __restrict__ row_exp, bool lo) {
   __shared__ uint32_t row_max;
   const int64_t r = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int q = lane >> 4;  // the lane's block within a group
+  const int l = lane & 15;  // its eight inputs within the block: 8 l ..
   const int64_t blocks = padded_in / 128;
+  const int64_t groups = (blocks + 3) / 4;
   const uint16_t* xs = static_cast<const uint16_t*>(x) + r * logical_in;
   if (threadIdx.x == 0) row_max = 0u;
   __syncthreads();
-  auto form = [&](int64_t b, float& v0, float& v1) {
-    const int64_t k0 = b * 128 + lane;
-    const int64_t k1 = k0 + 64;
-    const uint32_t x0 = xs[k0 < logical_in ? k0 : 0];
-    const uint32_t x1 = xs[k1 < logical_in ? k1 : 0];
-    const uint32_t s0 = suh[k0];
-    const uint32_t s1 = suh[k1];
-    v0 = k0 < logical_in ? u16_act(uint16_t(x0), x_dtype) * vq::f16_to_f32(uint16_t(s0)) : 0.0f;
-    v1 = k1 < logical_in ? u16_act(uint16_t(x1), x_dtype) * vq::f16_to_f32(uint16_t(s1)) : 0.0f;
-    vq::h128_wave(v0, v1, lane);
+  // the first input of the lane's eight in group G (clamped to the last block)
+  auto first_k = [&](int64_t G) { return min(4 * G + q, blocks - 1) * 128 + 8 * l; };
+  // eight 16-bit values p[k0 .. k0 + 7]: one 16-byte load where all are
+  // inside len and the address allows it, else one load each (0 past len)
+  auto load8 = [&](const uint16_t* p, int64_t k0, int64_t len, uint16_t (&h)[8]) {
+    if (k0 + 8 <= len && (reinterpret_cast<uintptr_t>(p + k0) & 15) == 0) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(p + k0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t word = w[j >> 1];
+        h[j] = uint16_t(word >> (16 * (j & 1)));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = k0 + j < len ? p[k0 + j] : uint16_t(0);
+    }
   };
+  auto form = [&](int64_t G, float (&v)[8]) {
+    const int64_t k0 = first_k(G);
+    uint16_t xh[8], sh[8];
+    load8(xs, k0, logical_in, xh);
+    load8(suh, k0, padded_in, sh);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[j] = k0 + j < logical_in ? u16_act(xh[j], x_dtype) * vq::f16_to_f32(sh[j]) : 0.0f;
+    }
+    vq::h128_rows(v, l);
+  };
+  auto live = [&](int64_t G) { return 4 * G + q < blocks; };
   float mx = 0.0f;
-  for (int64_t b = wave; b < blocks; b += 4) {
-    float v0, v1;
-    form(b, v0, v1);
-    mx = fmaxf(mx, fmaxf(fabsf(v0), fabsf(v1)));
+  float c[kCache][8];
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) form(min(int64_t(wave + 4 * i), groups - 1), c[i]);
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    if (wave + 4 * i < groups && live(wave + 4 * i)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(c[i][j]));
+    }
+  }
+  for (int64_t G = wave + 4 * kCache; G < groups; G += 4) {
+    float v[8];
+    form(G, v);
+    if (live(G)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+    }
   }
   mx = vq::wave_max(mx, lane);
   if (lane == 0) atomicMax(&row_max, __builtin_bit_cast(uint32_t, mx));
@@ -104,19 +147,32 @@ __global__ __launch_bounds__(256) void prefill_input(const void* __restrict__ x,
   const int e = scale_exponent(row_max);
   if (threadIdx.x == 0) row_exp[r] = e;
   _Float16* h = act + r * 2 * padded_in;
-  _Float16* l = h + padded_in;
-  for (int64_t b = wave; b < blocks; b += 4) {
-    float v0, v1;
-    form(b, v0, v1);
-    const float t0 = ldexpf(v0, e);
-    const float t1 = ldexpf(v1, e);
-    const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
-    const int64_t k0 = operand_order(b * 128 + lane);
-    const int64_t k1 = operand_order(b * 128 + lane + 64);
-    h[k0] = h0;
-    h[k1] = h1;
-    l[k0] = _Float16(t0 - float(h0));
-    l[k1] = _Float16(t1 - float(h1));
+  // inputs k0 + 2 i, k0 + 2 i + 1 are adjacent halves of the operand order
+  // at (k0 & ~31) + 8 i + 4 ((k0 >> 4) & 1) + 2 ((k0 >> 3) & 1)
+  auto store8 = [&](int64_t k0, const float (&v)[8]) {
+    const int64_t base = (k0 & ~int64_t(31)) + 4 * ((k0 >> 4) & 1) + 2 * ((k0 >> 3) & 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float t0 = ldexpf(v[2 * i], e);
+      const float t1 = ldexpf(v[2 * i + 1], e);
+      const _Float16 h0 = _Float16(t0), h1 = _Float16(t1);
+      const uint32_t hw = uint32_t(__builtin_bit_cast(uint16_t, h0)) | (uint32_t(__builtin_bit_cast(uint16_t, h1)) << 16);
+      *reinterpret_cast<uint32_t*>(h + base + 8 * i) = hw;
+      if (lo) {
+        const _Float16 l0 = _Float16(t0 - float(h0)), l1 = _Float16(t1 - float(h1));
+        const uint32_t lw = uint32_t(__builtin_bit_cast(uint16_t, l0)) | (uint32_t(__builtin_bit_cast(uint16_t, l1)) << 16);
+        *reinterpret_cast<uint32_t*>(h + padded_in + base + 8 * i) = lw;
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    if (wave + 4 * i < groups && live(wave + 4 * i)) store8(first_k(wave + 4 * i), c[i]);
+  }
+  for (int64_t G = wave + 4 * kCache; G < groups; G += 4) {
+    float v[8];
+    form(G, v);
+    if (live(G)) store8(first_k(G), v);
   }
 }
 
@@ -385,14 +441,26 @@ int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trel
   if (rows > 65535 * int64_t(kTileRows)) return vq::fail("EXL3 linear has too many rows");
   _Float16* act = reinterpret_cast<_Float16*>(workspace);
   int* row_exp = reinterpret_cast<int*>(workspace + rows * kp);
-  hipLaunchKernelGGL(prefill_input, dim3(unsigned(rows)), dim3(256), 0, stream, x, x_dtype,
-                     logical_in, kp, suh, act, row_exp);
-  if (int rc = vq::check_launch("exl3 prefill_input")) return rc;
   // the tile GEMM: up to 4 bits per weight, a 16-byte aligned trellis
-  // (LDS-DMA), 32-bit buffer offsets over the matrix and the activations
+  // (LDS-DMA), 32-bit buffer offsets over the matrix and the activations;
+  // it reads the activations' high parts alone
   const uintptr_t base = reinterpret_cast<uintptr_t>(trellis);
-  if (tile_rate(bits_x2) && (base & 15) == 0 && tiles_k * tiles_n * 16 * bits_x2 <= INT_MAX &&
-      rows * 4 * kp <= INT_MAX) {
+  const bool tile = tile_rate(bits_x2) && (base & 15) == 0 && tiles_k * tiles_n * 16 * bits_x2 <= INT_MAX &&
+                    rows * 4 * kp <= INT_MAX;
+  {
+    // the register cache sized to the 4-block groups a wavefront forms
+    const int64_t per_wave = ((kp / 128 + 3) / 4 + 3) / 4;
+    const dim3 grid{unsigned(rows)};
+    if (per_wave <= 1) {
+      hipLaunchKernelGGL(prefill_input<1>, grid, dim3(256), 0, stream, x, x_dtype, logical_in, kp, suh, act, row_exp, !tile);
+    } else if (per_wave <= 2) {
+      hipLaunchKernelGGL(prefill_input<2>, grid, dim3(256), 0, stream, x, x_dtype, logical_in, kp, suh, act, row_exp, !tile);
+    } else {
+      hipLaunchKernelGGL(prefill_input<4>, grid, dim3(256), 0, stream, x, x_dtype, logical_in, kp, suh, act, row_exp, !tile);
+    }
+  }
+  if (int rc = vq::check_launch("exl3 prefill_input")) return rc;
+  if (tile) {
     TileArgs t{};
     t.act = reinterpret_cast<const uint8_t*>(act);
     t.act_row_bytes = 4 * kp;
