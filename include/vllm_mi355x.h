@@ -326,6 +326,27 @@ int marlin_moe_act(const float* part, const int32_t* ids, int64_t ksplit, int64_
                    int64_t nh, float limit, void* h, int act_dtype, void* stream);
 
 /*
+ * marlin_moe_gemm in mode PARTIAL (same arguments, checks and sums; N % 128
+ * == 0, partials below 2 GiB) followed by marlin_moe_act on its partials
+ * (ids, limit; h rows of N / 2 elements, h_rows >= n_slots), bitwise equal
+ * to the two calls, in one launch: the last of the 2 * ksplit wavefronts
+ * that produce a (block, 64 gate columns) pair of tiles to finish forms
+ * that pair's h from every split's partials, counted by the library's
+ * arrival counters (one per block and 64 gate columns; when none are free
+ * it makes the two calls).  The partials are still written.  Calls that
+ * overlap on one stream's counters race, as on the split-K GEMV's.
+ * The reference's decode_gemm_orig + decode_act_orig pair
+ * (csrc/ampere_marlin/decode_orig.cu:272-305, :361-401) in one call.
+ */
+int marlin_moe_w13_act(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
+                       const int32_t* w, const void* scales, int64_t experts, const int32_t* sorted,
+                       int64_t sorted_numel, const int32_t* expert_ids, int64_t expert_ids_numel,
+                       const int32_t* ntpp, const int32_t* ids, int64_t top_k, int64_t n_slots,
+                       int64_t K, int64_t N, int64_t block_size, int64_t ksplit, float limit,
+                       float* part, int64_t part_numel, void* h, int64_t h_stride, int64_t h_rows,
+                       void* stream);
+
+/*
  * The dequantized weights of one packed matrix, out[k][n] (K x N, the
  * activation dtype), through the GEMM's own fragment and dequant path.
  * The inspection form of the decode marlin_moe_gemm fuses; the reference's

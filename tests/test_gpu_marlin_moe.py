@@ -356,6 +356,71 @@ def test_direct_and_staged_paths_bitwise_at_c4_shape(mm, device, dtype, bs):
     assert torch.equal(p1, p2)
 
 
+@pytest.mark.parametrize("dtype", [M.BF16, M.FP16])
+def test_w13_act_bitwise_equals_partial_then_act(mm, device, dtype):
+    """marlin_moe_w13_act (the w13 K-split GEMM whose SwiGLU is finished by
+    the last wavefront of each (block, 64 gate columns) to arrive) equals
+    marlin_moe_gemm(PARTIAL) then marlin_moe_act bit for bit: identity
+    routing at one token (one slot routed to no local expert) and aligned
+    blocks, K splits 1..8, one- and four-tile workgroups, calls of
+    different sizes back to back (every call returns its arrival counters to
+    zero), and four replays of a captured graph with eager work between."""
+    from vllm_mi355x.kernels.marlin_moe import _C
+    rng = np.random.default_rng(31 + dtype)
+    E, K, N, topk = 128, 2048, 768, 8
+    layer = Layer(rng, E, K, N, dtype, device)
+
+    def case(T, bs, ks, limit):
+        ids, _ = routing(rng, T, E, topk)
+        if bs is None:
+            ids[0, 3] = -1
+        x = dev_act(from_f32(rng.standard_normal((T, K)), dtype), dtype, device)
+        slots = T * topk
+        ids_d = dev(ids, device).view(-1)
+        if bs is None:
+            routed = (None, ids_d, None, 16)
+        else:
+            routed = (*mm[1].align(dev(ids, device), E, bs), bs)
+        sorted_ids, eids, ntpp, bsz = routed
+        part1 = torch.zeros(ks * slots * 2 * N, dtype=torch.float32, device=device)
+        part2 = torch.zeros_like(part1)
+        h1 = torch.zeros(slots, N, dtype=TORCH_DTYPE[dtype], device=device)
+        h2 = torch.zeros_like(h1)
+        _C.gemm(x, layer.w1, layer.s1, sorted_ids, eids, ntpp, None, topk, slots, K, 2 * N, bsz,
+                _C.MODE_PARTIAL, ks, part=part1)
+        _C.act(part1, ids_d, ks, slots, N, limit, h1)
+
+        def fused():
+            _C.w13_act(x, layer.w1, layer.s1, sorted_ids, eids, ntpp, ids_d, topk, slots, K, 2 * N,
+                       bsz, ks, limit, part2, h2)
+        return h1, h2, fused
+
+    cases = ((1, None, 4, math.inf), (1, None, 8, 7.0), (5, 16, 2, math.inf), (40, 8, 1, 0.5),
+             (40, 32, 4, 7.0), (256, 16, 1, math.inf), (3, 8, 16, 7.0))
+    for T, bs, ks, limit in cases:
+        print(f"w13_act dtype={dtype} T={T} bs={bs} ks={ks} limit={limit}", flush=True)
+        h1, h2, fused = case(T, bs, ks, limit)
+        fused()
+        torch.cuda.synchronize()
+        assert torch.equal(h1.view(torch.int16), h2.view(torch.int16)), (T, bs, ks)
+    print(f"w13_act graph dtype={dtype}", flush=True)
+    h1, h2, fused = case(1, None, 4, 7.0)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fused()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fused()
+    for _ in range(4):
+        h2.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(h1.view(torch.int16), h2.view(torch.int16))
+
+
 # ---- the reference's operator sequence ----------------------------------------------------
 
 def test_decode_ops_sequence_matches_fused(mm, device):

@@ -149,17 +149,8 @@ struct GemvArgs {
   int splits;            // K splits (padded_in / 128)
 };
 
-// Arrival counters of the fused finish: a pool in static device memory
-// (exl3_linear.hip; zero when the code object loads, and every launch
-// returns the slots it used to zero), one slot per 128-column block of a
-// launch.  The host hands out ranges of kCounterSlots slots, one per
-// (device, stream, graph capture): launches that may overlap (on other
-// streams, or in graphs replayed on other streams) never share a slot.
-constexpr int kCounterRanges = 128;
-constexpr int kCounterSlots = 1024;
-// One counter per 128-byte line: atomics to one line serialize, so column
-// blocks must not share lines.
-constexpr int kCounterStride = 32;
+// Arrival counters of the fused finish: the pool of exl3_internal.h, one
+// slot per 128-column block of a launch.
 
 // Four consecutive partial sums at byte offset `offset` of buffer `r`,
 // written through to the device-coherent level (cache policy sc1, that of an
@@ -167,7 +158,6 @@ constexpr int kCounterStride = 32;
 // arrival counter says they are complete.  A builtin rather than inline
 // assembly: the compiler must see the 16-byte store to keep the VALU off its
 // data registers for the cycle after it issues.
-constexpr int kCachePolicySc1 = 16;
 __device__ __forceinline__ void store_agent_x4(__amdgpu_buffer_rsrc_t r, int offset, f32x4_t v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, offset, 0, kCachePolicySc1);
 }

@@ -25,6 +25,34 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
   X(14, 2) X(16, 2)
 #endif
 
+// Arrival counters of fused finishes (the split-K GEMV's, the Marlin w13
+// SwiGLU's): a pool in static device memory (exl3_linear.hip; zero when the
+// code object loads, and every launch returns the slots it used to zero).
+// The host hands out ranges of kCounterSlots slots, one per (device, stream,
+// graph capture): launches that may overlap (on other streams, or in graphs
+// replayed on other streams) never share a slot, and launches in one range
+// run one after another.
+constexpr int kCounterRanges = 128;
+constexpr int kCounterSlots = 1024;
+// One counter per 128-byte line: atomics to one line serialize, so the units
+// a launch counts must not share lines.
+constexpr int kCounterStride = 32;
+
+// Cache policy bits of a buffer access at the device-coherent level (sc1,
+// that of an agent-scope access): what one XCD writes so, another XCD reads
+// so after an arrival counter says it is complete.
+constexpr int kCachePolicySc1 = 16;
+
+// The pool's device address and the first slot of the range of `stream`'s
+// current capture (or of its eager launches), or a null pool when `slots`
+// exceeds kCounterSlots or no range is free (the caller then takes a path
+// without counters).
+struct CounterSlots {
+  uint32_t* pool;
+  int base;
+};
+CounterSlots counter_slots(hipStream_t stream, int64_t slots);
+
 inline bool known_format(int64_t bits_x2, int64_t codebook) {
 #define VQ_KNOWN(B, C) if (bits_x2 == B && codebook == C) return true;
   VQ_EXL3_FORMATS(VQ_KNOWN)

@@ -80,6 +80,8 @@ int check_padded(int64_t n) {
   return vq::kOk;
 }
 
+}  // namespace
+
 // Arrival counters of a fused-finish launch over `blocks` column blocks:
 // the pool's device address and the launch's first slot, or a null pool (the
 // launch then uses the separate output kernel).  One range of kCounterSlots
@@ -89,11 +91,6 @@ int check_padded(int64_t n) {
 // graphs (or a graph and eager work) never share one, so graphs replayed
 // concurrently on different streams cannot collide.  Ranges are kept for the
 // life of the process (a graph may be replayed at any time).
-struct CounterSlots {
-  uint32_t* pool;
-  int base;
-};
-
 CounterSlots counter_slots(hipStream_t stream, int64_t blocks) {
   static std::mutex mutex;
   static std::map<std::tuple<int, hipStream_t, bool, unsigned long long>, int> ranges;
@@ -134,6 +131,8 @@ CounterSlots counter_slots(hipStream_t stream, int64_t blocks) {
   ranges[key] = base;
   return {pool, base};
 }
+
+namespace {
 
 // 128-input blocks per workgroup chosen automatically, always a divisor of
 // padded_in / 128: the fewest (1, 2, 4 or 8) that keep the grid within ~7

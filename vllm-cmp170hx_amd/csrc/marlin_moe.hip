@@ -35,6 +35,7 @@
 
 #include "../../include/vllm_mi355x.h"
 #include "common.h"
+#include "exl3_internal.h"
 
 namespace marlin {
 namespace {
@@ -50,7 +51,9 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kThreads = 256;
 constexpr int kMaxBlock = 64;  // tokens per aligned block (upstream block sizes 8..64)
 
-enum Mode : int { kPartial = 0, kStore = 1, kTopk = 2, kSwiglu = 3 };
+// kPartialAct (marlin_moe_w13_act only): kPartial, then the SwiGLU of each
+// (block, 64 gate columns) by the last of its 2 ksplit wavefronts to arrive.
+enum Mode : int { kPartial = 0, kStore = 1, kTopk = 2, kSwiglu = 3, kPartialAct = 4 };
 
 struct GemmArgs {
   const uint16_t* a;      // activations, row r at a + r * a_stride
@@ -66,7 +69,8 @@ struct GemmArgs {
   uint16_t* out;          // kStore / kTopk: row slot at out + slot * out_stride
   int64_t out_stride;
   int top_k, n_slots, K, N, bs, experts, groups_per_split;
-  float limit;            // kSwiglu: SwiGLU clamp (+inf: none)
+  float limit;            // kSwiglu / kPartialAct: SwiGLU clamp (+inf: none)
+  uint32_t* counters;     // kPartialAct: this launch's arrival counters, one per (block, gate tile)
 };
 
 // Raw buffer resource over [base, base + bytes): 32-bit offsets, and loads
@@ -206,6 +210,19 @@ __device__ __forceinline__ uint16_t to_act(float v) {
     return __builtin_bit_cast(uint16_t, _Float16(v));
   }
 }
+
+// h = RN(RN(SiLU(min(G, L))) * clamp(U, -L, L)), G and U the activation-dtype
+// roundings of the gate and up sums (decode_orig.cu:272-305).
+template <bool kBF16>
+__device__ __forceinline__ uint16_t swiglu(float gs, float us, float limit) {
+  const float gv = fminf(round_act<kBF16>(gs), limit);
+  const float uv = fmaxf(fminf(round_act<kBF16>(us), limit), -limit);
+  const float sl = round_act<kBF16>(gv / (1.0f + expf(-gv)));
+  return to_act<kBF16>(sl * uv);
+}
+
+using exl3::kCachePolicySc1;
+using exl3::kCounterStride;
 
 // ---- grouped GEMM -----------------------------------------------------------------
 
@@ -416,6 +433,8 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
       const int slot = s_slot[16 * sb + col];
       wts[sb] = kMode == kTopk && slot >= 0 ? round_act<kBF16>(g.topk_w[slot]) : 0.0f;
     }
+    // kPartialAct: the partials of every K split (fewer than 2^31 bytes)
+    const __amdgpu_buffer_rsrc_t part_buf = buffer(g.part, uint32_t(gridDim.z) * uint32_t(g.n_slots) * uint32_t(g.N) * 4u);
     // C fragment: lane holds columns 16 j + 4 q .. +3 of token 16 sb + col
 #pragma unroll
     for (int sb = 0; sb < kNs; ++sb) {
@@ -427,6 +446,12 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
         const f32x4_t v = acc[j][sb];
         if constexpr (kMode == kPartial) {
           *reinterpret_cast<f32x4_t*>(g.part + (int64_t(ks) * g.n_slots + slot) * g.N + n) = v;
+        } else if constexpr (kMode == kPartialAct) {
+          // through to the device-coherent level: the finishing wavefront
+          // may run on another XCD
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), part_buf,
+                                                 int(4 * ((int64_t(ks) * g.n_slots + slot) * g.N + n)), 0,
+                                                 kCachePolicySc1);
         } else {
           float x[4] = {v[0], v[1], v[2], v[3]};
           if constexpr (kMode == kTopk) {
@@ -439,6 +464,52 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
           *reinterpret_cast<u32x2_t*>(g.out + int64_t(slot) * g.out_stride + n) = packed;
         }
       }
+    }
+    if constexpr (kMode == kPartialAct) {
+      // one arrival per wavefront once its stores have completed (vmcnt
+      // counts stores); tiles t and t + Nh / 64 (gate and up) of every K
+      // split share the counter of (block b, gate tile)
+      __builtin_amdgcn_s_waitcnt(0);
+      const int gate_tiles = g.N >> 7;
+      const int tg = tile < gate_tiles ? tile : tile - gate_tiles;
+      uint32_t* counter = g.counters + (int64_t(b) * gate_tiles + tg) * kCounterStride;
+      uint32_t arrived = 0;
+      if (lane == 0) arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      arrived = __builtin_amdgcn_readfirstlane(arrived);
+      if (arrived != 2u * gridDim.z - 1u) return;
+      // the last: marlin_act_kernel's sums and rounding for columns 64 tg +
+      // lane of the block's slots, the partials read at the coherent level
+      const int nh = g.N >> 1;
+      const int n = 64 * tg + lane;
+      const int plane = 4 * g.n_slots * g.N;
+      for (int i = 0; i < g.bs; ++i) {
+        const int slot = s_slot[i];
+        if (slot < 0) continue;
+        const int off = 4 * (slot * g.N + n);
+        const int splits = int(gridDim.z);
+        float gs = 0.0f, us = 0.0f;
+        // eight splits' loads in flight per round (indices past the last
+        // split clamped, their terms not added), summed in split order
+        for (int k0 = 0; k0 < splits; k0 += 8) {
+          float gp[8], up[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int k = min(k0 + u, splits - 1);
+            gp[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(part_buf, off, k * plane, kCachePolicySc1));
+            up[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(part_buf, off + 4 * nh, k * plane,
+                                                                                   kCachePolicySc1));
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            if (k0 + u < splits) {
+              gs += gp[u];
+              us += up[u];
+            }
+          }
+        }
+        g.out[int64_t(slot) * g.out_stride + n] = swiglu<kBF16>(gs, us, g.limit);
+      }
+      if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
   if constexpr (kSub == 1) {
@@ -951,10 +1022,7 @@ __global__ __launch_bounds__(kThreads) void marlin_act_kernel(const float* part,
     gs += p[k * plane];
     us += p[k * plane + nh];
   }
-  const float gv = fminf(round_act<kBF16>(gs), limit);
-  const float uv = fmaxf(fminf(round_act<kBF16>(us), limit), -limit);
-  const float sl = round_act<kBF16>(gv / (1.0f + expf(-gv)));
-  h[int64_t(slot) * nh + n] = to_act<kBF16>(sl * uv);
+  h[int64_t(slot) * nh + n] = swiglu<kBF16>(gs, us, limit);
 }
 
 // ---- top-k sum (kernels/moe/routing.py:579-600) -------------------------------------
@@ -1484,6 +1552,7 @@ int launch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t
   switch (mode) {
     case kPartial: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kPartial>), grid, dim3(kThreads), 0, s, g); break;
     case kStore: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kStore>), grid, dim3(kThreads), 0, s, g); break;
+    case kPartialAct: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kPartialAct>), grid, dim3(kThreads), 0, s, g); break;
     default: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kTopk>), grid, dim3(kThreads), 0, s, g); break;
   }
   return vq::check_launch("marlin_gemm");
@@ -1530,6 +1599,15 @@ int dispatch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, int wide,
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Four tiles per workgroup once that still gives ~2 workgroups per CU (the
+// routed blocks are at most min(blocks, n_slots / 2 + experts); the cheaper
+// estimate of blocks routed by the slot count is used).
+int wide_tiles(int64_t blocks, int64_t n_slots, int64_t block_size, int64_t experts, int64_t N,
+               int64_t ksplit) {
+  const int64_t routed_blocks = std::min<int64_t>(blocks, (n_slots + block_size - 1) / block_size + experts / 2);
+  return routed_blocks * (N / 256) * ksplit >= 512 ? 1 : 0;
+}
 
 }  // namespace
 }  // namespace marlin
@@ -1582,9 +1660,15 @@ int prepare_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
   if (ksplit <= 0 || groups % ksplit != 0 || ksplit > 65535) {
     return fail("ksplit must divide K / 128");
   }
-  if (mode == kPartial) {
+  if (mode == kPartial || mode == kPartialAct) {
     if (!part || part_numel < ksplit * n_slots * N) return fail("w13 partial buffer");
     if (!aligned16(part)) return fail("w13 partial buffer must be 16-byte aligned");
+    if (mode == kPartialAct) {
+      if (N % 128 != 0) return fail("w13 SwiGLU: the gate and up halves must be whole 64-column tiles");
+      if (ksplit * n_slots * N * 4 >= (int64_t(1) << 31)) return fail("w13 partials must stay below 2 GiB");
+      if (!out || out_stride < N / 2 || out_rows < n_slots) return fail("h output too small");
+      if (std::isnan(limit)) return fail("act: limit must not be NaN");
+    }
   } else if (mode == kStore || mode == kTopk) {
     if (ksplit != 1) return fail("a stored output takes one k-slice");
     if (!out || out_stride < N || out_stride % 4 != 0 || out_rows < n_slots) return fail("output too small");
@@ -1637,7 +1721,7 @@ extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int
                                int64_t block_size, int mode, int64_t ksplit, float* part,
                                int64_t part_numel, void* out, int64_t out_stride, int64_t out_rows,
                                void* stream) {
-  if (mode == marlin::kSwiglu) return vq::fail("unknown marlin_moe_gemm mode");
+  if (mode == marlin::kSwiglu || mode == marlin::kPartialAct) return vq::fail("unknown marlin_moe_gemm mode");
   marlin::GemmArgs g;
   int64_t blocks = 0;
   if (int rc = marlin::prepare_gemm(a, act_dtype, a_rows, a_stride, w, scales, experts, sorted, sorted_numel,
@@ -1648,13 +1732,45 @@ extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int
   }
   if (blocks == 0) return vq::kOk;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  // four tiles per workgroup once that still gives ~2 workgroups per CU
-  // (the routed blocks are at most min(blocks, n_slots / 2 + experts); use
-  // the cheaper estimate of blocks routed by the slot count)
-  const int64_t routed_blocks = std::min<int64_t>(blocks, (n_slots + block_size - 1) / block_size + experts / 2);
-  const int wide = routed_blocks * (N / 256) * ksplit >= 512 ? 1 : 0;
+  const int wide = marlin::wide_tiles(blocks, n_slots, block_size, experts, N, ksplit);
   return act_dtype == vq::kBF16 ? marlin::dispatch_gemm<true>(g, mode, int(blocks), int(ksplit), wide, s)
                                 : marlin::dispatch_gemm<false>(g, mode, int(blocks), int(ksplit), wide, s);
+}
+
+extern "C" int marlin_moe_w13_act(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
+                                  const int32_t* w, const void* scales, int64_t experts,
+                                  const int32_t* sorted, int64_t sorted_numel, const int32_t* expert_ids,
+                                  int64_t expert_ids_numel, const int32_t* ntpp, const int32_t* ids,
+                                  int64_t top_k, int64_t n_slots, int64_t K, int64_t N, int64_t block_size,
+                                  int64_t ksplit, float limit, float* part, int64_t part_numel, void* h,
+                                  int64_t h_stride, int64_t h_rows, void* stream) {
+  marlin::GemmArgs g;
+  int64_t blocks = 0;
+  if (!ids) return vq::fail("w13 SwiGLU: routed ids required");
+  if (h_stride != N / 2) return vq::fail("w13 SwiGLU: h rows of N / 2 elements");
+  if (int rc = marlin::prepare_gemm(a, act_dtype, a_rows, a_stride, w, scales, experts, sorted, sorted_numel,
+                                    expert_ids, expert_ids_numel, ntpp, nullptr, top_k, n_slots, K, N,
+                                    block_size, marlin::kPartialAct, ksplit, limit, part, part_numel, h,
+                                    h_stride, h_rows, g, blocks)) {
+    return rc;
+  }
+  if (blocks == 0) return vq::kOk;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int wide = marlin::wide_tiles(blocks, n_slots, block_size, experts, N, ksplit);
+  // one arrival counter per (block, 64 gate columns)
+  const exl3::CounterSlots slots = exl3::counter_slots(s, blocks * (N / 128));
+  if (slots.pool) {
+    g.counters = slots.pool + int64_t(slots.base) * marlin::kCounterStride;
+    return act_dtype == vq::kBF16
+        ? marlin::dispatch_gemm<true>(g, marlin::kPartialAct, int(blocks), int(ksplit), wide, s)
+        : marlin::dispatch_gemm<false>(g, marlin::kPartialAct, int(blocks), int(ksplit), wide, s);
+  }
+  // no counter slots free: the partials, then the separate SwiGLU launch
+  const int rc = act_dtype == vq::kBF16
+      ? marlin::dispatch_gemm<true>(g, marlin::kPartial, int(blocks), int(ksplit), wide, s)
+      : marlin::dispatch_gemm<false>(g, marlin::kPartial, int(blocks), int(ksplit), wide, s);
+  if (rc) return rc;
+  return marlin_moe_act(part, ids, ksplit, n_slots, N / 2, limit, h, act_dtype, stream);
 }
 
 extern "C" int marlin_moe_gemm_direct(const void* a_perm, int act_dtype, int64_t a_rows, int64_t a_stride,
@@ -1665,6 +1781,7 @@ extern "C" int marlin_moe_gemm_direct(const void* a_perm, int act_dtype, int64_t
                                       int64_t n_slots, int64_t K, int64_t N, int64_t block_size, int mode,
                                       int64_t ksplit, float limit, float* part, int64_t part_numel,
                                       void* out, int64_t out_stride, int64_t out_rows, void* stream) {
+  if (mode == marlin::kPartialAct) return vq::fail("unknown marlin_moe_gemm_direct mode");
   marlin::GemmArgs g;
   int64_t blocks = 0;
   if (int rc = marlin::prepare_gemm(a_perm, act_dtype, a_rows, a_stride, w, scales, experts, sorted,

@@ -98,6 +98,16 @@ SIGNATURES = {
     ]),
     "marlin_moe_act": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, ctypes.c_float, c_vp, c_int,
                                c_vp]),
+    "marlin_moe_w13_act": (c_int, [
+        c_vp, c_int, c_i64, c_i64, c_vp,      # a, act_dtype, a_rows, a_stride, w
+        c_vp, c_i64,                          # scales, experts
+        c_vp, c_i64, c_vp, c_i64, c_vp,       # sorted, numel, expert_ids, numel, ntpp
+        c_vp, c_i64, c_i64,                   # ids, top_k, n_slots
+        c_i64, c_i64, c_i64, c_i64,           # K, N, block_size, ksplit
+        ctypes.c_float,                       # limit
+        c_vp, c_i64, c_vp, c_i64, c_i64,      # part, part_numel, h, h_stride, h_rows
+        c_vp,                                 # stream
+    ]),
     "marlin_dequant": (c_int, [c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_vp]),
     "moe_sum": (c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp]),
     "moe_sum_add": (c_int, [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp]),

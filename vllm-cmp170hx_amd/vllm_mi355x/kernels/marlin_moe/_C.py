@@ -184,6 +184,45 @@ def align_permute(topk_ids, num_experts, block_size, sorted_ids, expert_ids, ntp
     _native.check(status)
 
 
+def w13_act(a, w, s, sorted_ids, expert_ids, ntpp, ids, top_k, n_slots, K, N, block_size, ksplit,
+            limit, part, h) -> None:
+    """marlin_moe_w13_act on torch tensors: gemm(..., MODE_PARTIAL, ksplit,
+    part=part) then act(part, ids, ksplit, n_slots, N // 2, limit, h), in one
+    launch while arrival counters are free."""
+    _require(a.dtype in _DTYPE_CODES and a.dim() == 2 and a.stride(1) == 1,
+             "a: bf16 or fp16, unit inner stride")
+    _require(s.dtype == a.dtype, "scales must have the activation dtype")
+    _require(w.dtype == torch.int32 and w.is_contiguous() and s.is_contiguous(),
+             "weights contiguous")
+    _require(w.dim() == 3 and w.size(1) * 16 == K and w.size(2) == 2 * N,
+             "w: int32 [E, K/16, 2N]")
+    _require(s.dim() == 3 and s.size(0) == w.size(0) and s.size(1) * 128 == K and s.size(2) == N,
+             "s: [E, K/128, N]")
+    identity = sorted_ids is None
+    _require(identity == (ntpp is None), "sorted ids and num_tokens_post_pad come together")
+    _require(expert_ids.dtype == torch.int32 and expert_ids.is_contiguous() and
+             ids.dtype == torch.int32 and ids.is_contiguous() and ids.numel() >= n_slots and
+             (identity or (sorted_ids.dtype == torch.int32 and ntpp.dtype == torch.int32)),
+             "routing dtypes")
+    for t, name in ((w, "w"), (s, "s"), (sorted_ids, "sorted"), (expert_ids, "eids"),
+                    (ntpp, "ntpp"), (ids, "ids"), (part, "part"), (h, "h")):
+        if t is not None:
+            _on(t, a.device, name)
+    _require(part.dtype == torch.float32 and part.is_contiguous(), "w13 partial buffer")
+    _require(h.dtype == a.dtype and h.dim() == 2 and h.is_contiguous() and h.size(1) == N // 2,
+             "h: activation dtype, contiguous rows of N / 2")
+    with torch.cuda.device(a.device):
+        status = _native.load().marlin_moe_w13_act(
+            a.data_ptr(), _DTYPE_CODES[a.dtype], a.size(0), a.stride(0), w.data_ptr(),
+            s.data_ptr(), w.size(0), 0 if identity else sorted_ids.data_ptr(),
+            0 if identity else sorted_ids.numel(),
+            expert_ids.data_ptr(), expert_ids.numel(), 0 if identity else ntpp.data_ptr(),
+            ids.data_ptr(), int(top_k), int(n_slots), int(K), int(N), int(block_size),
+            int(ksplit), float(limit), part.data_ptr(), part.numel(), h.data_ptr(), h.stride(0),
+            h.size(0), _stream(a.device))
+    _native.check(status)
+
+
 def act(part, ids, ksplit, n_slots, nh, limit, h) -> None:
     """marlin_moe_act on torch tensors."""
     _require(part.dtype == torch.float32 and part.is_contiguous(), "part: fp32")

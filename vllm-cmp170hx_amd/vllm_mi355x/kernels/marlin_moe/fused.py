@@ -183,9 +183,14 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
         kernel_moe_align_block_size(local, E, bs, buf["sorted"], buf["expert_ids"], buf["ntpp"],
                                     None, None)
         sorted_ids, expert_ids, ntpp = buf["sorted"], buf["expert_ids"], buf["ntpp"]
-    _C.gemm(hidden_states, w1, w1_scale, sorted_ids, expert_ids, ntpp, None,
-            topk, slots, K, 2 * N, bs, _C.MODE_PARTIAL, ks, part=buf["part"])
-    _C.act(buf["part"], local.view(-1), ks, slots, N, limit, buf["h"])
+    if N % 64 == 0:
+        # the w13 partials and their SwiGLU in one launch
+        _C.w13_act(hidden_states, w1, w1_scale, sorted_ids, expert_ids, ntpp, local.view(-1),
+                   topk, slots, K, 2 * N, bs, ks, limit, buf["part"], buf["h"])
+    else:
+        _C.gemm(hidden_states, w1, w1_scale, sorted_ids, expert_ids, ntpp, None,
+                topk, slots, K, 2 * N, bs, _C.MODE_PARTIAL, ks, part=buf["part"])
+        _C.act(buf["part"], local.view(-1), ks, slots, N, limit, buf["h"])
     _C.gemm(buf["h"], w2, w2_scale, sorted_ids, expert_ids, ntpp, tw, 1, slots,
             N, K, bs, _C.MODE_TOPK, 1, out=buf["c3"])
     moe_sum(buf["c3"].view(M, topk, K), out, local, E)
