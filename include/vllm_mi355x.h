@@ -347,6 +347,27 @@ int marlin_moe_w13_act(const void* a, int act_dtype, int64_t a_rows, int64_t a_s
                        void* stream);
 
 /*
+ * marlin_moe_gemm in mode TOPK with identity routing (sorted and ntpp NULL,
+ * ksplit 1, a: one row per slot, so the GEMM's own top_k is 1; top_k here:
+ * slots per token, n_slots a multiple of it; out rows of exactly N
+ * elements, below 2 GiB) followed by moe_sum of its rows with expert_ids as the
+ * routed ids (sum_out[t][n] = RN(FP32 sum over the slots of token t, in slot
+ * order, whose id is in [0, experts))), bitwise equal to the two calls, in
+ * one launch: the last wavefront of a token's routed slots to finish a
+ * 64-column tile sums that tile, counted by the library's arrival counters
+ * (one per token and 64 columns; when none are free, or top_k > 64, it
+ * makes the two calls).  The slot rows are still written.  Calls that overlap on one
+ * stream's counters race.  The reference's one-token decode_gemm_orig (w2)
+ * + moe_sum pair (csrc/ampere_marlin/decode_orig.cu:361-390,
+ * vllm_sm80/kernels/moe/routing.py:579-600) in one call.
+ */
+int marlin_moe_w2_sum(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride, const int32_t* w,
+                      const void* scales, int64_t experts, const int32_t* expert_ids,
+                      int64_t expert_ids_numel, const float* topk_w, int64_t top_k, int64_t n_slots,
+                      int64_t K, int64_t N, int64_t block_size, void* out, int64_t out_stride,
+                      int64_t out_rows, void* sum_out, void* stream);
+
+/*
  * The dequantized weights of one packed matrix, out[k][n] (K x N, the
  * activation dtype), through the GEMM's own fragment and dequant path.
  * The inspection form of the decode marlin_moe_gemm fuses; the reference's

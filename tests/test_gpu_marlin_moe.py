@@ -421,6 +421,63 @@ def test_w13_act_bitwise_equals_partial_then_act(mm, device, dtype):
         assert torch.equal(h1.view(torch.int16), h2.view(torch.int16))
 
 
+@pytest.mark.parametrize("dtype", [M.BF16, M.FP16])
+def test_w2_sum_bitwise_equals_topk_then_sum(mm, device, dtype):
+    """marlin_moe_w2_sum (identity routing: the w2 slot rows, and the sum of
+    a token's routed slots finished by the last of their wavefronts to
+    arrive) equals marlin_moe_gemm(TOPK) then moe_sum bit for bit: one token
+    of 8 slots (one routed to no local expert), three tokens of 4, one of 2,
+    sizes back to back (every call returns its arrival counters to zero),
+    and four replays of a captured graph with eager work between."""
+    from vllm_mi355x.kernels.marlin_moe import _C
+    rng = np.random.default_rng(47 + dtype)
+    E, K, N = 128, 768, 2048  # w2: intermediate 768 in, hidden 2048 out
+
+    w2 = dev(random_words(rng, E, K // 16, 2 * N), device)
+    s2 = dev_act(random_scales(rng, (E, K // 128, N), dtype), dtype, device)
+
+    def case(T, topk, drop):
+        ids, tw = routing(rng, T, E, topk)
+        if drop:
+            ids[0, 1] = -1
+        slots = T * topk
+        ids_d, tw_d = dev(ids, device).view(-1), dev(tw, device).view(-1)
+        h = dev_act(from_f32(rng.standard_normal((slots, K)), dtype), dtype, device)
+        c3a = torch.zeros(slots, N, dtype=TORCH_DTYPE[dtype], device=device)
+        c3b, outa = torch.zeros_like(c3a), torch.zeros(T, N, dtype=TORCH_DTYPE[dtype], device=device)
+        outb = torch.zeros_like(outa)
+        _C.gemm(h, w2, s2, None, ids_d, None, tw_d, 1, slots, K, N, 16, _C.MODE_TOPK, 1, out=c3a)
+        mm[1].moe_sum(c3a.view(T, topk, N), outa, ids_d.view(T, topk), E)
+
+        def fused():
+            _C.w2_sum(h, w2, s2, ids_d, tw_d, topk, slots, K, N, 16, c3b, outb)
+        return (c3a, outa), (c3b, outb), fused
+
+    for T, topk, drop in ((1, 8, True), (3, 4, False), (1, 2, False), (1, 8, False)):
+        print(f"w2_sum dtype={dtype} T={T} topk={topk} drop={drop}", flush=True)
+        a, b, fused = case(T, topk, drop)
+        fused()
+        torch.cuda.synchronize()
+        for x, y in zip(a, b):
+            assert torch.equal(x.view(torch.int16), y.view(torch.int16)), (T, topk)
+    print(f"w2_sum graph dtype={dtype}", flush=True)
+    a, b, fused = case(1, 8, True)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fused()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fused()
+    for _ in range(4):
+        b[1].zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(a[1].view(torch.int16), b[1].view(torch.int16))
+
+
 # ---- the reference's operator sequence ----------------------------------------------------
 
 def test_decode_ops_sequence_matches_fused(mm, device):

@@ -53,7 +53,10 @@ constexpr int kMaxBlock = 64;  // tokens per aligned block (upstream block sizes
 
 // kPartialAct (marlin_moe_w13_act only): kPartial, then the SwiGLU of each
 // (block, 64 gate columns) by the last of its 2 ksplit wavefronts to arrive.
-enum Mode : int { kPartial = 0, kStore = 1, kTopk = 2, kSwiglu = 3, kPartialAct = 4 };
+// kTopkSum (marlin_moe_w2_sum only, identity routing): kTopk, then the sum
+// over a token's routed slots of each 64 columns by the last of its slots'
+// wavefronts to arrive.
+enum Mode : int { kPartial = 0, kStore = 1, kTopk = 2, kSwiglu = 3, kPartialAct = 4, kTopkSum = 5 };
 
 struct GemmArgs {
   const uint16_t* a;      // activations, row r at a + r * a_stride
@@ -70,7 +73,10 @@ struct GemmArgs {
   int64_t out_stride;
   int top_k, n_slots, K, N, bs, experts, groups_per_split;
   float limit;            // kSwiglu / kPartialAct: SwiGLU clamp (+inf: none)
-  uint32_t* counters;     // kPartialAct: this launch's arrival counters, one per (block, gate tile)
+  uint32_t* counters;     // kPartialAct: this launch's arrival counters, one per (block, gate tile);
+                          // kTopkSum: one per (token, tile)
+  uint16_t* sum_out;      // kTopkSum: [n_slots / sum_topk][N] slot sums
+  int sum_topk;           // kTopkSum: slots per token (a holds one row per slot)
 };
 
 // Raw buffer resource over [base, base + bytes): 32-bit offsets, and loads
@@ -209,6 +215,11 @@ __device__ __forceinline__ uint16_t to_act(float v) {
   } else {
     return __builtin_bit_cast(uint16_t, _Float16(v));
   }
+}
+
+template <bool kBF16>
+__device__ __forceinline__ float act_f32(uint16_t v) {
+  return kBF16 ? vq::bf16_to_f32(v) : vq::f16_to_f32(v);
 }
 
 // h = RN(RN(SiLU(min(G, L))) * clamp(U, -L, L)), G and U the activation-dtype
@@ -431,10 +442,12 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
 #pragma unroll
     for (int sb = 0; sb < kNs; ++sb) {
       const int slot = s_slot[16 * sb + col];
-      wts[sb] = kMode == kTopk && slot >= 0 ? round_act<kBF16>(g.topk_w[slot]) : 0.0f;
+      wts[sb] = (kMode == kTopk || kMode == kTopkSum) && slot >= 0 ? round_act<kBF16>(g.topk_w[slot]) : 0.0f;
     }
-    // kPartialAct: the partials of every K split (fewer than 2^31 bytes)
+    // kPartialAct: the partials of every K split; kTopkSum: the slot rows
+    // (each fewer than 2^31 bytes)
     const __amdgpu_buffer_rsrc_t part_buf = buffer(g.part, uint32_t(gridDim.z) * uint32_t(g.n_slots) * uint32_t(g.N) * 4u);
+    const __amdgpu_buffer_rsrc_t out_buf = buffer(g.out, uint32_t(g.n_slots) * uint32_t(g.out_stride) * 2u);
     // C fragment: lane holds columns 16 j + 4 q .. +3 of token 16 sb + col
 #pragma unroll
     for (int sb = 0; sb < kNs; ++sb) {
@@ -454,16 +467,63 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
                                                  kCachePolicySc1);
         } else {
           float x[4] = {v[0], v[1], v[2], v[3]};
-          if constexpr (kMode == kTopk) {
+          if constexpr (kMode == kTopk || kMode == kTopkSum) {
             const float w = wts[sb];
 #pragma unroll
             for (int u = 0; u < 4; ++u) x[u] = round_act<kBF16>(x[u]) * w;  // exact product
           }
           const u32x2_t packed = {uint32_t(to_act<kBF16>(x[0])) | (uint32_t(to_act<kBF16>(x[1])) << 16),
                                   uint32_t(to_act<kBF16>(x[2])) | (uint32_t(to_act<kBF16>(x[3])) << 16)};
-          *reinterpret_cast<u32x2_t*>(g.out + int64_t(slot) * g.out_stride + n) = packed;
+          if constexpr (kMode == kTopkSum) {
+            // through to the device-coherent level, as kPartialAct's partials
+            __builtin_amdgcn_raw_buffer_store_b64(packed, out_buf, int(2 * (int64_t(slot) * g.out_stride + n)), 0,
+                                                  kCachePolicySc1);
+          } else {
+            *reinterpret_cast<u32x2_t*>(g.out + int64_t(slot) * g.out_stride + n) = packed;
+          }
         }
       }
+    }
+    if constexpr (kMode == kTopkSum) {
+      // identity routing: block b is slot b of token b / sum_topk.  One arrival
+      // per wavefront once its stores have completed; the last of the
+      // token's routed slots (ids in [0, experts)) forms moe_sum_kernel's
+      // FP32 slot-order sum of this tile's 64 columns
+      __builtin_amdgcn_s_waitcnt(0);
+      const int topk = g.sum_topk;
+      const int t = b / topk;
+      // the token's routed slots as bits (topk <= 64)
+      const int32_t* tok_ids = g.eids + int64_t(t) * topk;
+      uint64_t routed = 0;
+      for (int k = 0; k < topk; ++k) {
+        const int id = tok_ids[k];
+        if (id >= 0 && id < g.experts) routed |= uint64_t(1) << k;
+      }
+      const uint32_t expected = uint32_t(__builtin_popcountll(routed));
+      uint32_t* counter = g.counters + (int64_t(t) * (g.N >> 6) + tile) * kCounterStride;
+      uint32_t arrived = 0;
+      if (lane == 0) arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      arrived = __builtin_amdgcn_readfirstlane(arrived);
+      if (arrived != expected - 1u) return;
+      const int n = 64 * tile + lane;
+      float acc = 0.0f;
+      // eight slots' loads in flight per round, summed in slot order
+      for (int k0 = 0; k0 < topk; k0 += 8) {
+        bool use[8];
+        uint16_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          use[u] = k0 + u < topk && ((routed >> (k0 + u)) & 1) != 0;
+          const int row = t * topk + min(k0 + u, topk - 1);
+          v[u] = __builtin_amdgcn_raw_buffer_load_b16(out_buf, 2 * (row * int(g.out_stride) + n), 0, kCachePolicySc1);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (use[u]) acc += act_f32<kBF16>(v[u]);
+        }
+      }
+      g.sum_out[int64_t(t) * g.N + n] = to_act<kBF16>(acc);
+      if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if constexpr (kMode == kPartialAct) {
       // one arrival per wavefront once its stores have completed (vmcnt
@@ -1029,10 +1089,6 @@ __global__ __launch_bounds__(kThreads) void marlin_act_kernel(const float* part,
 
 // out[t][c] = RN(sum over slots k = 0..topk-1 in order of in[t][k][c]) in FP32;
 // with ids, a slot whose id is outside [0, experts) adds nothing.
-template <bool kBF16>
-__device__ __forceinline__ float act_f32(uint16_t v) {
-  return kBF16 ? vq::bf16_to_f32(v) : vq::f16_to_f32(v);
-}
 
 // kVec columns per thread (8 with 16-byte loads when hidden % 8 == 0, else 1).
 // With `shared` (the shared expert's output, element strides sh0 / sh1; sh1
@@ -1553,6 +1609,7 @@ int launch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t
     case kPartial: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kPartial>), grid, dim3(kThreads), 0, s, g); break;
     case kStore: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kStore>), grid, dim3(kThreads), 0, s, g); break;
     case kPartialAct: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kPartialAct>), grid, dim3(kThreads), 0, s, g); break;
+    case kTopkSum: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kTopkSum>), grid, dim3(kThreads), 0, s, g); break;
     default: hipLaunchKernelGGL((marlin_gemm<kBF16, kTilesWG, kSub, kTopk>), grid, dim3(kThreads), 0, s, g); break;
   }
   return vq::check_launch("marlin_gemm");
@@ -1669,11 +1726,15 @@ int prepare_gemm(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
       if (!out || out_stride < N / 2 || out_rows < n_slots) return fail("h output too small");
       if (std::isnan(limit)) return fail("act: limit must not be NaN");
     }
-  } else if (mode == kStore || mode == kTopk) {
+  } else if (mode == kStore || mode == kTopk || mode == kTopkSum) {
     if (ksplit != 1) return fail("a stored output takes one k-slice");
     if (!out || out_stride < N || out_stride % 4 != 0 || out_rows < n_slots) return fail("output too small");
     if ((reinterpret_cast<uintptr_t>(out) & 7) != 0) return fail("output must be 8-byte aligned");
-    if (mode == kTopk && !topk_w) return fail("topk weights required");
+    if (mode != kStore && !topk_w) return fail("topk weights required");
+    if (mode == kTopkSum) {
+      if (sorted) return fail("w2 sum: identity routing only");
+      if (n_slots * out_stride * 2 >= (int64_t(1) << 31)) return fail("w2 sum: slot rows must stay below 2 GiB");
+    }
   } else if (mode == kSwiglu) {
     if (ksplit != 1) return fail("a stored output takes one k-slice");
     if (N % 256 != 0) return fail("SwiGLU: the gate and up halves must be whole 128-column pairs");
@@ -1721,7 +1782,7 @@ extern "C" int marlin_moe_gemm(const void* a, int act_dtype, int64_t a_rows, int
                                int64_t block_size, int mode, int64_t ksplit, float* part,
                                int64_t part_numel, void* out, int64_t out_stride, int64_t out_rows,
                                void* stream) {
-  if (mode == marlin::kSwiglu || mode == marlin::kPartialAct) return vq::fail("unknown marlin_moe_gemm mode");
+  if (mode == marlin::kSwiglu || mode >= marlin::kPartialAct) return vq::fail("unknown marlin_moe_gemm mode");
   marlin::GemmArgs g;
   int64_t blocks = 0;
   if (int rc = marlin::prepare_gemm(a, act_dtype, a_rows, a_stride, w, scales, experts, sorted, sorted_numel,
@@ -1773,6 +1834,54 @@ extern "C" int marlin_moe_w13_act(const void* a, int act_dtype, int64_t a_rows, 
   return marlin_moe_act(part, ids, ksplit, n_slots, N / 2, limit, h, act_dtype, stream);
 }
 
+namespace marlin {
+namespace {
+int launch_moe_sum(const void* in, int act_dtype, int64_t tokens, int64_t topk, int64_t hidden,
+                   const int32_t* ids, int64_t experts, const void* shared, int64_t sh0, int64_t sh1,
+                   void* out, void* stream, const char* what);
+}  // namespace
+}  // namespace marlin
+
+extern "C" int marlin_moe_w2_sum(const void* a, int act_dtype, int64_t a_rows, int64_t a_stride,
+                                 const int32_t* w, const void* scales, int64_t experts,
+                                 const int32_t* expert_ids, int64_t expert_ids_numel, const float* topk_w,
+                                 int64_t top_k, int64_t n_slots, int64_t K, int64_t N, int64_t block_size,
+                                 void* out, int64_t out_stride, int64_t out_rows, void* sum_out,
+                                 void* stream) {
+  marlin::GemmArgs g;
+  int64_t blocks = 0;
+  if (!sum_out || (reinterpret_cast<uintptr_t>(sum_out) & 1) != 0) return vq::fail("w2 sum: 2-byte aligned sums");
+  if (out_stride != N) return vq::fail("w2 sum: slot rows of N elements");
+  if (top_k <= 0 || top_k > INT_MAX || n_slots % top_k != 0) return vq::fail("w2 sum: whole tokens of top_k slots");
+  // a holds one row per slot (the GEMM's own top_k is 1)
+  if (int rc = marlin::prepare_gemm(a, act_dtype, a_rows, a_stride, w, scales, experts, nullptr, 0, expert_ids,
+                                    expert_ids_numel, nullptr, topk_w, 1, n_slots, K, N, block_size,
+                                    marlin::kTopkSum, 1, INFINITY, nullptr, 0, out, out_stride, out_rows, g,
+                                    blocks)) {
+    return rc;
+  }
+  if (blocks == 0) return vq::kOk;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int wide = marlin::wide_tiles(blocks, n_slots, block_size, experts, N, 1);
+  const int64_t tokens = n_slots / top_k;
+  g.sum_out = static_cast<uint16_t*>(sum_out);
+  g.sum_topk = int(top_k);
+  // one arrival counter per (token, 64 columns)
+  const exl3::CounterSlots slots =
+      top_k <= 64 ? exl3::counter_slots(s, tokens * (N / 64)) : exl3::CounterSlots{nullptr, -1};
+  if (slots.pool) {
+    g.counters = slots.pool + int64_t(slots.base) * marlin::kCounterStride;
+    return act_dtype == vq::kBF16 ? marlin::dispatch_gemm<true>(g, marlin::kTopkSum, int(blocks), 1, wide, s)
+                                  : marlin::dispatch_gemm<false>(g, marlin::kTopkSum, int(blocks), 1, wide, s);
+  }
+  // no counter slots free: the slot rows, then the separate sum
+  const int rc = act_dtype == vq::kBF16 ? marlin::dispatch_gemm<true>(g, marlin::kTopk, int(blocks), 1, wide, s)
+                                        : marlin::dispatch_gemm<false>(g, marlin::kTopk, int(blocks), 1, wide, s);
+  if (rc) return rc;
+  return marlin::launch_moe_sum(out, act_dtype, tokens, top_k, N, expert_ids, experts, nullptr, 0, 0, sum_out,
+                                stream, "marlin_moe_w2_sum");
+}
+
 extern "C" int marlin_moe_gemm_direct(const void* a_perm, int act_dtype, int64_t a_rows, int64_t a_stride,
                                       const int32_t* w, const void* scales, int64_t experts,
                                       const int32_t* sorted, int64_t sorted_numel,
@@ -1781,7 +1890,7 @@ extern "C" int marlin_moe_gemm_direct(const void* a_perm, int act_dtype, int64_t
                                       int64_t n_slots, int64_t K, int64_t N, int64_t block_size, int mode,
                                       int64_t ksplit, float limit, float* part, int64_t part_numel,
                                       void* out, int64_t out_stride, int64_t out_rows, void* stream) {
-  if (mode == marlin::kPartialAct) return vq::fail("unknown marlin_moe_gemm_direct mode");
+  if (mode >= marlin::kPartialAct) return vq::fail("unknown marlin_moe_gemm_direct mode");
   marlin::GemmArgs g;
   int64_t blocks = 0;
   if (int rc = marlin::prepare_gemm(a_perm, act_dtype, a_rows, a_stride, w, scales, experts, sorted,

@@ -96,6 +96,12 @@ SIGNATURES = {
         c_vp, c_int, c_i64, c_i64, c_i64,     # a, act_dtype, rows, cols, a_stride
         c_vp, c_i64, c_vp,                    # out, out_stride, stream
     ]),
+    "marlin_moe_w2_sum": (c_int, [
+        c_vp, c_int, c_i64, c_i64, c_vp,      # a, act_dtype, a_rows, a_stride, w
+        c_vp, c_i64, c_vp, c_i64, c_vp,       # scales, experts, expert_ids, numel, topk_w
+        c_i64, c_i64, c_i64, c_i64, c_i64,    # top_k, n_slots, K, N, block_size
+        c_vp, c_i64, c_i64, c_vp, c_vp,       # out, out_stride, out_rows, sum_out, stream
+    ]),
     "marlin_moe_act": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, ctypes.c_float, c_vp, c_int,
                                c_vp]),
     "marlin_moe_w13_act": (c_int, [

@@ -223,6 +223,38 @@ def w13_act(a, w, s, sorted_ids, expert_ids, ntpp, ids, top_k, n_slots, K, N, bl
     _native.check(status)
 
 
+def w2_sum(a, w, s, expert_ids, topk_w, top_k, n_slots, K, N, block_size, c3, out) -> None:
+    """marlin_moe_w2_sum on torch tensors, identity routing (block b is slot b,
+    expert_ids[b] its local expert, a one row per slot): gemm(..., MODE_TOPK,
+    out=c3) then moe_sum(c3 as [n_slots / top_k, top_k, N], out, expert_ids),
+    in one launch while arrival counters are free."""
+    _require(a.dtype in _DTYPE_CODES and a.dim() == 2 and a.stride(1) == 1,
+             "a: bf16 or fp16, unit inner stride")
+    _require(s.dtype == a.dtype, "scales must have the activation dtype")
+    _require(w.dtype == torch.int32 and w.is_contiguous() and s.is_contiguous(),
+             "weights contiguous")
+    _require(w.dim() == 3 and w.size(1) * 16 == K and w.size(2) == 2 * N,
+             "w: int32 [E, K/16, 2N]")
+    _require(s.dim() == 3 and s.size(0) == w.size(0) and s.size(1) * 128 == K and s.size(2) == N,
+             "s: [E, K/128, N]")
+    _require(expert_ids.dtype == torch.int32 and expert_ids.is_contiguous(), "routing dtypes")
+    _require(topk_w.dtype == torch.float32 and topk_w.is_contiguous(), "topk weights fp32")
+    _require(c3.dtype == a.dtype and c3.is_contiguous() and c3.numel() >= n_slots * N,
+             "c3: contiguous slot rows of N")
+    _require(out.dtype == a.dtype and out.is_contiguous() and out.numel() >= n_slots // top_k * N,
+             "out: contiguous token rows of N")
+    for t, name in ((w, "w"), (s, "s"), (expert_ids, "eids"), (topk_w, "topk_w"), (c3, "c3"),
+                    (out, "out")):
+        _on(t, a.device, name)
+    with torch.cuda.device(a.device):
+        status = _native.load().marlin_moe_w2_sum(
+            a.data_ptr(), _DTYPE_CODES[a.dtype], a.size(0), a.stride(0), w.data_ptr(),
+            s.data_ptr(), w.size(0), expert_ids.data_ptr(), expert_ids.numel(),
+            topk_w.data_ptr(), int(top_k), int(n_slots), int(K), int(N), int(block_size),
+            c3.data_ptr(), int(N), c3.numel() // N, out.data_ptr(), _stream(a.device))
+    _native.check(status)
+
+
 def act(part, ids, ksplit, n_slots, nh, limit, h) -> None:
     """marlin_moe_act on torch tensors."""
     _require(part.dtype == torch.float32 and part.is_contiguous(), "part: fp32")

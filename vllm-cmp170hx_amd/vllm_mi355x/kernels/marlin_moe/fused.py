@@ -191,6 +191,10 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
         _C.gemm(hidden_states, w1, w1_scale, sorted_ids, expert_ids, ntpp, None,
                 topk, slots, K, 2 * N, bs, _C.MODE_PARTIAL, ks, part=buf["part"])
         _C.act(buf["part"], local.view(-1), ks, slots, N, limit, buf["h"])
+    if sorted_ids is None:
+        # identity routing: the w2 rows and their top-k sum in one launch
+        _C.w2_sum(buf["h"], w2, w2_scale, expert_ids, tw, topk, slots, N, K, bs, buf["c3"], out)
+        return out
     _C.gemm(buf["h"], w2, w2_scale, sorted_ids, expert_ids, ntpp, tw, 1, slots,
             N, K, bs, _C.MODE_TOPK, 1, out=buf["c3"])
     moe_sum(buf["c3"].view(M, topk, K), out, local, E)
