@@ -157,9 +157,12 @@ def test_moe_matches_oracle_with_expert_map_and_masked_routes(ops, device, rows,
     _assert_moe_close(_out_np(out), _oracle_f32(expected, code), f"moe rows={rows}", GEMV_ABS_RMS)
 
 
-@pytest.mark.parametrize("bits_x2", [2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("bits_x2", [2, 3, 4, 5, 6, 7, 8, 10, 16])
 @pytest.mark.parametrize("rows,dtype", [(1, "bf16"), (9, "fp16"), (40, "bf16")])
 def test_moe_v2_fixed_rate_matches_oracle_and_moe_out(ops, device, bits_x2, rows, dtype):
+    """moe_out_v2 at a layer rate (2..8: the fixed-rate kernels; 10 and 16,
+    as the reference's (2560, 640, 10) v2 layer: the run-time-rate kernel)
+    against the oracle and bitwise against moe_out."""
     print(f"moe_v2 bits_x2={bits_x2} rows={rows} {dtype}", flush=True)
     rng = np.random.default_rng(1000 * bits_x2 + rows)
     hidden, intermediate, experts, topk = 384, 256, 6, 4
