@@ -9,12 +9,12 @@ shape, a 4096 x 14336 matrix at 4 bits per weight (bits_x2 8, mul1
 codebook), M = 1 fp16 activation row ~N(0,1), fp16 output; seeded uniform
 trellis words, suh / svh = +-1 x N(1, 0.05).  Twelve distinct weight copies
 (353 MB, more than the 256 MB Infinity Cache) are used round-robin so every
-step streams its weights from HBM.  The K timed steps run as replays of a
-HIP graph of back-to-back calls, timed with HIP events on the stream they
-run on, after at least MIN_WARMUP_CALLS untimed calls (~0.2 s of the same
-work, whatever --warmup asks: a shorter run still measures the GPU coming
-up to its sustained clock, ~2.5% below the steady rate; the JSON line's
-"warmup" is the count actually run; --min-warmup 0 for counter runs).
+step streams its weights from HBM.  Exactly --warmup untimed steps run
+first, then exactly --steps timed steps as replays of HIP graphs of
+back-to-back calls (uploaded before the timed region), timed with HIP
+events on the stream they run on.  The other workloads of the line run
+before the headline, so the GPU is at its sustained clock when the timed
+steps start (from a cold start the first ~20 ms run ~2.5% slower).
 
 value = algorithmic bytes per step / time per step, in GB/s, where the bytes
 are the packed weights + suh/svh + activations + output
@@ -67,7 +67,6 @@ MFMA_FP16_PEAK_TFLOPS = 2500.0
 K_IN, N_OUT, BITS_X2, CODEBOOK, ROWS = 4096, 14336, 8, 2, 1
 COPIES = 12
 GRAPH_CALLS = 120
-MIN_WARMUP_CALLS = 12000
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "exl3_gemv_4096x14336_4bit_m1_traffic.md")
 
 
@@ -91,6 +90,57 @@ def make_matrix(torch, gen, device, k, n, bits_x2, scales="sign"):
         return (trellis, torch.randn(k, device=device, generator=gen).half(),
                 (0.05 * torch.randn(n, device=device, generator=gen)).half())
     return trellis, sign_scales(k), sign_scales(n)
+
+
+def _hip_graph_upload(torch, graph, stream) -> None:
+    """hipGraphUpload of a captured graph's executable: its first replay in
+    a timed region then pays no upload."""
+    import ctypes
+    lib = ctypes.CDLL("libamdhip64.so")
+    lib.hipGraphUpload.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.hipGraphUpload.restype = ctypes.c_int
+    rc = lib.hipGraphUpload(ctypes.c_void_p(graph.raw_cuda_graph_exec()), ctypes.c_void_p(stream.cuda_stream))
+    if rc != 0:
+        raise RuntimeError(f"hipGraphUpload failed ({rc})")
+
+
+def time_steps_exact(torch, calls, warmup, steps, per_graph=120):
+    """ms per call over exactly `steps` timed calls after exactly `warmup`
+    untimed ones: the warm-up calls run eagerly (they also make the
+    library's first launches), the timed calls as replays of a graph of
+    per_graph calls plus one graph of the remainder, uploaded first; HIP
+    events on the replay stream bracket the replays."""
+    for i in range(warmup):
+        calls(i)
+    torch.cuda.synchronize()
+    per_graph = max(1, min(per_graph, steps))
+    full, rem = divmod(steps, per_graph)
+    stream = torch.cuda.Stream()
+    graphs = []
+    for size, reps in ((per_graph, full), (rem, 1)):
+        if size == 0 or reps == 0:
+            continue
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(size):
+                    calls(i)
+        graphs.append((graph, reps))
+    torch.cuda.synchronize()
+    for graph, _ in graphs:
+        _hip_graph_upload(torch, graph, stream)
+    stream.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for graph, reps in graphs:
+            for _ in range(reps):
+                graph.replay()
+        end.record(stream)
+        end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
 
 
 def time_graph(torch, calls, per_graph, warmup, steps):
@@ -141,9 +191,9 @@ def gpu_gemv(args, torch):
         t, suh, svh = mats[i % COPIES]
         ops.linear_out(x, t, suh, svh, BITS_X2, CODEBOOK, K_IN, N_OUT, out, ws)
 
-    ms, steps, warm = time_graph(torch, call, GRAPH_CALLS, max(args.warmup, args.min_warmup), args.steps)
+    ms = time_steps_exact(torch, call, args.warmup, args.steps, GRAPH_CALLS)
     del mats
-    return ms, steps, warm
+    return ms, args.steps, args.warmup
 
 
 def gpu_gemv_configs(args, torch):
@@ -171,7 +221,7 @@ def gpu_gemv_configs(args, torch):
             t, suh, svh = mats[i % len(mats)]
             ops.linear_out(x, t, suh, svh, bits_x2, CODEBOOK, k, n, out, ws)
 
-        ms, _, _ = time_graph(torch, call, GRAPH_CALLS, args.warmup, max(240, args.steps // 2))
+        ms, _, _ = time_graph(torch, call, GRAPH_CALLS, 240, 480)
         gbs = nbytes / (ms * 1e-3) / 1e9
         results[name] = {"k": k, "n": n, "bits_per_weight": bits_x2 / 2, "rows": rows,
                          "us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
@@ -292,7 +342,26 @@ def cpu_marlin_moe(seconds: float, torch):
 
 # ---- EXL3 prefill and MoE ---------------------------------------------------------------
 
+class _Fp16Tiles:
+    """exl3_set_tile_precision(1) inside the block: the many-row tile GEMM on
+    the FP16 high parts of the activations alone (the opt-in below the
+    reference's precision); the default (high and low parts) after it."""
+
+    def __enter__(self):
+        from vllm_mi355x import _native
+        self.lib = _native.load()
+        _native.check(self.lib.exl3_set_tile_precision(1))
+
+    def __exit__(self, *exc):
+        from vllm_mi355x import _native
+        _native.check(self.lib.exl3_set_tile_precision(0))
+        return False
+
+
 def gpu_exl3_prefill(torch, rows=2048, k=8192, n=28672, other_rows=(512, 8192)):
+    """The many-row linear at the default precision (FP16 high and low
+    activation parts, ~22 bits, as the reference's tensor-core kernels), and
+    at the FP16-only opt-in under "fp16_only"."""
     from vllm_mi355x.kernels.exl3 import ops
 
     ops.ensure_extension()
@@ -314,8 +383,12 @@ def gpu_exl3_prefill(torch, rows=2048, k=8192, n=28672, other_rows=(512, 8192)):
         return {"ms": round(ms, 3), "tflops": round(tflops, 1),
                 "mfma_util": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4)}
 
-    result = {"workload": f"{k}x{n} 4-bit mul1, M={rows}, fp16", **measure(rows)}
+    result = {"workload": f"{k}x{n} 4-bit mul1, M={rows}, fp16", "precision": "fp16 hi+lo activations",
+              **measure(rows)}
     result["by_rows"] = {str(m): measure(m) for m in other_rows}
+    with _Fp16Tiles():
+        result["fp16_only"] = {"precision": "fp16 activations (high parts alone)", **measure(rows),
+                               "by_rows": {str(m): measure(m) for m in other_rows}}
     return result
 
 
@@ -381,10 +454,88 @@ def gpu_exl3_moe(torch, tokens=(64, 2048), experts=256, hidden=7168, inter=2048,
                 "mfma_util": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4)}
 
     by_tokens = {str(t_count): measure(t_count) for t_count in tokens}
+    with _Fp16Tiles():
+        fp16_only = {str(t_count): measure(t_count) for t_count in tokens if t_count > 256}
     del keep
     return {"workload": (f"{experts}+1 experts, {hidden}/{inter}, {bits_x2 / 2:g}-bit mul1, top-{topk} "
                          f"Zipf(1.1), {tokens[0]} tokens, fp16"),
-            **by_tokens[str(tokens[0])], "by_tokens": by_tokens}
+            "precision": "fp16 hi+lo activations",
+            **by_tokens[str(tokens[0])], "by_tokens": by_tokens,
+            "fp16_only": {"precision": "tile GEMM on fp16 activations (high parts alone)",
+                          "by_tokens": fp16_only}}
+
+
+def gpu_exl3_moe_prefill(torch, tokens=(2048, 65, 512, 3460), experts=256, hidden=2560, inter=640,
+                         topk=10, bits_x2=10):
+    """The one configuration the reference's moe_out_prefill serves
+    (csrc/exl3/moe_prefill.h:9-14): 256 local experts, hidden 2560,
+    intermediate 640, every matrix bits_x2 10 mul1, top-10 from softmax of
+    ~N(0, 1) logits, bf16 activations, 65 to 3460 rows, through
+    _exl3_C::moe_out_prefill; the same 2048-row call through moe_out (the
+    run-time-format GEMV in 8-row tasks, what moe_out_prefill ran before it
+    had a many-row kernel) for comparison.  The first count is the line's
+    headline."""
+    from vllm_mi355x.kernels.exl3 import ops
+
+    ops.ensure_extension()
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device)
+    gen.manual_seed(11)
+    keep, ptrs, meta = [], [], []
+    for _ in range(experts):
+        p, m = [], []
+        for kk, nn in ((hidden, inter), (hidden, inter), (inter, hidden)):
+            t, suh, svh = make_matrix(torch, gen, device, kk, nn, bits_x2, scales="test")
+            keep += [t, suh, svh]
+            p.append([t.data_ptr(), suh.data_ptr(), svh.data_ptr()])
+            m.append([kk, nn, bits_x2, 2])
+        ptrs.append(p)
+        meta.append(m)
+    ptrs = torch.tensor(ptrs, dtype=torch.int64, device=device)
+    meta = torch.tensor(meta, dtype=torch.int64, device=device)
+    emap = torch.arange(experts, dtype=torch.int32, device=device)
+    per_expert = 3 * hidden * inter * bits_x2 // 16 + 2 * 2 * (hidden + inter) + 2 * (hidden + inter)
+
+    def measure(t_count, op):
+        tw, ti = softmax_topk(torch, torch.randn(t_count, experts, generator=gen, device=device), topk)
+        x = torch.randn(t_count, hidden, generator=gen, device=device).bfloat16()
+        out = torch.empty_like(x)
+        ws = torch.empty(ops.moe_workspace_size(t_count, hidden, inter, topk, experts),
+                         dtype=torch.float32, device=device)
+        fn = getattr(torch.ops._exl3_C, op)
+
+        def call(i):
+            fn(x, ti, tw, ptrs, meta, emap, inter, out, ws)
+
+        reps = 4
+        ms, _, _ = time_graph(torch, call, reps, reps, 3 * reps)
+        if not torch.isfinite(out.float()).all():
+            raise RuntimeError(f"EXL3 MoE prefill bench: non-finite outputs at {t_count} tokens")
+        touched = int(torch.unique(ti).numel())
+        nbytes = touched * per_expert + 2 * 2 * t_count * hidden
+        flops = 2 * 3 * hidden * inter * t_count * topk
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        tflops = flops / (ms * 1e-3) / 1e12
+        return {"us_per_forward": round(ms * 1e3, 1), "tokens_per_s": round(t_count / (ms * 1e-3)),
+                "experts_touched": touched, "hbm_gbs": round(gbs, 1),
+                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "tflops": round(tflops, 1),
+                "mfma_util": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4)}
+
+    by_tokens = {str(t): measure(t, "moe_out_prefill") for t in tokens}
+    with _Fp16Tiles():
+        fp16_only = {str(tokens[0]): measure(tokens[0], "moe_out_prefill")}
+    runtime_gemv = measure(tokens[0], "moe_out")
+    del keep
+    head = by_tokens[str(tokens[0])]
+    return {"workload": (f"moe_out_prefill {experts} experts, {hidden}/{inter}, bits_x2 {bits_x2} mul1, "
+                         f"top-{topk}, {tokens[0]} tokens, bf16"),
+            "precision": "fp16 hi+lo activations", **head, "by_tokens": by_tokens,
+            "fp16_only": {"precision": "tile GEMM on fp16 activations (high parts alone)",
+                          "by_tokens": fp16_only},
+            "runtime_decode_gemv": {"op": "moe_out (run-time-format GEMV, 8-row tasks)",
+                                    **runtime_gemv,
+                                    "speedup_of_moe_out_prefill": round(
+                                        runtime_gemv["us_per_forward"] / head["us_per_forward"], 2)}}
 
 
 def cpu_model() -> str:
@@ -468,19 +619,20 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=1200)
     parser.add_argument("--warmup", type=int, default=120)
-    parser.add_argument("--min-warmup", type=int, default=MIN_WARMUP_CALLS,
-                        help="least untimed GEMV calls before the timed ones (counter runs: 0)")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-extras", action="store_true",
                         help="only the headline GEMV (profiling runs)")
-    parser.add_argument("--only", choices=("prefill", "exl3_moe", "marlin"), default=None,
+    parser.add_argument("--only", choices=("prefill", "exl3_moe", "marlin", "moe_prefill"), default=None,
                         help="profiling runs: only this workload, its JSON on one line (not the "
                              "benchmark line)")
     parser.add_argument("--copy-mb", type=int, default=0,
                         help="also run 10 plain device copies of this many MiB (the counter "
                              "calibration of FETCH_SIZE / WRITE_SIZE)")
     args = parser.parse_args()
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be positive and --warmup nonnegative", file=sys.stderr)
+        return 2
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(the hot path is a single-GPU kernel; multi-GPU sharding is not built here)",
@@ -501,11 +653,29 @@ def main() -> int:
             del src, dst
 
     if args.only:
-        run = {"prefill": gpu_exl3_prefill, "exl3_moe": gpu_exl3_moe, "marlin": gpu_marlin_moe}[args.only]
+        run = {"prefill": gpu_exl3_prefill, "exl3_moe": gpu_exl3_moe, "marlin": gpu_marlin_moe,
+               "moe_prefill": gpu_exl3_moe_prefill}[args.only]
         result = run(torch)
         calibration_copies()
         print(json.dumps({args.only: result}))
         return 0
+    extras = {}
+    if not args.no_extras:
+        # before the headline: the GPU is then at its sustained clock
+        moe = gpu_marlin_moe(torch)
+        at256 = moe["256"]
+        extras["int4_moe"] = {
+            "workload": "Marlin int4 fused MoE, 128 experts, hidden 2048, inter 768, top-8, fp16",
+            "tokens_per_s_at_256": at256["tokens_per_s"],
+            "mfma_util_at_256": at256["mfma_util"],
+            "hbm_frac_at_256": at256["hbm_frac"],
+            "bound_at_256": "hbm",
+            "by_tokens": moe,
+        }
+        extras["exl3_gemv_configs"] = gpu_gemv_configs(args, torch)
+        extras["exl3_prefill"] = gpu_exl3_prefill(torch)
+        extras["exl3_moe"] = gpu_exl3_moe(torch)
+        extras["exl3_moe_prefill"] = gpu_exl3_moe_prefill(torch)
     ms, steps, warm = gpu_gemv(args, torch)
     calibration_copies()
     nbytes = gemv_bytes(K_IN, N_OUT, BITS_X2, ROWS)
@@ -538,20 +708,7 @@ def main() -> int:
             "traffic": measured_traffic(),
         },
     }
-    if not args.no_extras:
-        moe = gpu_marlin_moe(torch)
-        at256 = moe["256"]
-        result["int4_moe"] = {
-            "workload": "Marlin int4 fused MoE, 128 experts, hidden 2048, inter 768, top-8, fp16",
-            "tokens_per_s_at_256": at256["tokens_per_s"],
-            "mfma_util_at_256": at256["mfma_util"],
-            "hbm_frac_at_256": at256["hbm_frac"],
-            "bound_at_256": "hbm",
-            "by_tokens": moe,
-        }
-        result["exl3_gemv_configs"] = gpu_gemv_configs(args, torch)
-        result["exl3_prefill"] = gpu_exl3_prefill(torch)
-        result["exl3_moe"] = gpu_exl3_moe(torch)
+    result.update(extras)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, torch)
         if not args.no_extras:

@@ -107,13 +107,15 @@ int exl3_linear_prefill_rows(void);
  *   workspace FP32, >= exl3_linear_workspace_size(rows, ...) elements,
  *            16-byte aligned, overlapping no other argument.
  * The weights are decoded bit-exactly; the products are summed in FP32 on
- * the matrix cores.  Up to 32 rows the activations are split into FP16 high
- * and low parts (about 22 significant bits), so the result agrees with the
- * reference's sequential FP32 chain to FP32 rounding, not bit for bit.
- * Above 32 rows, at up to 4 bits per weight with a 16-byte aligned trellis,
- * the many-row tile GEMM rounds each rotated input once to FP16 (as the
- * reference's GPU kernels do): FP16-operand tolerance, an rms error of about
- * 2^-12 rms(result); other many-row calls keep the split.  A small-M call
+ * the matrix cores, with the activations split into FP16 high and low
+ * parts (about 22 significant bits, the activation precision of the
+ * reference's tensor-core kernels, csrc/exl3/dense_prefill_tc.h:5-12), so
+ * the result agrees with the reference's sequential FP32 chain to FP32
+ * rounding, not bit for bit.  Above 32 rows a 16-byte aligned trellis runs
+ * on the many-row tile GEMM, any other on the decode-to-LDS prefill GEMM;
+ * under exl3_set_tile_precision(1) the tile GEMM rounds each rotated input
+ * once to FP16 instead (FP16-operand tolerance, an rms error of about
+ * 2^-12 rms(result), half the matrix work).  A small-M call
  * whose K-split partials (under a forced exl3_set_gemv_blocks, or an
  * unaligned trellis) exceed the workspace runs in column ranges that fit.
  * Replaces _exl3_C::linear_out (csrc/exl3/dense.cu:80-149; schema
@@ -169,17 +171,39 @@ int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hidden, const
 
 /*
  * Test and tuning switch, process-wide: the routed-row count from which an
- * expert of a fixed-rate (moe_out_v2, up to 4 bits per weight) call runs on
- * the many-row tile GEMM (tasks of up to 128 rows) instead of the small-M
- * GEMV (tasks of up to 32 rows); 0 = automatic (48 rows, and only when
- * the call's tile tasks make at least 128 workgroups in the narrower
- * projection), any other value = that threshold with no workgroup minimum
- * (1: every expert with 16-byte aligned matrices).  The tile GEMM rounds
- * each rotated input once to FP16 (FP16-operand tolerance), the GEMV keeps
- * FP16 high and low parts.  No counterpart in the reference (its nearest is
- * the prefill routing of moe_out_prefill, ops.py:1880-1910).
+ * expert of a fixed-rate call (exl3_moe_out with bits_x2 > 0: moe_out_v2,
+ * and moe_out_prefill at its bits_x2 10) runs on the many-row tile GEMM
+ * (tasks of up to 128 rows) instead of the small-M GEMV; 0 = automatic (48
+ * rows, and only when the call's tile tasks make at least 128 workgroups in
+ * the narrower projection), any other value = that threshold with no
+ * workgroup minimum (1: every expert with 16-byte aligned matrices).  Both
+ * kernels keep FP16 high and low activation parts (unless
+ * exl3_set_tile_precision(1)).  No counterpart in the reference (its
+ * nearest is the prefill routing of moe_out_prefill, ops.py:1880-1910).
  */
 int exl3_set_moe_tile_rows(int rows);
+
+/*
+ * Precision switch, process-wide: 0 (default) = the many-row tile GEMM
+ * (exl3_linear_out above 32 rows, the MoE tile tasks) multiplies FP16 high
+ * and low activation parts (~22 bits) against the exact FP16 weights, as
+ * the reference's tensor-core kernels split them
+ * (csrc/exl3/dense_prefill_tc.h:5-12); 1 = the high parts alone (each
+ * rotated input rounded once to FP16: half the matrix work, an rms error of
+ * about 2^-12 rms(result)), an explicit opt-in below the reference's
+ * precision.  No counterpart in the reference.
+ */
+int exl3_set_tile_precision(int fp16_only);
+
+/*
+ * Test and tuning switch, process-wide: the kernel exl3_linear_out runs
+ * above 32 rows: 0 = automatic (the tile GEMM for a 16-byte aligned
+ * trellis, else the decode-to-LDS prefill GEMM), 1 = the prefill GEMM,
+ * 2 = as 0.  Both keep the activations' high and low parts (the tile GEMM
+ * unless exl3_set_tile_precision(1)).  No counterpart in the reference
+ * (its nearest is set_gemm_shape_override, csrc/exl3/gemm.cu:400-409).
+ */
+int exl3_set_prefill_kernel(int kernel);
 
 /*
  * Test and tuning switch, process-wide: how exl3_linear_out finishes its

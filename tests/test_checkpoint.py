@@ -1,7 +1,8 @@
 """EXL3 checkpoint ingestion on the CPU (vllm_mi355x/kernels/exl3/checkpoint.py,
-mirroring vllm_sm80/kernels/exl3/utils.py:57-288 and quant.py:382-466):
-header inventory, matrix validation and its refusals, H128-block shards,
-loading, on synthetic checkpoints written with the safetensors library."""
+the on-disk rules of vllm_sm80/kernels/exl3/utils.py:183-288 and
+quant.py:382-466): header inventory, matrix validation and its refusals,
+H128-block shards, loading, on synthetic checkpoints written with the
+safetensors library."""
 
 import json
 import struct
@@ -49,9 +50,9 @@ def test_load_whole_and_sharded(ckpt):
     assert torch.equal(s.trellis, torch.cat([t[8:16, 0:8], t[8:16, 16:24]], 1))
     assert torch.equal(s.suh, tensors[f"{p}.suh"][128:256])
     assert torch.equal(s.svh, torch.cat([tensors[f"{p}.svh"][0:128], tensors[f"{p}.svh"][256:384]]))
-    with pytest.raises(ValueError, match="complete H128 blocks"):
+    with pytest.raises(ValueError, match="not whole H128 blocks"):
         C.Exl3PackedWeight(m.matrices[p], 64, 128, slice(0, 64), [slice(0, 128)])
-    with pytest.raises(ValueError, match="logical/padded"):
+    with pytest.raises(ValueError, match="does not pad to the stored"):
         m.matrices[p].validate_logical(100, 380)
 
 
@@ -67,12 +68,12 @@ def test_shard_slices():
 
 
 @pytest.mark.parametrize("case,message", [
-    ("multiplier", "multiplier"), ("both_markers", "conflicting EXL3 codebook"),
-    ("no_marker", "conflicting EXL3 codebook"), ("orphan", "Orphan"),
-    ("trellis_dtype", "Invalid EXL3 trellis"), ("geometry", "tile geometry"),
-    ("svh_shape", "incompatible EXL3 tensor"), ("rate", "bitrate/codebook"),
-    ("dense_conflict", "Conflicting dense"), ("duplicate", "Duplicate EXL3 source"),
-    ("index_conflict", "index/header conflict")])
+    ("multiplier", "holds multiplier"), ("both_markers", "exactly one codebook marker"),
+    ("no_marker", "exactly one codebook marker"), ("orphan", "without a trellis"),
+    ("trellis_dtype", "must be int16"), ("geometry", "not whole H128 blocks of whole"),
+    ("svh_shape", "svh must be fp16"), ("rate", "not a rate of codebook"),
+    ("dense_conflict", "both a dense .weight"), ("duplicate", "appears in both"),
+    ("index_conflict", "which does not hold it")])
 def test_refusals(tmp_path, case, message):
     rng = np.random.default_rng(1)
     p = "layer.proj"
@@ -119,12 +120,12 @@ def test_header_extent_checks(tmp_path):
     header[name]["data_offsets"][1] += 2  # claims more bytes than its shape
     body = json.dumps(header).encode()
     (tmp_path / "a.safetensors").write_bytes(struct.pack("<Q", len(body)) + body + raw[8 + n:])
-    with pytest.raises(ValueError, match="Invalid tensor extent|noncontiguous"):
+    with pytest.raises(ValueError, match="spans bytes|overlaps|gap"):
         C.read_headers(tmp_path / "a.safetensors")
     (tmp_path / "a.safetensors").write_bytes(raw + b"\0\0\0\0")
-    with pytest.raises(ValueError, match="Unaccounted"):
+    with pytest.raises(ValueError, match="belong to no tensor"):
         C.read_headers(tmp_path / "a.safetensors")
-    with pytest.raises(ValueError, match="requires local safetensors"):
+    with pytest.raises(ValueError, match="no \\*.safetensors files"):
         C.Exl3Manifest(tmp_path / "nothing")
 
 

@@ -6,7 +6,9 @@ Bars:
   * decoded weights: bit-exact (every format, aligned and unaligned bases);
   * linear_out: the oracle computes the reference's exact FP32 chain; the
     GPU sums on the matrix cores in another order with the activations split
-    into FP16 high/low parts, so FP32 outputs must agree to
+    into FP16 high/low parts (every kernel: the small-M GEMV, the many-row
+    tile GEMM and the decode-to-LDS prefill GEMM), so FP32 outputs must
+    agree to
     |err| <= 2^-14 * rms(ref) + 2^-16 * |ref| (a few FP32 roundings of a
     K-term sum; a wrong decode or index is off by O(rms)), and BF16 outputs
     within one BF16 ulp (a value next to a rounding boundary may round the
@@ -59,13 +61,14 @@ def _assert_fp32_close(actual, expected, name):
     assert (err <= bound).all(), f"{name}: err {err.flat[worst]:.3g} > {bound.flat[worst]:.3g} (rms {rms:.3g})"
 
 
-def _assert_tile_close(actual, expected, name):
-    """The many-row path's bar (FP16 operand tolerance): that path rounds each
-    rotated input once to FP16 (relative error <= 2^-11, as the reference's
-    GPU kernels do) and accumulates in FP32, so an output's error is a sum of
-    K independent rounding terms, about 2^-12 rms(ref) in rms.  Bar: every
-    output within 2^-8 rms(ref) + 2^-10 |ref| (max-abs), and the rms error
-    within 2^-10 rms(ref)."""
+def _assert_fp16_operand_close(actual, expected, name):
+    """The bar of the tile GEMM at FP16 precision (exl3_set_tile_precision(1),
+    an opt-in below the reference's precision): each rotated input is
+    rounded once to FP16 (relative error <= 2^-11) and the products are
+    accumulated in FP32, so an output's error is a sum of K independent
+    rounding terms, about 2^-12 rms(ref) in rms.  Bar: every output within
+    2^-8 rms(ref) + 2^-10 |ref| (max-abs), and the rms error within 2^-10
+    rms(ref)."""
     expected = expected.astype(np.float64)
     rms = float(np.sqrt(np.mean(expected ** 2)))
     err = np.abs(actual.astype(np.float64) - expected)
@@ -308,8 +311,7 @@ def test_prefill_matches_oracle(ops, device, rows, bits_x2, codebook):
                               logical_out, torch.float32))
     sample = sorted({0, 1, rows // 2, rows - 2, rows - 1})
     want = O.linear_out(x[sample], code, trellis, suh, svh, bits_x2, codebook, logical_out, O.FP32)
-    check = _assert_fp32_close if rows <= 32 else _assert_tile_close
-    check(got[sample], want, f"prefill rows={rows}")
+    _assert_fp32_close(got[sample], want, f"prefill rows={rows}")
 
 
 @pytest.mark.parametrize("rows", [40, 300])
@@ -346,4 +348,122 @@ def test_prefill_benchmark_shape(ops, device):
     got = _out_np(_run_linear(ops, device, trellis, suh, svh, x, code, 8, 2, n, torch.float32))
     sample = [0, 255, 511]
     want = O.linear_out(x[sample], code, trellis, suh, svh, 8, 2, n, O.FP32)
-    _assert_tile_close(got[sample], want, "prefill 8192x28672")
+    _assert_fp32_close(got[sample], want, "prefill 8192x28672")
+
+
+@pytest.fixture()
+def prefill_switches():
+    """exl3_set_prefill_kernel (0 automatic, 1 the decode-to-LDS prefill_gemm,
+    2 the tile GEMM) and exl3_set_tile_precision (1: FP16 high parts alone),
+    reset after the test."""
+    from vllm_mi355x import _native
+    lib = _native.load()
+
+    def kernel(k):
+        _native.check(lib.exl3_set_prefill_kernel(k))
+
+    def fp16_only(on):
+        _native.check(lib.exl3_set_tile_precision(int(on)))
+
+    yield kernel, fp16_only
+    _native.check(lib.exl3_set_prefill_kernel(0))
+    _native.check(lib.exl3_set_tile_precision(0))
+
+
+@pytest.mark.parametrize("rows", [33, 300, 513])
+@pytest.mark.parametrize("bits_x2,codebook", [(10, 1), (10, 2), (12, 1), (12, 2), (14, 1), (14, 2),
+                                              (16, 1), (16, 2), (3, 2), (8, 2)])
+@pytest.mark.parametrize("kernel", [1, 2])
+def test_prefill_kernels_every_rate_match_oracle(ops, device, prefill_switches, rows, bits_x2,
+                                                 codebook, kernel):
+    """Both many-row kernels at the rates above 4 bits per weight (the
+    reference's real checkpoints hold mostly bits_x2 10 / 12 / 16 dense
+    matrices) and two below, aligned trellis, ragged logical sizes and a
+    partial 256-column tile: the decode-to-LDS prefill_gemm (kernel 1) and
+    the register-decode tile GEMM (kernel 2), against the oracle on sampled
+    rows at the FP32 bar."""
+    print(f"prefill kernel={kernel} rows={rows} bits_x2={bits_x2} cb={codebook}", flush=True)
+    set_kernel, _ = prefill_switches
+    rng = np.random.default_rng(7000 + 100 * bits_x2 + 10 * codebook + rows)
+    k, n = 512, 768 + 128
+    trellis, suh, svh = random_matrix(rng, k, n, bits_x2, scales="test")
+    logical_in, logical_out = k - 5, n - 3
+    x, code = random_acts(rng, rows, logical_in, "bf16")
+    set_kernel(kernel)
+    got = _out_np(_run_linear(ops, device, trellis, suh, svh, x, code, bits_x2, codebook,
+                              logical_out, torch.float32))
+    sample = sorted({0, 1, rows // 2, rows - 2, rows - 1})
+    want = O.linear_out(x[sample], code, trellis, suh, svh, bits_x2, codebook, logical_out, O.FP32)
+    _assert_fp32_close(got[sample], want, f"kernel={kernel} rows={rows} bits_x2={bits_x2}")
+
+
+@pytest.mark.parametrize("offset_bytes", [2, 4])
+@pytest.mark.parametrize("bits_x2,codebook", [(10, 2), (12, 1), (14, 2), (16, 1), (16, 2), (8, 2)])
+@pytest.mark.parametrize("rows", [33, 300, 513])
+def test_prefill_unaligned_trellis_matches_oracle(ops, device, rows, offset_bytes, bits_x2,
+                                                  codebook):
+    """Many-row calls on trellis bases off a 16-byte boundary take the
+    decode-to-LDS prefill_gemm (halfword loads at a 2-byte offset, words at
+    a 4-byte one), against the oracle."""
+    print(f"prefill unaligned offset={offset_bytes} rows={rows} bits_x2={bits_x2}", flush=True)
+    rng = np.random.default_rng(7500 + offset_bytes + 10 * bits_x2 + rows)
+    k, n = 512, 384
+    trellis, suh, svh = random_matrix(rng, k, n, bits_x2, scales="test")
+    x, code = random_acts(rng, rows, k, "fp16")
+    flat = torch.empty(trellis.size + 8, dtype=torch.int16, device=device)
+    shift = offset_bytes // 2
+    view = flat[shift:shift + trellis.size].view(trellis.shape)
+    view.copy_(_dev(trellis, device))
+    assert view.data_ptr() % 16 == offset_bytes
+    out = torch.empty(rows, n, dtype=torch.float32, device=device)
+    ws = torch.empty(ops.linear_workspace_size(rows, k, n), dtype=torch.float32, device=device)
+    ops.linear_out(_to_torch_act(x, code, device), view, _dev(suh, device), _dev(svh, device),
+                   bits_x2, codebook, k, n, out, ws)
+    torch.cuda.synchronize()
+    sample = sorted({0, rows // 3, rows - 1})
+    want = O.linear_out(x[sample], code, trellis, suh, svh, bits_x2, codebook, n, O.FP32)
+    _assert_fp32_close(out.cpu().numpy()[sample], want, f"offset={offset_bytes} bits_x2={bits_x2}")
+
+
+@pytest.mark.parametrize("shape", [(4096, 1024), (5120, 512)])
+@pytest.mark.parametrize("kernel", [0, 1])
+def test_prefill_checkpoint_geometries_bits10(ops, device, prefill_switches, shape, kernel):
+    """Two dense geometries of the reference's real checkpoint inventory
+    (tests/models/deepseek_v41/sm80/fixtures/exl3_headers.json: a 4096 ->
+    1024 slice and the 5120 -> 512 projection) at bits_x2 10, mul1, 300
+    rows, on the automatic kernel and on prefill_gemm."""
+    print(f"prefill checkpoint geometry {shape} kernel={kernel}", flush=True)
+    set_kernel, _ = prefill_switches
+    k, n = shape
+    rng = np.random.default_rng(k + n)
+    trellis, suh, svh = random_matrix(rng, k, n, 10, scales="test")
+    x, code = random_acts(rng, 300, k, "bf16")
+    set_kernel(kernel)
+    got = _out_np(_run_linear(ops, device, trellis, suh, svh, x, code, 10, 2, n, torch.float32))
+    sample = [0, 150, 299]
+    want = O.linear_out(x[sample], code, trellis, suh, svh, 10, 2, n, O.FP32)
+    _assert_fp32_close(got[sample], want, f"{shape} kernel={kernel}")
+
+
+@pytest.mark.parametrize("bits_x2,codebook", [(8, 2), (4, 1), (3, 2), (10, 2), (16, 1)])
+@pytest.mark.parametrize("rows", [40, 300])
+def test_tile_fp16_precision_opt_in(ops, device, prefill_switches, bits_x2, codebook, rows):
+    """exl3_set_tile_precision(1): the tile GEMM on the FP16 high parts alone
+    (half the MFMAs), at the FP16-operand bar; the default afterwards is
+    the FP32 bar again."""
+    print(f"tile fp16 opt-in bits_x2={bits_x2} rows={rows}", flush=True)
+    _, fp16_only = prefill_switches
+    rng = np.random.default_rng(8100 + bits_x2 + rows)
+    k, n = 1024, 768
+    trellis, suh, svh = random_matrix(rng, k, n, bits_x2, scales="test")
+    x, code = random_acts(rng, rows, k, "fp16")
+    sample = [0, rows // 2, rows - 1]
+    want = O.linear_out(x[sample], code, trellis, suh, svh, bits_x2, codebook, n, O.FP32)
+    fp16_only(True)
+    got = _out_np(_run_linear(ops, device, trellis, suh, svh, x, code, bits_x2, codebook, n,
+                              torch.float32))
+    _assert_fp16_operand_close(got[sample], want, f"fp16 bits_x2={bits_x2}")
+    fp16_only(False)
+    got = _out_np(_run_linear(ops, device, trellis, suh, svh, x, code, bits_x2, codebook, n,
+                              torch.float32))
+    _assert_fp32_close(got[sample], want, f"hi/lo bits_x2={bits_x2}")

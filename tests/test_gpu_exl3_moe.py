@@ -55,19 +55,20 @@ def _oracle_f32(out, code):
     return O.bf16_bits_to_f32(out) if code == O.BF16 else out.astype(np.float32)
 
 
-# Absolute part of the MoE bar, in units of rms(ref).  Experts on the
-# small-M GEMV carry ~22-bit activations (FP16 high + low parts): 2^-13, and
-# an rms error within 2^-10 rms(ref).  Experts with enough rows for the
-# many-row tile GEMM round each rotated input once to FP16 (as the
-# reference's GPU kernels do), about 2^-11 rms(ref) of error through the
-# three projections, which also moves bf16 outputs across rounding
-# boundaries (one bf16 ulp, 2^-8 relative, for about one output in 16):
-# 2^-8 (max-abs), and an rms error within 2^-8 rms(ref).
+# Absolute part of the MoE bar, in units of rms(ref).  Both expert kernels
+# (the small-M GEMV and the many-row tile GEMM) carry ~22-bit activations
+# (FP16 high + low parts): 2^-13, and an rms error within 2^-10 rms(ref).
+# Under exl3_set_tile_precision(1) (an opt-in below the reference's
+# precision) the tile GEMM rounds each rotated input once to FP16, about
+# 2^-11 rms(ref) of error through the three projections, which also moves
+# bf16 outputs across rounding boundaries (one bf16 ulp, 2^-8 relative, for
+# about one output in 16): 2^-8 (max-abs), and an rms error within 2^-8
+# rms(ref).
 GEMV_ABS_RMS = 2.0 ** -13
-TILE_ABS_RMS = 2.0 ** -8
+FP16_ABS_RMS = 2.0 ** -8
 
 
-def _assert_moe_close(actual, expected, name, abs_rms=TILE_ABS_RMS, rms_bar=None):
+def _assert_moe_close(actual, expected, name, abs_rms=GEMV_ABS_RMS, rms_bar=None):
     expected = expected.astype(np.float64)
     rms = float(np.sqrt(np.mean(expected ** 2)))
     err = np.abs(actual.astype(np.float64) - expected)
@@ -77,7 +78,7 @@ def _assert_moe_close(actual, expected, name, abs_rms=TILE_ABS_RMS, rms_bar=None
     assert (err <= bound).all(), (
         f"{name}: err {err.flat[worst]:.3g} > {bound.flat[worst]:.3g} (rms {rms:.3g})")
     if rms_bar is None:
-        rms_bar = 2.0 ** -8 if abs_rms >= TILE_ABS_RMS else 2.0 ** -10
+        rms_bar = 2.0 ** -8 if abs_rms >= FP16_ABS_RMS else 2.0 ** -10
     assert np.sqrt(np.mean(err ** 2)) <= rms_bar * rms, f"{name}: rms error"
 
 
@@ -382,12 +383,26 @@ def tile_rows():
     _native.check(lib.exl3_set_moe_tile_rows(0))
 
 
-@pytest.mark.parametrize("bits_x2", [2, 3, 4, 5, 6, 7, 8])
+@pytest.fixture()
+def tile_fp16():
+    """exl3_set_tile_precision: True = the tile GEMM on FP16 high parts
+    alone; reset to the default (high and low parts) after the test."""
+    from vllm_mi355x import _native
+    lib = _native.load()
+
+    def set_(on):
+        _native.check(lib.exl3_set_tile_precision(int(on)))
+
+    yield set_
+    _native.check(lib.exl3_set_tile_precision(0))
+
+
+@pytest.mark.parametrize("bits_x2", [2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16])
 @pytest.mark.parametrize("rows,dtype", [(5, "bf16"), (40, "fp16")])
 def test_moe_tile_path_matches_oracle_and_gemv(ops, device, tile_rows, bits_x2, rows, dtype):
-    """Every expert on the many-row tile GEMM (threshold forced to 1 row):
-    against the oracle, and against the small-M GEMV path to the same bar
-    (the two sum in different FP32 orders)."""
+    """Every expert on the many-row tile GEMM (threshold forced to 1 row),
+    at every mul1 rate: against the oracle, and against the small-M GEMV
+    path to the same bar (the two sum in different FP32 orders)."""
     print(f"moe tile path bits_x2={bits_x2} rows={rows} {dtype}", flush=True)
     rng = np.random.default_rng(3000 * bits_x2 + rows)
     hidden, intermediate, experts, topk = 384, 256 + 128, 6, 4
@@ -408,6 +423,31 @@ def test_moe_tile_path_matches_oracle_and_gemv(ops, device, tile_rows, bits_x2, 
     _assert_moe_close(_out_np(tiled), _oracle_f32(expected, code), f"tile bits_x2={bits_x2}")
     _assert_moe_close(_out_np(tiled), _out_np(gemv).astype(np.float64), "tile vs gemv")
     assert torch.equal(tiled.view(torch.int16), again.view(torch.int16))
+
+
+@pytest.mark.parametrize("bits_x2", [3, 8, 10, 16])
+def test_moe_tile_fp16_precision_opt_in(ops, device, tile_rows, tile_fp16, bits_x2):
+    """exl3_set_tile_precision(1): the tile experts' rows on FP16 high parts
+    alone, at the FP16-operand bar; the default afterwards meets the
+    GEMV's bar again."""
+    print(f"moe tile fp16 opt-in bits_x2={bits_x2}", flush=True)
+    rng = np.random.default_rng(3500 + bits_x2)
+    hidden, intermediate, experts, topk, rows = 384, 384, 6, 4, 40
+    layer = Layer(rng, experts, hidden, intermediate, [(bits_x2, 2)], device, scales="sign")
+    ids = np.stack([rng.permutation(experts)[:topk] for _ in range(rows)])
+    weights = rng.random((rows, topk)).astype(np.float32)
+    expert_map = np.arange(experts, dtype=np.int64)
+    x_host, code, x = _acts(rng, rows, hidden, "bf16", device)
+    args = (_dev(ids, device), _dev(weights, device), layer, _dev(expert_map, device), intermediate)
+    expected = _oracle_f32(O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map,
+                                     intermediate, out_dtype=code), code)
+    tile_rows(1)
+    tile_fp16(True)
+    fp16 = _run(ops, x, *args, bits_x2=bits_x2)
+    _assert_moe_close(_out_np(fp16), expected, f"fp16 tile bits_x2={bits_x2}", FP16_ABS_RMS)
+    tile_fp16(False)
+    hilo = _run(ops, x, *args, bits_x2=bits_x2)
+    _assert_moe_close(_out_np(hilo), expected, f"hi/lo tile bits_x2={bits_x2}")
 
 
 @pytest.mark.parametrize("path", ["gemv", "tile"])
@@ -432,11 +472,10 @@ def test_moe_ragged_logical_sizes_match_oracle(ops, device, tile_rows, path, dty
     out = _run(ops, x, *args, bits_x2=6)
     expected = O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map, intermediate,
                          out_dtype=code)
-    bar = TILE_ABS_RMS if path == "tile" else GEMV_ABS_RMS
-    _assert_moe_close(_out_np(out), _oracle_f32(expected, code), f"ragged {path}", bar)
+    _assert_moe_close(_out_np(out), _oracle_f32(expected, code), f"ragged {path}")
 
 
-def test_moe_tile_path_clamp_geometry_and_alignment(ops, device, tile_rows):
+def test_moe_tile_path_clamp_geometry_and_alignment(ops, device, tile_rows, tile_fp16):
     """The tile path with the SwiGLU clamp, an expert of the wrong geometry
     (NaN rows, never read) and expert matrices at 2-byte offsets (routed to
     the GEMV, which reads any alignment)."""
@@ -454,11 +493,18 @@ def test_moe_tile_path_clamp_geometry_and_alignment(ops, device, tile_rows):
     expected = O.moe_out(x_host, code, ids, weights, layer.oracle, expert_map, intermediate,
                          swiglu_limit=0.5)
     # The clamp at 0.5 cuts gate / up sums of magnitude ~100 (inputs x4 over
-    # 512 inputs); FP16 operands leave them an absolute error of ~2^-12 of
-    # that magnitude, which the clamp does not shrink where it lets values
-    # through: a bar in units of the pre-clamp scale, 2^-4 rms(ref) max-abs
-    # and 2^-6 rms(ref) rms (an unclamped result is off by O(rms(ref))).
-    _assert_moe_close(_out_np(out), _oracle_f32(expected, code), "tile clamp", 2.0 ** -4, 2.0 ** -6)
+    # 512 inputs); the sums' absolute error, which the clamp does not shrink
+    # where it lets values through, is in units of that pre-clamp scale:
+    # with high and low parts (~22 bits) a bar of 2^-10 rms(ref), as the
+    # GEMV's clamp case; FP16 operands alone (the opt-in) leave ~2^-12 of
+    # the pre-clamp magnitude: 2^-4 rms(ref) max-abs and 2^-6 rms(ref) rms
+    # (an unclamped result is off by O(rms(ref))).
+    _assert_moe_close(_out_np(out), _oracle_f32(expected, code), "tile clamp", 2.0 ** -10)
+    tile_fp16(True)
+    out = _run(ops, x, *args, limit=0.5, bits_x2=6)
+    tile_fp16(False)
+    _assert_moe_close(_out_np(out), _oracle_f32(expected, code), "fp16 tile clamp", 2.0 ** -4,
+                      2.0 ** -6)
     # expert 2 at 2-byte offsets: GEMV tasks; the others stay on tiles
     ptrs = layer.ptrs.cpu().numpy()
     for p, (t, _, _, _, _) in enumerate(layer.host[2]):

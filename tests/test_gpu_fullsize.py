@@ -27,7 +27,7 @@ import torch
 from oracle import exl3_oracle as O
 from oracle import marlin_oracle as M
 from tests.exl3_cases import random_acts, random_matrix
-from tests.test_gpu_exl3_linear import _assert_tile_close, _dev, _out_np, _run_linear
+from tests.test_gpu_exl3_linear import _assert_fp32_close, _dev, _out_np, _run_linear
 from tests.test_gpu_exl3_moe import _assert_moe_close, _oracle_f32, _run
 from tests.test_gpu_marlin_moe import Layer as MarlinLayer
 from tests.test_gpu_marlin_moe import assert_close, dev, dev_act, from_f32, host_bits, routing
@@ -58,7 +58,7 @@ def test_prefill_full_shape_sampled_rows(ops, device, prefill_matrix, rows):
     assert np.isfinite(got).all()
     sample = [0, rows - 1]
     want = O.linear_out(x[sample], code, trellis, suh, svh, 8, 2, 28672, O.FP32)
-    _assert_tile_close(got[sample], want, f"prefill M={rows}")
+    _assert_fp32_close(got[sample], want, f"prefill M={rows}")
 
 
 # ---- EXL3 3-bit MoE layer at 2048 tokens --------------------------------------------
@@ -141,6 +141,70 @@ def test_moe_full_layer_2048_tokens(ops, device):
                          weights[rows_s].cpu().numpy(), oracle_layer, oracle_map, intermediate,
                          out_dtype=O.FP16)
     _assert_moe_close(_out_np(out[rows_s]), _oracle_f32(expected, O.FP16), "2048-token layer")
+
+
+# ---- moe_out_prefill's served configuration ---------------------------------------
+
+@pytest.fixture(scope="module")
+def prefill_moe_layer(device):
+    return _full_layer(device, 256, 2560, 640, 10, 2560)
+
+
+@pytest.mark.parametrize("rows", [65, 512, 3460])
+def test_moe_prefill_served_config(ops, device, prefill_moe_layer, rows):
+    """The one configuration the reference's moe_out_prefill serves: hidden
+    2560, intermediate 640, every routed matrix bits_x2 10 mul1, 65 to 3460
+    rows, 256 local experts, top-10 (csrc/exl3/moe_prefill.h:9-14,
+    vllm_sm80/kernels/exl3/ops.py:75-80), through
+    torch.ops._exl3_C.moe_out_prefill.  At 3460 rows most experts run on the
+    tile GEMM, at 65 on the small-M GEMV.  Three sampled tokens (routed to
+    three experts each, the other slots masked) against the oracle; the
+    call is deterministic and each token's result does not depend on the
+    other rows (a token routed alone runs on the GEMV: the MoE bar)."""
+    print(f"moe_out_prefill 256 x 2560/640 bits_x2 10 top-10 rows={rows}", flush=True)
+    hidden, intermediate, experts, topk = 2560, 640, 256, 10
+    layer = prefill_moe_layer
+    gen = torch.Generator(device=device)
+    gen.manual_seed(rows)
+    logits = torch.randn(rows, experts, generator=gen, device=device)
+    tw, ti = torch.topk(torch.softmax(logits, -1), topk, dim=-1)
+    tw = tw / tw.sum(-1, keepdim=True)
+    ids, weights = ti.int(), tw.float()
+    sampled = {0: (3, 17, 200), rows // 2: (5, 90, 255), rows - 1: (17, 42, 128)}
+    for t, chosen in sampled.items():
+        ids[t] = torch.tensor(list(chosen) + [-1] * (topk - 3), dtype=torch.int32)
+    ids, weights = ids.contiguous(), weights.contiguous()
+    emap = torch.arange(experts, dtype=torch.int32, device=device)
+    x = torch.randn(rows, hidden, generator=gen, device=device).bfloat16()
+    size = ops.moe_workspace_size(rows, hidden, intermediate, topk, experts)
+
+    def call(xx, ii, ww):
+        out = torch.full_like(xx, float("nan"))
+        ws = torch.empty(size, dtype=torch.float32, device=device)
+        torch.ops._exl3_C.moe_out_prefill(xx, ii, ww, layer.ptrs, layer.meta, emap, intermediate,
+                                          out, ws)
+        torch.cuda.synchronize()
+        return out
+
+    out = call(x, ids, weights)
+    assert torch.isfinite(out.float()).all() and out.float().abs().max() > 0
+    assert torch.equal(out.view(torch.int16), call(x, ids, weights).view(torch.int16))
+    r = rows // 3
+    alone = call(x[r:r + 1], ids[r:r + 1], weights[r:r + 1])
+    _assert_moe_close(_out_np(alone), _out_np(out[r:r + 1]).astype(np.float64), f"token {r}")
+    used = sorted({e for chosen in sampled.values() for e in chosen})
+    host = []
+    for e in used:
+        host.append([(t.cpu().numpy(), u.cpu().numpy(), v.cpu().numpy(), 10, 2)
+                     for t, u, v in layer.keep[3 * e:3 * e + 3]])
+    oracle_map = np.full(experts, -1, np.int64)
+    oracle_map[used] = np.arange(len(used))
+    rows_s = sorted(sampled)
+    xs = x[rows_s].view(torch.int16).cpu().numpy().view(np.uint16)
+    expected = O.moe_out(xs, O.BF16, ids[rows_s].cpu().numpy().astype(np.int64),
+                         weights[rows_s].cpu().numpy(), O.MoELayer(host), oracle_map, intermediate,
+                         out_dtype=O.BF16)
+    _assert_moe_close(_out_np(out[rows_s]), _oracle_f32(expected, O.BF16), f"rows={rows}")
 
 
 # ---- Marlin int4 MoE at the full expert shape ---------------------------------------

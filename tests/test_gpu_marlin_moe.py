@@ -232,6 +232,36 @@ def test_fused_zero_weights_masked_slots_and_empty(mm, device):
     assert out.shape == (0, K)
 
 
+def test_one_token_unrouted_writes_zeros(mm, device):
+    """One token takes the identity-routed path, whose w2 launch also forms
+    the top-k sum: a token none of whose slots is routed (ids outside the
+    experts, or an expert map sending every chosen expert to -1) still gets
+    its zero sum written, over whatever the output buffer held."""
+    rng = np.random.default_rng(19)
+    E, K, N, topk = 4, 256, 128, 3
+    layer = Layer(rng, E, K, N, M.BF16, device)
+    x = dev_act(from_f32(rng.standard_normal((1, K)), M.BF16), M.BF16, device)
+    w = torch.ones(1, topk, device=device)
+    nan = torch.full((1, K), float("nan"), dtype=x.dtype, device=device)
+    ids = torch.tensor([[-1, E, E + 3]], dtype=torch.int32, device=device)
+    out = mm[0].fused_marlin_moe(x, layer.w1, layer.w2, layer.s1, layer.s2, w, ids,
+                                 output=nan.clone())
+    assert torch.equal(out, torch.zeros_like(out))
+    emap = torch.tensor([-1, -1, 0, 1, 2, 3, -1], dtype=torch.int32, device=device)
+    ids = torch.tensor([[0, 1, 6]], dtype=torch.int32, device=device)
+    out = mm[0].fused_marlin_moe(x, layer.w1, layer.w2, layer.s1, layer.s2, w, ids,
+                                 expert_map=emap, output=nan.clone())
+    assert torch.equal(out, torch.zeros_like(out))
+    # one slot routed: the sum is that slot's row alone, and equals the
+    # staged path's
+    ids = torch.tensor([[-1, 2, E]], dtype=torch.int32, device=device)
+    out = mm[0].fused_marlin_moe(x, layer.w1, layer.w2, layer.s1, layer.s2, w, ids,
+                                 output=nan.clone())
+    ref = mm[0].fused_marlin_moe(x, layer.w1, layer.w2, layer.s1, layer.s2, w, ids,
+                                 path="staged")
+    assert torch.equal(out, ref)
+
+
 def test_fused_expert_map(mm, device):
     rng = np.random.default_rng(10)
     E_local, E_global, K, N, topk, T = 3, 6, 128, 128, 3, 9

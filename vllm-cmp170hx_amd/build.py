@@ -24,10 +24,12 @@ OBJDIR = os.path.join(HERE, "_build")
 
 # (source, object name, extra flags).  The small-M GEMV instantiations are
 # one source compiled once per part of the format list, so they build in
-# parallel (exl3_gemv.h).
+# parallel (exl3_gemv.h); the tile GEMM's likewise.
 GEMV_PARTS = 8
+TILE_PARTS = 4  # the tile GEMM's instantiations likewise (exl3_tile.h)
 # The slowest sources first.
 SOURCES = [("exl3_gemv_part.hip", f"exl3_gemv_part{p}", [f"-DVQ_GEMV_PART={p}"]) for p in range(GEMV_PARTS)] + \
+          [("exl3_tile_part.hip", f"exl3_tile_part{p}", [f"-DVQ_TILE_PART={p}"]) for p in range(TILE_PARTS)] + \
           [("marlin_moe.hip", "marlin_moe", []), ("exl3_gemm.hip", "exl3_gemm", []),
            ("exl3_linear.hip", "exl3_linear", []), ("exl3_moe.hip", "exl3_moe", []),
            ("exl3_ple.hip", "exl3_ple", []),

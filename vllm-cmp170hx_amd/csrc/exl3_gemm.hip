@@ -9,14 +9,14 @@
 //     the k order of the MFMA operands: within every 32-input step, group g
 //     (8 halves) holds inputs {2g, 2g+1, 2g+8, 2g+9} of its two 16-input tile
 //     rows.  Row r: [high: padded_in halves][low: padded_in halves]; the
-//     low parts are written only when prefill_gemm is the GEMM that reads
-//     them.
+//     low parts are written unless the GEMM reads the high parts alone.
 //  2. the GEMM:
-//     * up to 4 bits per weight with a 16-byte aligned trellis: tile_gemm
-//       (exl3_tile.h), weights decoded in registers straight into MFMA B
-//       operands, 128 x 256 tiles, on the high parts only (each rotated
-//       input rounded once to FP16, as the reference's GPU kernels do);
-//     * other rates (and unaligned trellis bases): prefill_gemm, 256 x 256
+//     * a 16-byte aligned trellis: tile_gemm (exl3_tile.h), weights decoded
+//       in registers straight into MFMA B operands, 128 x 256 tiles, on the
+//       high and low parts (the default) or, under
+//       exl3_set_tile_precision(1), the high parts alone (each rotated input
+//       rounded once to FP16);
+//     * other trellis bases: prefill_gemm, 256 x 256
 //       output tiles, 16 wavefronts, four per SIMD (8 along M x 2 along N,
 //       32 x 128 each = 1 x 4 v_mfma_f32_32x32x16_f16 tiles).  Per K step of
 //       32 inputs the workgroup decodes the 32 x 256 weight slab (32 trellis
@@ -34,6 +34,7 @@
 // above, and one int row exponent per row after them.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <type_traits>
 
@@ -64,8 +65,7 @@ constexpr int kLdsK = kBK + 8;      // LDS row stride in halves (80 bytes)
 // eight consecutive inputs a lane, H128 in registers and DPP); wavefront w
 // takes groups w, w + 4, ..., the first kCache of them kept in registers.
 // Pass 1 finds the row maximum of |t|, pass 2 writes the scaled high parts
-// (and the low parts when `lo`: the GEMM reading them is not the tile
-// GEMM) as dword pairs; groups past the register cache are formed again
+// (and the low parts when `lo`: the GEMM reads them) as dword pairs; groups past the register cache are formed again
 // (the same operations, so the same values).  Inputs past logical_in form
 // +0, as the reference's zero padding.
 // Half offset of input k within its 32-input step, in the operand order.
@@ -421,16 +421,30 @@ int launch_gemm(bool aligned, const PrefillArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-namespace {
-
-template <int kBitsX2, int kCodebook>
-int launch_tile(const TileArgs& a, hipStream_t stream) {
-  const dim3 grid(unsigned((a.np + kTileCols - 1) / kTileCols), unsigned((a.rows + kTileRows - 1) / kTileRows));
-  hipLaunchKernelGGL((tile_gemm<kBitsX2, kCodebook, false>), grid, dim3(kTileThreads), 0, stream, a);
-  return vq::check_launch("exl3 tile_gemm");
+int launch_tile_gemm(int64_t bits_x2, int64_t codebook, bool moe, bool lo, const TileArgs& a, dim3 grid,
+                     hipStream_t stream) {
+  const int index = format_index(int(bits_x2), int(codebook));
+  if (index < 0 || !known_format(bits_x2, codebook) || !tile_rate(bits_x2)) {
+    return vq::fail("Unsupported EXL3 rate/codebook combination");
+  }
+  switch (index % kTileParts) {
+#define VQ_PART(P) \
+  case P: return tile_launch_part<P>(bits_x2, codebook, moe, lo, a, grid, stream);
+    VQ_PART(0) VQ_PART(1) VQ_PART(2) VQ_PART(3)
+#undef VQ_PART
+  }
+  return vq::fail("Unsupported EXL3 rate/codebook combination");
 }
 
+namespace {
+
+// exl3_set_tile_precision / exl3_set_prefill_kernel
+std::atomic<int> g_tile_fp16_only{0};
+std::atomic<int> g_prefill_kernel{0};
+
 }  // namespace
+
+bool tile_fp16_only() { return g_tile_fp16_only.load() != 0; }
 
 int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trellis,
                    int64_t tiles_k, int64_t tiles_n, const uint16_t* suh, const uint16_t* svh,
@@ -441,22 +455,25 @@ int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trel
   if (rows > 65535 * int64_t(kTileRows)) return vq::fail("EXL3 linear has too many rows");
   _Float16* act = reinterpret_cast<_Float16*>(workspace);
   int* row_exp = reinterpret_cast<int*>(workspace + rows * kp);
-  // the tile GEMM: up to 4 bits per weight, a 16-byte aligned trellis
-  // (LDS-DMA), 32-bit buffer offsets over the matrix and the activations;
-  // it reads the activations' high parts alone
+  // the tile GEMM: a 16-byte aligned trellis (LDS-DMA), 32-bit buffer
+  // offsets over the matrix and the activations; under
+  // exl3_set_tile_precision(1) it reads the activations' high parts alone
   const uintptr_t base = reinterpret_cast<uintptr_t>(trellis);
-  const bool tile = tile_rate(bits_x2) && (base & 15) == 0 && tiles_k * tiles_n * 16 * bits_x2 <= INT_MAX &&
-                    rows * 4 * kp <= INT_MAX;
+  const int forced = g_prefill_kernel.load();
+  const bool tile = forced != 1 && tile_rate(bits_x2) && (base & 15) == 0 &&
+                    tiles_k * tiles_n * 16 * bits_x2 <= INT_MAX && rows * 4 * kp <= INT_MAX;
+  const bool tile_lo = !tile_fp16_only();
+  const bool lo = !tile || tile_lo;
   {
     // the register cache sized to the 4-block groups a wavefront forms
     const int64_t per_wave = ((kp / 128 + 3) / 4 + 3) / 4;
     const dim3 grid{unsigned(rows)};
     if (per_wave <= 1) {
-      hipLaunchKernelGGL(prefill_input<1>, grid, dim3(256), 0, stream, x, x_dtype, logical_in, kp, suh, act, row_exp, !tile);
+      hipLaunchKernelGGL(prefill_input<1>, grid, dim3(256), 0, stream, x, x_dtype, logical_in, kp, suh, act, row_exp, lo);
     } else if (per_wave <= 2) {
-      hipLaunchKernelGGL(prefill_input<2>, grid, dim3(256), 0, stream, x, x_dtype, logical_in, kp, suh, act, row_exp, !tile);
+      hipLaunchKernelGGL(prefill_input<2>, grid, dim3(256), 0, stream, x, x_dtype, logical_in, kp, suh, act, row_exp, lo);
     } else {
-      hipLaunchKernelGGL(prefill_input<4>, grid, dim3(256), 0, stream, x, x_dtype, logical_in, kp, suh, act, row_exp, !tile);
+      hipLaunchKernelGGL(prefill_input<4>, grid, dim3(256), 0, stream, x, x_dtype, logical_in, kp, suh, act, row_exp, lo);
     }
   }
   if (int rc = vq::check_launch("exl3 prefill_input")) return rc;
@@ -476,11 +493,8 @@ int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trel
     t.out = out;
     t.out_dtype = out_dtype;
     t.logical_out = logical_out;
-#define VQ_CASE(B, C) \
-    if (bits_x2 == B && codebook == C) return launch_tile<B, C>(t, stream);
-    VQ_CASE(2, 1) VQ_CASE(4, 1) VQ_CASE(6, 1) VQ_CASE(8, 1)
-    VQ_CASE(2, 2) VQ_CASE(3, 2) VQ_CASE(4, 2) VQ_CASE(5, 2) VQ_CASE(6, 2) VQ_CASE(7, 2) VQ_CASE(8, 2)
-#undef VQ_CASE
+    const dim3 grid(unsigned((np + kTileCols - 1) / kTileCols), unsigned((rows + kTileRows - 1) / kTileRows));
+    return launch_tile_gemm(bits_x2, codebook, false, tile_lo, t, grid, stream);
   }
   PrefillArgs a{act, row_exp, trellis, svh, out, rows, kp, np, tiles_n, logical_out, out_dtype};
   const bool aligned = (base & 3) == 0;
@@ -498,3 +512,15 @@ int prefill_linear(const void* x, int x_dtype, int64_t rows, const uint8_t* trel
 }
 
 }  // namespace exl3
+
+extern "C" int exl3_set_tile_precision(int fp16_only) {
+  if (fp16_only != 0 && fp16_only != 1) return vq::fail("EXL3 tile precision must be 0 (high and low parts) or 1 (FP16)");
+  exl3::g_tile_fp16_only.store(fp16_only);
+  return vq::kOk;
+}
+
+extern "C" int exl3_set_prefill_kernel(int kernel) {
+  if (kernel < 0 || kernel > 2) return vq::fail("EXL3 prefill kernel must be 0 (automatic), 1 or 2");
+  exl3::g_prefill_kernel.store(kernel);
+  return vq::kOk;
+}

@@ -830,15 +830,6 @@ int launch_format(bool aligned, int load, const GemvArgs* gemv, int gemv_blocks,
 // VQ_EXL3_FORMATS is instantiated by part i % kGemvParts.
 constexpr int kGemvParts = 8;
 
-constexpr int format_index(int bits_x2, int codebook) {
-  int i = 0;
-#define VQ_INDEX(B, C)                       \
-  if (bits_x2 == B && codebook == C) return i; \
-  ++i;
-  VQ_EXL3_FORMATS(VQ_INDEX)
-#undef VQ_INDEX
-  return -1;
-}
 
 // launch_format for the formats of part P (exl3_gemv_part.hip, built with
 // VQ_GEMV_PART = P); a format of another part is refused.

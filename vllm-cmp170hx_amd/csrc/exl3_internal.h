@@ -53,6 +53,18 @@ struct CounterSlots {
 };
 CounterSlots counter_slots(hipStream_t stream, int64_t slots);
 
+// Position of a format in VQ_EXL3_FORMATS (-1: not admitted); the kernels'
+// instantiations are split over separately compiled parts by it.
+constexpr int format_index(int bits_x2, int codebook) {
+  int i = 0;
+#define VQ_INDEX(B, C)                       \
+  if (bits_x2 == B && codebook == C) return i; \
+  ++i;
+  VQ_EXL3_FORMATS(VQ_INDEX)
+#undef VQ_INDEX
+  return -1;
+}
+
 inline bool known_format(int64_t bits_x2, int64_t codebook) {
 #define VQ_KNOWN(B, C) if (bits_x2 == B && codebook == C) return true;
   VQ_EXL3_FORMATS(VQ_KNOWN)
@@ -84,6 +96,11 @@ __device__ __forceinline__ int scale_exponent(uint32_t max_bits) {
 __device__ __forceinline__ float u16_act(uint16_t v, int dtype) {
   return dtype == vq::kBF16 ? vq::bf16_to_f32(v) : vq::f16_to_f32(v);
 }
+
+// Activation precision of the many-row tile GEMM (exl3_set_tile_precision,
+// exl3_gemm.hip): false (the default) = FP16 high and low parts, true = the
+// high part alone.
+bool tile_fp16_only();
 
 // Large-M (prefill) dense linear, rows > 32 (exl3_gemm.hip).  Arguments as
 // exl3_linear_out's, validated by it; workspace holds rows * padded_in

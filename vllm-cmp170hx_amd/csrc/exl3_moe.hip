@@ -10,15 +10,17 @@
 //  2. per projection (gate, up): moe_form builds t = H128(x[a / topk] * suh)
 //     of every local assignment, as FP16 high/low parts in MFMA B-operand
 //     order with one power-of-two scale per assignment row (the high parts
-//     alone for the tile experts' rows); moe_gemv runs
+//     alone for the tile experts' rows when the tile GEMM runs at FP16
+//     precision); moe_gemv runs
 //     every task against its expert's matrix: one workgroup = (task, 128
 //     output columns) over the whole K range, trellis streamed with
 //     coalesced buffer loads, decoded in registers, each decoded operand fed
 //     to v_mfma_f32_16x16x32_f16 for every 8-row sub-block of the task, then
 //     the output H128 and svh in the same kernel.  Experts with at least
-//     48 routed rows (fixed rates up to 4 bits, 16-byte aligned matrices)
-//     run instead on the tile GEMM (exl3_tile.h: 128-row tasks x 256
-//     columns, FP16 high parts only), when their tasks make enough
+//     48 routed rows (a call's fixed rate, 16-byte aligned matrices) run
+//     instead on the tile GEMM (exl3_tile.h: 128-row tasks x 256 columns,
+//     high and low parts, or the high parts alone under
+//     exl3_set_tile_precision(1)), when their tasks make enough
 //     workgroups to fill the chip.
 //  3. moe_form (activation): clamp, SiLU(gate) * up * suh_down, H128 - the
 //     down projection's activations, in the same B-operand form.
@@ -322,7 +324,7 @@ template <bool kActivate, int kCache>
 __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, int x_dtype,
                                                 int64_t hidden, int64_t intermediate, int projection,
                                                 const int* table, float* ws, MoeLayout lay,
-                                                float limit) {
+                                                float limit, bool tile_lo) {
   __shared__ uint32_t row_max;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -336,8 +338,9 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   const int64_t e = local_expert(routing, a);
   const int64_t* ptrs = routing.ptrs + e * 9;
   // the tile experts' rows (sorted rows from the first tile task's first
-  // on) feed only the tile GEMM, which reads the high parts
-  const bool lo = table[2] == 0 ||
+  // on) feed only the tile GEMM, which reads the low parts unless it runs
+  // at FP16 precision
+  const bool lo = tile_lo || table[2] == 0 ||
                   int(blockIdx.x) < reinterpret_cast<const int4*>(table + lay.tasks())[table[3]].y;
   int* exps = reinterpret_cast<int*>(ws + lay.ints()) + lay.exps() + a * (lay.kmax() / 128);
   const __amdgpu_buffer_rsrc_t dst =
@@ -935,9 +938,9 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   const int task_rows = exl3::task_rows(fixed);
   const int64_t max_tasks =
       std::min<int64_t>(assignments, (assignments + task_rows - 1) / task_rows + local_experts);
-  // experts with enough rows run on the tile GEMM (fixed rates up to 4 bits)
-  // Experts with enough rows run on the tile GEMM (fixed rates up to 4
-  // bits).  Tile tasks = sum over those experts of ceil(rows / 128), at most
+  // Experts with enough rows run on the tile GEMM (a call with one rate for
+  // the layer, any rate).  Tile tasks = sum over those experts of
+  // ceil(rows / 128), at most
   // assignments / tile_rows for a threshold up to 64 rows; when that bound
   // is under the workgroup minimum (enough tasks for kMinTileBlocks
   // workgroups in the narrower projection) no call can have tile tasks and
@@ -947,7 +950,9 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   const int min_tile_tasks = exl3::tile_min_tasks(
       int((exl3::kMinTileBlocks * exl3::kTileCols + narrow - 1) / narrow));
   int64_t max_tiles = 0;
-  if (fixed > 0 && exl3::tile_rate(fixed) && assignments >= tile_rows) {
+  const int tile_bits = bits_x2 > 0 && exl3::tile_rate(bits_x2) ? int(bits_x2) : 0;
+  const bool tile_lo = !exl3::tile_fp16_only();
+  if (tile_bits > 0 && assignments >= tile_rows) {
     max_tiles = tile_rows <= 64 ? assignments / tile_rows
                                 : assignments / exl3::kTileRows + assignments / tile_rows + 1;
     max_tiles = std::min<int64_t>(max_tiles, assignments);
@@ -985,13 +990,7 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       t.task_group = int(std::min<int64_t>(8, per_xcd));
       const int64_t groups = (per_xcd + t.task_group - 1) / t.task_group;
       const dim3 grid{unsigned(8 * groups * t.task_group * t.col_tiles), 1u, 1u};
-      switch (fixed) {
-#define VQ_TILE(B) case B: hipLaunchKernelGGL((exl3::tile_gemm<B, 2, true>), grid, dim3(exl3::kTileThreads), 0, s, t); break;
-        VQ_TILE(2) VQ_TILE(3) VQ_TILE(4) VQ_TILE(5) VQ_TILE(6) VQ_TILE(7) VQ_TILE(8)
-#undef VQ_TILE
-        default: return fail("EXL3 MoE: no tile GEMM for this rate");
-      }
-      return check_launch("exl3 moe tile_gemm");
+      return exl3::launch_tile_gemm(tile_bits, 2, true, tile_lo, t, grid, s);
     };
     const int want_bits = fixed == 0 ? int(bits_x2) : 0;
     auto gemv = [&](int projection, int64_t kp, int64_t np, int64_t in_off, int64_t out_off) {
@@ -1014,7 +1013,7 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       const dim3 grid{unsigned(assignments), 1u, 1u};
 #define VQ_FORM(A, C)                                                                              \
   hipLaunchKernelGGL((exl3::moe_form<A, C>), grid, dim3(256), 0, s, routing, x, x_dtype, hidden, \
-                     intermediate_size, projection, table, workspace, lay, swiglu_limit)
+                     intermediate_size, projection, table, workspace, lay, swiglu_limit, tile_lo)
       if (activate) {
         if (per_wave <= 1) VQ_FORM(true, 1); else if (per_wave <= 2) VQ_FORM(true, 2); else VQ_FORM(true, 4);
       } else {

@@ -21,18 +21,22 @@
 // the 16 bytes of group g of row m: stored in LDS as [g][m] (1 KB per block),
 // read with one ds_read_b128 at 16 * lane, conflict-free.
 //
-// Activations: FP16 at a per-row power-of-two scale (the high part of the
-// activation buffer; its low part serves the small-M kernels), accumulated in
-// FP32: one rounding of each rotated input to FP16, as in the reference's
-// GPU kernels.
+// Activations: each rotated input at a per-row power-of-two scale, split
+// into FP16 high and low parts (t 2^e = hi + lo, ~22 bits) with both parts
+// multiplied against the exact FP16 weight into one FP32 accumulator (kLo,
+// the default: the activation precision of the reference's tensor-core
+// kernels, csrc/exl3/dense_prefill_tc.h:5-12), or the high part alone
+// (!kLo: each rotated input rounded once to FP16, half the MFMAs; an
+// explicit opt-in).
 //
 // Pipeline, per wavefront (one barrier a step):
-//   * trellis: LDS-DMA (buffer_load ... lds), 1 KB per step, into a ring of
-//     4 slots, issued 4 steps ahead; a step's ring words are read and
-//     decoded (into registers) one step before its MFMAs;
-//   * activations: LDS-DMA of the tile's 8 row blocks per step, 2 per
-//     wavefront, into 3 buffers, issued 2 steps ahead; the
-//     operands of row block rb + 2 are read under the MFMAs of rb;
+//   * trellis: LDS-DMA (buffer_load ... lds), 128 bits_x2 bytes per step
+//     (one 1 KB load up to 4 bits per weight, two above), into a ring of 4
+//     slots, issued 4 steps ahead; a step's ring words are read and decoded
+//     (into registers) one step before its MFMAs;
+//   * activations: LDS-DMA of the tile's 8 row blocks per step (and their
+//     low parts), 2 (4) per wavefront, into 3 buffers, issued 2 steps ahead;
+//     the operands of row block rb + 2 are read under the MFMAs of rb;
 //   * step s: issue the activation loads of s + 2, read the words of s + 1,
 //     issue the trellis load of s + 4, run the MFMAs of s with the decode of
 //     s + 1 between them (the VALU work of one step under the matrix work of
@@ -62,9 +66,11 @@ constexpr int kTileRing = 4;
 constexpr int kTileADma = kTileBlocks / kTileWaves;  // 1 KB activation loads per wave and step
 constexpr int kTileRedStride = kTileCols + 4;       // epilogue row stride (floats)
 
-// The tile GEMM serves these rates (the trellis of one step of a wavefront
-// fits one 1 KB load).
-constexpr bool tile_rate(int64_t bits_x2) { return bits_x2 >= 2 && bits_x2 <= 8; }
+// The tile GEMM serves every rate: the trellis of one step of a wavefront
+// (four tile columns x two tile rows, 128 bits_x2 bytes) is one 1 KB load
+// up to 4 bits per weight, two above.
+constexpr bool tile_rate(int64_t bits_x2) { return bits_x2 >= 2 && bits_x2 <= 16; }
+constexpr int tile_slot_bytes(int bits_x2) { return bits_x2 <= 8 ? 1024 : 2048; }
 
 struct TileArgs {
   // activation rows: row r at act + r * act_row_bytes, [high: kp halves]
@@ -92,6 +98,7 @@ struct TileArgs {
   const int64_t* meta;
   int projection;
   float* moe_out;
+  const int* moe_row_exp;  // MoE: exponent of assignment a at moe_row_exp[a * exp_stride]
   int col_tiles;           // column tiles per task
   int task_group;          // tasks per group in an XCD's order (1..8)
 };
@@ -118,36 +125,15 @@ template <int kOffset>
 __device__ __forceinline__ void tile_read4(uint32_t& v, uint32_t address) {
   asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(address), "i"(kOffset));
 }
-// At most n LDS reads still pending (they complete in order): a ready.
+// At most n LDS reads still pending (they complete in order).
 template <int n>
-__device__ __forceinline__ void tile_wait(half8_t& a) {
-  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(n));
-}
-// Every LDS read done: a and the ring words ready.
-template <int kWords>
-__device__ __forceinline__ void tile_wait_last(half8_t& a, uint32_t (&w)[2][2][kWords]) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a));
-#pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < kWords; ++i) asm volatile("" : "+v"(w[p][h][i]));
-}
-// At most n LDS reads pending: a and the ring words (read before a) ready.
-template <int n, int kWords>
-__device__ __forceinline__ void tile_wait(half8_t& a, uint32_t (&w)[2][2][kWords]) {
-  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(n));
-#pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < kWords; ++i) asm volatile("" : "+v"(w[p][h][i]));
-}
-template <int n, int kWords>
-__device__ __forceinline__ void tile_wait_words(uint32_t (&w)[2][2][kWords]) {
+__device__ __forceinline__ void tile_lgkm() {
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(n));
+}
+// v is ready (after a tile_lgkm that covers its read).
+__device__ __forceinline__ void tile_ready(half8_t& v) { asm volatile("" : "+v"(v)); }
+template <int kWords>
+__device__ __forceinline__ void tile_ready(uint32_t (&w)[2][2][kWords]) {
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -156,19 +142,26 @@ __device__ __forceinline__ void tile_wait_words(uint32_t (&w)[2][2][kWords]) {
       for (int i = 0; i < kWords; ++i) asm volatile("" : "+v"(w[p][h][i]));
 }
 
-template <int kBitsX2, int kCodebook, bool kMoe>
+template <int kBitsX2, int kCodebook, bool kMoe, bool kLo>
 __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   constexpr int kRows = kTileRows;
   constexpr int kBlocks = kRows / 16;
   constexpr int kADma = kBlocks / kTileWaves;
-  static_assert(tile_rate(kBitsX2), "one 1 KB trellis load per step");
+  constexpr int kParts = kLo ? 2 : 1;      // activation parts: high (and low)
+  constexpr int kAL = kParts * kADma;      // activation loads per wavefront and step
+  static_assert(tile_rate(kBitsX2), "a rate the tile GEMM serves");
   constexpr int kWords = LaneLoad<kBitsX2>::kWords;
   constexpr int kTileBytes = 16 * kBitsX2;
   constexpr int kRowChunk = 4 * kTileBytes;  // one tile row of a wavefront's four tile columns
-  __shared__ __attribute__((aligned(16))) uint8_t a_lds[kTileABufs][kBlocks][1024];
-  __shared__ __attribute__((aligned(16))) uint8_t t_lds[kTileWaves][kTileRing][1024];
-  __shared__ int row_id[kRows];
-  __shared__ int row_e[kRows];
+  constexpr int kSlot = tile_slot_bytes(kBitsX2);
+  constexpr int kTL = kSlot / 1024;          // trellis loads per wavefront and step
+  constexpr int kChunkLanes = kRowChunk / 16;
+  static_assert(kRowChunk % 16 == 0 && 2 * kRowChunk <= kSlot, "a step's trellis fits its slot");
+  // 80 KB at most (two workgroups per CU in 160 KB)
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[kTileABufs][kParts * kBlocks][1024];
+  __shared__ __attribute__((aligned(16))) uint8_t t_lds[kTileWaves][kTileRing][kSlot];
+  static_assert(sizeof(a_lds) + sizeof(t_lds) <= 80 * 1024, "two workgroups per CU");
+  static_assert(sizeof(t_lds) >= 2 * kRows * sizeof(int), "the epilogue's row table fits the ring");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -238,18 +231,22 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     svh = a.svh;
     tiles_n = a.tiles_n;
   }
-  if (tid < kRows) {
-    const int t = tid < nrows ? tid : nrows - 1;  // rows past the tile repeat its last row
-    int r;
+  // the activation row of the tile's row t (rows past the tile repeat its
+  // last row)
+  auto row_of = [&](int t) -> int {
+    t = t < nrows ? t : nrows - 1;
     if constexpr (kMoe) {
-      r = a.table[4 + first + t];
+      return a.table[4 + first + t];
     } else {
-      r = int(int64_t(blockIdx.y) * kRows + t);
+      return int(int64_t(blockIdx.y) * kRows + t);
     }
-    row_id[tid] = r;
-    row_e[tid] = a.row_exp[int64_t(r) * a.exp_stride];
+  };
+  // thread t < kRows keeps row t's id and exponent for the epilogue
+  int my_row = 0, my_e = 0;
+  if (tid < kRows) {
+    my_row = row_of(tid);
+    my_e = a.row_exp[int64_t(my_row) * a.exp_stride];
   }
-  __syncthreads();
 
   const int nblocks = (nrows + 15) >> 4;  // 16-row blocks with rows
   const int steps = int(a.kp / 32);
@@ -261,35 +258,53 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   const int64_t tc_load = tc0 + 4 <= tiles_n ? tc0 : 0;
 
   // ---- loads ----
-  // trellis: lane l copies 16 bytes of the step's two tile rows (lanes past
-  // them copy the first 16 bytes again, into the slot's unread tail)
+  // trellis: 16-byte chunk c = lane + 64 u of load u (chunks past the
+  // step's two tile rows copy the first chunk again, into the slot's unread
+  // tail); chunk c lands at byte 16 c of the slot
   const __amdgpu_buffer_rsrc_t t_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(trellis + tc_load * kTileBytes), 0, (steps * 2 - 1) * row_bytes + kRowChunk,
       0x00020000);
-  const int t_voff = lane < 2 * kRowChunk / 16 ? (lane / (kRowChunk / 16)) * row_bytes +
-                                                     16 * (lane % (kRowChunk / 16))
-                                               : 0;
+  int t_voff[kTL];
+#pragma unroll
+  for (int u = 0; u < kTL; ++u) {
+    const int c = lane + 64 * u;
+    t_voff[u] = c < 2 * kChunkLanes ? (c / kChunkLanes) * row_bytes + 16 * (c % kChunkLanes) : 0;
+  }
+  // (each builtin's offsets are locals: an array element passed straight
+  // to the builtin makes the host compilation drop the kernel's launch stub)
   auto load_trellis = [&](int s) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(t_rsrc, (tile_lds_ptr_t)&t_lds[wave][s % kTileRing][0], 16,
-                                             t_voff, s * 2 * row_bytes, 0, 0);
+#pragma unroll
+    for (int u = 0; u < kTL; ++u) {
+      const int voff = t_voff[u];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(t_rsrc, (tile_lds_ptr_t)&t_lds[wave][s % kTileRing][1024 * u], 16,
+                                               voff, s * 2 * row_bytes, 0, 0);
+    }
   };
-  // activations: this wavefront's row blocks rb = kADma * wave + i
-  // low part j / kBlocks, row block j % kBlocks); lane (g, m) copies
-  // group g of row 16 rb + m
+  // activations: this wavefront's row blocks rb = kADma * wave + i; lane
+  // (g, m) copies group g of row 16 rb + m, its high part into block rb of
+  // the buffer and its low part (2 kp bytes on) into block kBlocks + rb
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(a.act), 0, int(a.act_rows * a.act_row_bytes), 0x00020000);
+  const int lo_off = int(2 * a.kp);
   int a_voff[kADma];
 #pragma unroll
   for (int i = 0; i < kADma; ++i) {
     const int rb = kADma * wave + i;
-    a_voff[i] = int(int64_t(row_id[16 * rb + m]) * a.act_row_bytes + 16 * g);
+    a_voff[i] = int(int64_t(row_of(16 * rb + m)) * a.act_row_bytes + 16 * g);
   }
   auto load_act = [&](int s) {
     const int buf = s % kTileABufs;
 #pragma unroll
     for (int i = 0; i < kADma; ++i) {
+      const int hi_voff = a_voff[i];
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (tile_lds_ptr_t)&a_lds[buf][kADma * wave + i][0],
-                                               16, a_voff[i], s * 64, 0, 0);
+                                               16, hi_voff, s * 64, 0, 0);
+      if constexpr (kLo) {
+        const int lo_voff = hi_voff + lo_off;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc,
+                                                 (tile_lds_ptr_t)&a_lds[buf][kBlocks + kADma * wave + i][0],
+                                                 16, lo_voff, s * 64, 0, 0);
+      }
     }
   };
 
@@ -314,7 +329,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
 
   // LDS reads in the loop go through tile_read* (outside the compiler's
   // tracking of the LDS-DMA loads, which would make each read wait for
-  // every load in flight); tile_wait names the values it makes ready.
+  // every load in flight); tile_ready names the values a wait made ready.
   const uint32_t a_lane = vq::lds_address(&a_lds[0][0][0]) + 16 * lane;
   const uint32_t t_base = vq::lds_address(&t_lds[wave][0][0]);
   uint32_t word_addr[2][2][kWords];
@@ -326,13 +341,13 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
       for (int i = 0; i < kWords; ++i) word_addr[p][h][i] = t_base + word_off[p][h][i];
   uint32_t words[2][2][kWords];
   auto read_words = [&](auto slot) {
-    constexpr int kSlot = decltype(slot)::value;
+    constexpr int kSlotIdx = decltype(slot)::value;
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < kWords; ++i) tile_read4<kSlot * 1024>(words[p][h][i], word_addr[p][h][i]);
+        for (int i = 0; i < kWords; ++i) tile_read4<kSlotIdx * kSlot>(words[p][h][i], word_addr[p][h][i]);
   };
 
   // decode of step words w into B operands of pair p: first / second MFMA
@@ -352,45 +367,51 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   load_trellis(min(2, last));
   load_act(min(1, last));
   load_trellis(min(3, last));
-  vq::wait_vmcnt<kADma + 2>();  // T(0), T(1) and A(0) of this wavefront landed
+  vq::wait_vmcnt<kAL + 2 * kTL>();  // T(0), T(1) and A(0) of this wavefront landed
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   read_words(std::integral_constant<int, 0>{});
-  tile_wait_words<0>(words);
+  tile_lgkm<0>();
+  tile_ready(words);
   half8_t b_cur[2][2];              // step s's B operands
   decode_pair(words, 0, b_cur);
   decode_pair(words, 1, b_cur);
 
-  // step s, its trellis in ring slot kSlot = s % 4 (the loop runs four steps
+  // step s, its trellis in ring slot kS = s % 4 (the loop runs four steps
   // an iteration: steps is a multiple of 4): the MFMAs of kRB row blocks of
-  // step s on b_cur, with the words of step s + 1 read and decoded between
-  // them
+  // step s on b_cur (high parts, then low parts), with the words of step
+  // s + 1 read and decoded between them
   auto step = [&](int s, auto slot, auto row_blocks) {
-    constexpr int kSlot = decltype(slot)::value;
+    constexpr int kS = decltype(slot)::value;
     constexpr int kRB = decltype(row_blocks)::value;
+    static_assert(kRB >= 2, "two row blocks read ahead");
     load_act(min(s + 2, last));
     // T(s + 1) landed: after it came A(s), T(s + 2), A(s + 1), T(s + 3),
     // A(s + 2)
-    vq::wait_vmcnt<3 * kADma + 2>();
-    read_words(std::integral_constant<int, (kSlot + 1) % kTileRing>{});  // (past the last step: unused)
+    vq::wait_vmcnt<3 * kAL + 2 * kTL>();
+    read_words(std::integral_constant<int, (kS + 1) % kTileRing>{});  // (past the last step: unused)
     // this step's slot (its words read and decoded a step ago) takes step s + 4
     load_trellis(min(s + 4, last));
 
     half8_t b_next[2][2];
-    const uint32_t a_buf = a_lane + uint32_t(s % kTileABufs) * (kBlocks * 1024);
-    half8_t ah[kRB];
-    tile_read16<0 * 1024>(ah[0], a_buf);
-    tile_read16<1 * 1024>(ah[1], a_buf);
+    const uint32_t a_buf = a_lane + uint32_t(s % kTileABufs) * (kParts * kBlocks * 1024);
+    half8_t ah[kRB], al[kRB];
+    auto read_a = [&](auto rb_tag) {
+      constexpr int rb = decltype(rb_tag)::value;
+      tile_read16<rb * 1024>(ah[rb], a_buf);
+      if constexpr (kLo) tile_read16<(kBlocks + rb) * 1024>(al[rb], a_buf);
+    };
+    read_a(std::integral_constant<int, 0>{});
+    read_a(std::integral_constant<int, 1>{});
     static_for<kRB>([&](auto rb_tag) {
       constexpr int rb = decltype(rb_tag)::value;
-      if constexpr (rb == 0) {
-        tile_wait<1>(ah[rb], words);  // (the words were read before ah[0])
-      } else if constexpr (rb + 1 < kRB) {
-        tile_wait<1>(ah[rb]);
-      } else {
-        tile_wait_last(ah[rb], words);
-      }
-      if constexpr (rb + 2 < kRB) tile_read16<(rb + 2) * 1024>(ah[rb + 2], a_buf);
+      // the reads of row block rb + 1 may still be pending (the words were
+      // read before row block 0's)
+      tile_lgkm<rb + 1 < kRB ? kParts : 0>();
+      tile_ready(ah[rb]);
+      if constexpr (kLo) tile_ready(al[rb]);
+      if constexpr (rb == 0) tile_ready(words);
+      if constexpr (rb + 2 < kRB) read_a(std::integral_constant<int, rb + 2>{});
       if constexpr (rb == 0) {
         decode_pair(words, 0, b_next);
         decode_pair(words, 1, b_next);
@@ -400,6 +421,13 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           acc[rb][p][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[rb], b_cur[p][j], acc[rb][p][j], 0, 0, 0);
+      if constexpr (kLo) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[rb][p][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[rb], b_cur[p][j], acc[rb][p][j], 0, 0, 0);
+      }
     });
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -408,7 +436,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     }
     // A(s + 1) of this wavefront landed: after it came T(s + 3), A(s + 2),
     // T(s + 4); then every wavefront's (and every read of buffer s) is done
-    vq::wait_vmcnt<kADma + 2>();
+    vq::wait_vmcnt<kAL + 2 * kTL>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
@@ -436,6 +464,13 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   // the clamped loads past the last step may still be landing in the LDS
   // the epilogue reuses
   vq::wait_vmcnt<0>();
+  __syncthreads();
+  int* row_id = reinterpret_cast<int*>(&t_lds[0][0][0]);
+  int* row_e = row_id + kRows;
+  if (tid < kRows) {
+    row_id[tid] = my_row;
+    row_e[tid] = my_e;
+  }
   __syncthreads();
   // Wavefront w finishes 128-column block blk = w & 1 of the tile: in each
   // row block, rows 8 (w >> 1) + 4 b + q (b = 0, 1), one per 16-lane row q
@@ -498,5 +533,22 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     __syncthreads();
   }
 }
+
+// The tile GEMM's instantiations are split over kTileParts separately
+// compiled objects (exl3_tile_part.hip): format i of VQ_EXL3_FORMATS lives
+// in part i % kTileParts, with its dense kernels (both precisions) and, for
+// mul1 rates, its MoE kernels.
+constexpr int kTileParts = 4;
+
+// Launches tile_gemm<bits_x2, codebook, moe, lo> for a format of part P
+// (a format of another part is refused).
+template <int P>
+int tile_launch_part(int64_t bits_x2, int64_t codebook, bool moe, bool lo, const TileArgs& a, dim3 grid,
+                     hipStream_t stream);
+
+// Launches tile_gemm<bits_x2, codebook, moe, lo> from the part that holds it
+// (exl3_gemm.hip).
+int launch_tile_gemm(int64_t bits_x2, int64_t codebook, bool moe, bool lo, const TileArgs& a, dim3 grid,
+                     hipStream_t stream);
 
 }  // namespace exl3

@@ -270,7 +270,22 @@ __global__ __launch_bounds__(kThreads, 2) void marlin_gemm(GemmArgs g) {
   if (g.sorted && int64_t(b) * g.bs >= int64_t(g.ntpp[0])) return;
   // (a vector load: the kernel writes memory the compiler cannot tell apart)
   const int e = vq::uniform(g.eids[b]);
-  if (e < 0 || e >= g.experts) return;
+  if (e < 0 || e >= g.experts) {
+    if constexpr (kMode == kTopkSum) {
+      // a token none of whose slots is routed has no arriving wavefront to
+      // write its sum: the block of its first slot writes the zero sum
+      const int topk = g.sum_topk;
+      const int t = b / topk;
+      if (b != t * topk || !tile_ok || wk != 0) return;
+      const int32_t* tok_ids = g.eids + int64_t(t) * topk;
+      for (int k = 0; k < topk; ++k) {
+        const int id = tok_ids[k];
+        if (id >= 0 && id < g.experts) return;
+      }
+      g.sum_out[int64_t(t) * g.N + 64 * tile + lane] = to_act<kBF16>(0.0f);
+    }
+    return;
+  }
   if (tid < kMaxBlock) {
     int slot = -1;
     if (!g.sorted) {

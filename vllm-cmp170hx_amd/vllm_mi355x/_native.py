@@ -58,6 +58,8 @@ SIGNATURES = {
     ]),
     "exl3_set_gemv_finish": (c_int, [c_int]),
     "exl3_set_moe_tile_rows": (c_int, [c_int]),
+    "exl3_set_tile_precision": (c_int, [c_int]),
+    "exl3_set_prefill_kernel": (c_int, [c_int]),
     "exl3_set_gemv_blocks": (c_int, [c_int]),
     "exl3_set_gemv_groups": (c_int, [c_int]),
     "exl3_moe_workspace_size": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64]),

@@ -78,7 +78,7 @@ SCHEMAS = {
 # moe_prefill_v2.cu:1162-1175, moe_prefill_try.cu:1381-1399,
 # moe_v2_try.cu:1542-1559): each is served by one of the operators above.
 _LINEAR_ALIASES = ("linear_out_prefill",)
-_MOE_ALIASES = ("moe_out_mixed", "moe_out_prefill")               # moe_out's signature
+_MOE_ALIASES = ("moe_out_mixed",)                                  # moe_out's signature
 _MOE_V2_ALIASES = ("moe_out_v2_fold", "moe_out_prefill_v2", "moe_out_prefill_try")
 _MOE_V2_MIXED = ("moe_out_v2_mixed", "moe_out_prefill_try_mixed")  # any format per expert
 _MOE_V2_TRY = ("moe_out_v2_try", "moe_out_v2_try_mixed")          # swiglu_limit required
@@ -92,7 +92,7 @@ def _alias_schema(base: str, name: str) -> str:
 
 for _n in _LINEAR_ALIASES:
     SCHEMAS[_n] = _alias_schema("linear_out", _n)
-for _n in _MOE_ALIASES:
+for _n in _MOE_ALIASES + ("moe_out_prefill",):
     SCHEMAS[_n] = _alias_schema("moe_out", _n)
 for _n in _MOE_V2_ALIASES + _MOE_V2_MIXED:
     SCHEMAS[_n] = _alias_schema("moe_out_v2", _n)
@@ -223,6 +223,22 @@ def moe_out_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map
               0, out, workspace, swiglu_limit)
 
 
+# The one rate every routed matrix of a moe_out_prefill call has: the
+# reference's operator is built for bits_x2 10 with codebook 2 alone
+# (csrc/exl3/moe_prefill.cu:37-40, :169-171).
+MOE_PREFILL_BITS_X2 = 10
+
+
+def moe_out_prefill_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
+                         intermediate_size, out, workspace, swiglu_limit=0.0) -> None:
+    """moe_out's schema at the reference's prefill operator's one rate: the
+    fixed-rate path (tile GEMM for the experts with many routed rows, at
+    any hidden / intermediate size); an expert of another format gets NaN
+    rows where the reference's kernel traps."""
+    _moe_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map, intermediate_size,
+              MOE_PREFILL_BITS_X2, out, workspace, swiglu_limit)
+
+
 def moe_out_v2_impl(x, topk_ids, topk_weights, packed_ptrs, packed_meta, expert_map,
                     intermediate_size, bits_x2, out, workspace, swiglu_limit=0.0) -> None:
     if int(bits_x2) <= 0:
@@ -351,6 +367,7 @@ def register() -> None:
         lib.impl(name, linear_out_impl, "CUDA")
     for name in _MOE_ALIASES:
         lib.impl(name, moe_out_impl, "CUDA")
+    lib.impl("moe_out_prefill", moe_out_prefill_impl, "CUDA")
     for name in _MOE_V2_ALIASES + _MOE_V2_TRY:
         lib.impl(name, moe_out_v2_impl, "CUDA")
     for name in _MOE_V2_MIXED:
