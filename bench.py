@@ -106,35 +106,42 @@ def _hip_graph_upload(torch, graph, stream) -> None:
 
 def time_steps_exact(torch, calls, warmup, steps, per_graph=120):
     """ms per call over exactly `steps` timed calls after exactly `warmup`
-    untimed ones: the warm-up calls run eagerly (they also make the
-    library's first launches), the timed calls as replays of a graph of
-    per_graph calls plus one graph of the remainder, uploaded first; HIP
-    events on the replay stream bracket the replays."""
-    for i in range(warmup):
-        calls(i)
+    untimed ones.  The first warm-up call runs eagerly (the library's first
+    launches), the others as one graph replayed right before the timed
+    region, so the GPU is still busy with them while the timed replays are
+    enqueued; the timed calls are replays of a graph of per_graph calls plus
+    one graph of the remainder, all graphs uploaded first; HIP events on the
+    replay stream bracket the timed replays."""
+    if warmup > 0:
+        calls(0)
     torch.cuda.synchronize()
     per_graph = max(1, min(per_graph, steps))
     full, rem = divmod(steps, per_graph)
     stream = torch.cuda.Stream()
-    graphs = []
-    for size, reps in ((per_graph, full), (rem, 1)):
-        if size == 0 or reps == 0:
-            continue
+
+    def capture(first, size):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
             with torch.cuda.graph(graph, stream=stream):
-                for i in range(size):
+                for i in range(first, first + size):
                     calls(i)
-        graphs.append((graph, reps))
+        return graph
+
+    warm = capture(1, warmup - 1) if warmup > 1 else None
+    timed = [(capture(warmup, per_graph), full)] if full else []
+    if rem:
+        timed.append((capture(warmup, rem), 1))
     torch.cuda.synchronize()
-    for graph, _ in graphs:
+    for graph in ([warm] if warm is not None else []) + [g for g, _ in timed]:
         _hip_graph_upload(torch, graph, stream)
     stream.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        if warm is not None:
+            warm.replay()
         start.record(stream)
-        for graph, reps in graphs:
+        for graph, reps in timed:
             for _ in range(reps):
                 graph.replay()
         end.record(stream)
