@@ -209,15 +209,24 @@ int exl3_set_prefill_kernel(int kernel);
  * Test and tuning switch, process-wide: how exl3_linear_out finishes its
  * small-M (<= 8 rows) launches.  -1 (default): the last workgroup of each
  * 128-column block sums the K-split partials and writes the outputs, using
- * arrival counters from a static pool of 128 ranges per device, one range
- * per (stream, graph capture) so launches that may overlap never share one
- * (once the ranges are spent, later streams and captures use the separate
- * kernel); 0: always a separate output kernel; 1: as -1.  Both finishes add
- * in the same order, so results are bitwise equal.
+ * arrival counters from a static pool of 128 ranges per device: one range
+ * per stream for its eager launches and one per stream for every graph
+ * captured on it (graphs captured on one stream must not be replayed
+ * concurrently with each other; once the ranges are spent, launches on
+ * further streams use the separate kernel, counted by
+ * exl3_counter_fallbacks); 0: always a separate output kernel; 1: as -1.
+ * Both finishes add in the same order, so results are bitwise equal.
  * No counterpart in the reference (its nearest is the test-only
  * set_gemm_shape_override, csrc/exl3/gemm.cu:400-409).
  */
 int exl3_set_gemv_finish(int mode);
+
+/*
+ * Launches since the library loaded that found no arrival-counter range
+ * and took the separate finish (a performance fallback, never a wrong
+ * result).  No counterpart in the reference.
+ */
+int64_t exl3_counter_fallbacks(void);
 
 /*
  * Test and tuning switch, process-wide: 128-input blocks per workgroup of

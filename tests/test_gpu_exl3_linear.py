@@ -467,3 +467,53 @@ def test_tile_fp16_precision_opt_in(ops, device, prefill_switches, bits_x2, code
     got = _out_np(_run_linear(ops, device, trellis, suh, svh, x, code, bits_x2, codebook, n,
                               torch.float32))
     _assert_fp32_close(got[sample], want, f"hi/lo bits_x2={bits_x2}")
+
+
+def _graph_nodes(graph) -> int:
+    import ctypes
+    lib = ctypes.CDLL("libamdhip64.so")
+    count = ctypes.c_size_t(0)
+    rc = lib.hipGraphGetNodes(ctypes.c_void_p(graph.raw_cuda_graph()), None, ctypes.byref(count))
+    assert rc == 0, f"hipGraphGetNodes failed ({rc})"
+    return count.value
+
+
+def test_many_captures_keep_the_fused_finish(ops, device):
+    """Every graph captured on one stream shares that stream's arrival-counter
+    range: after 220 captures the last graph still holds the one fused GEMV
+    launch (no separate output kernel), no launch fell back, and every graph
+    replays bitwise equal to the eager call."""
+    from vllm_mi355x import _native
+    print("220 graph captures on one stream", flush=True)
+    lib = _native.load()
+    k, n, bits_x2 = 1024, 2048, 8
+    rng = np.random.default_rng(220)
+    trellis, suh, svh = random_matrix(rng, k, n, bits_x2)
+    x, _ = random_acts(rng, 1, k, "fp16")
+    t, u, v = _dev(trellis, device), _dev(suh, device), _dev(svh, device)
+    xt = _dev(x, device)
+    out = torch.empty(1, n, dtype=torch.float32, device=device)
+    ws = torch.empty(ops.linear_workspace_size(1, k, n), dtype=torch.float32, device=device)
+    ops.linear_out(xt, t, u, v, bits_x2, 2, k, n, out, ws)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    before = lib.exl3_counter_fallbacks()
+    stream = torch.cuda.Stream()
+    graphs = []
+    for _ in range(220):
+        graph = torch.cuda.CUDAGraph(keep_graph=True)
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                ops.linear_out(xt, t, u, v, bits_x2, 2, k, n, out, ws)
+        graph.instantiate()
+        graphs.append(graph)
+    torch.cuda.synchronize()
+    assert lib.exl3_counter_fallbacks() == before
+    assert _graph_nodes(graphs[-1]) == 1 and _graph_nodes(graphs[0]) == 1
+    for graph in (graphs[0], graphs[-1], graphs[107]):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    del graphs

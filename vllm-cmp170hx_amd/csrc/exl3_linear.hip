@@ -24,6 +24,8 @@ namespace exl3 {
 
 // The arrival-counter pool of the fused finish (see exl3_gemv.h).
 __device__ uint32_t g_gemv_counters[kCounterRanges * kCounterSlots * kCounterStride];
+// Launches that found no counter range (they used the separate finish).
+std::atomic<long long> g_counter_fallbacks{0};
 
 namespace {
 
@@ -85,19 +87,27 @@ int check_padded(int64_t n) {
 // Arrival counters of a fused-finish launch over `blocks` column blocks:
 // the pool's device address and the launch's first slot, or a null pool (the
 // launch then uses the separate output kernel).  One range of kCounterSlots
-// slots per (device, stream, graph capture): eager launches on one stream run
-// in order and share its range; the launches recorded on one stream of one
-// capture form a chain in the graph and share that capture's range; two
-// graphs (or a graph and eager work) never share one, so graphs replayed
-// concurrently on different streams cannot collide.  Ranges are kept for the
-// life of the process (a graph may be replayed at any time).
+// slots per (device, stream) for eager launches and one per (device, stream)
+// for the launches recorded while that stream captures a graph: eager
+// launches on one stream run in order and share its range; every graph
+// captured on one stream shares that stream's capture range, so replays of
+// such graphs must not overlap each other (replays on one stream, the way
+// graphs are replayed, never do); a graph never shares a range with eager
+// work, so a graph replayed on another stream while its capture stream runs
+// eager launches cannot collide with them.  Ranges are kept for the life of
+// the process (a graph may be replayed at any time); any number of captures
+// reuse their stream's range.  Fallbacks (more streams than ranges) are
+// counted (exl3_counter_fallbacks).
 CounterSlots counter_slots(hipStream_t stream, int64_t blocks) {
   static std::mutex mutex;
-  static std::map<std::tuple<int, hipStream_t, bool, unsigned long long>, int> ranges;
+  static std::map<std::tuple<int, hipStream_t, bool>, int> ranges;
   static std::map<int, int> used;
   static std::map<int, uint32_t*> pools;
   const CounterSlots none{nullptr, -1};
-  if (blocks > kCounterSlots) return none;
+  if (blocks > kCounterSlots) {
+    g_counter_fallbacks.fetch_add(1);
+    return none;
+  }
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) {
     (void)hipGetLastError();
@@ -110,7 +120,6 @@ CounterSlots counter_slots(hipStream_t stream, int64_t blocks) {
     return none;
   }
   const bool capturing = status != hipStreamCaptureStatusNone;
-  if (!capturing) capture = 0;
   std::lock_guard<std::mutex> lock(mutex);
   uint32_t*& pool = pools[device];
   if (!pool) {
@@ -122,11 +131,14 @@ CounterSlots counter_slots(hipStream_t stream, int64_t blocks) {
     }
     pool = static_cast<uint32_t*>(address);
   }
-  const auto key = std::make_tuple(device, stream, capturing, capture);
+  const auto key = std::make_tuple(device, stream, capturing);
   const auto it = ranges.find(key);
   if (it != ranges.end()) return {pool, it->second};
   int& n = used[device];
-  if (n >= kCounterRanges) return none;
+  if (n >= kCounterRanges) {
+    g_counter_fallbacks.fetch_add(1);
+    return none;
+  }
   const int base = n++ * kCounterSlots;
   ranges[key] = base;
   return {pool, base};
@@ -490,3 +502,5 @@ extern "C" int exl3_set_gemv_finish(int mode) {
   exl3::g_finish_mode.store(mode);
   return vq::kOk;
 }
+
+extern "C" int64_t exl3_counter_fallbacks(void) { return exl3::g_counter_fallbacks.load(); }

@@ -56,10 +56,10 @@ constexpr int64_t kMaxRouteExperts = 4096;
 constexpr int kTaskRows = 32;
 constexpr int task_rows(int bits_x2) { return bits_x2 > 0 ? kTaskRows : 8; }
 // The rate of the fixed-rate GEMV serving a call's bits_x2 (moe_out_v2's
-// 2..8, decoded by specialized kernels), or 0: the run-time-format decode,
-// which serves moe_out (any admitted format per expert) and moe_out_v2 at
-// 10..16 (checked per expert against the layer's rate).
-constexpr int fixed_rate(int64_t bits_x2) { return bits_x2 >= 2 && bits_x2 <= 8 ? int(bits_x2) : 0; }
+// mul1 rates 2..16 and moe_out_prefill's 10, decoded by specialized
+// kernels), or 0: the run-time-format decode, which serves moe_out (any
+// admitted format per expert).
+constexpr int fixed_rate(int64_t bits_x2) { return bits_x2 >= 2 && bits_x2 <= 16 ? int(bits_x2) : 0; }
 
 // Routing of one call (reference: csrc/exl3/moe.cu:19-55).
 struct Routing {
@@ -527,7 +527,7 @@ __device__ __forceinline__ void progress_priority(int step, int steps) {
 // want_bits (run-time decode only): the layer's mul1 rate every expert must
 // have (moe_out_v2 above 4 bits), or 0 for any admitted format (moe_out).
 template <int kBitsX2>
-__global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing routing, int projection, int64_t kp,
+__global__ __launch_bounds__(256, kBitsX2 > 8 ? 3 : (kBitsX2 > 0 ? 4 : 2)) void moe_gemv(Routing routing, int projection, int64_t kp,
                                                 int64_t np, const int* table, float* ws,
                                                 MoeLayout lay, int64_t in_offset,
                                                 int64_t out_offset, int want_bits) {
@@ -639,9 +639,13 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
     rexp[tid] = exps[int64_t(sorted[first + min(tid, nrows - 1)]) * (lay.kmax() / 128)];
   }
 
-  // trellis ring (fixed rate: one coalesced dword per lane per tile row, words
-  // gathered with ds_bpermute; run-time rate: decoded from the tile directly)
+  // trellis ring (fixed rate up to 4 bits per weight: one coalesced dword
+  // per lane per tile row, words gathered with ds_bpermute; wider fixed
+  // rates: each lane loads its own window words; run-time rate: decoded
+  // from the tile directly)
+  constexpr bool kGather = kFixed && kBitsX2 <= 8;
   constexpr int kWords = LaneLoad<kFixed ? kBitsX2 : 8>::kWords;
+  constexpr int kRaw = kGather ? 1 : kWords;
   const int raw_off = lane < 8 * bits_x2 ? 4 * lane : 0;
   int widx[kWords];
   lane_word_index<kFixed ? kBitsX2 : 8>(L, widx);
@@ -654,20 +658,31 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
   // trellis loads in flight, as flat loads would make them.
   const __amdgpu_buffer_rsrc_t tr_buf = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(chunk), 0, int((steps * 2 - 1) * row_bytes + 2 * tile_bytes), 0x00020000);
-  uint32_t raw[kDepth][2];
+  uint32_t raw[kDepth][2][kRaw];
   // (the alignment is a compile-time branch of the stream below: with a
   // run-time branch in the loop the compiler, unsure of the loads in flight
   // where the paths meet, waits for all of them before each use)
+  auto load_word = [&](auto aligned_tag, int offset, int row) -> uint32_t {
+    if constexpr (decltype(aligned_tag)::value) {
+      return __builtin_amdgcn_raw_buffer_load_b32(tr_buf, offset, row, 0);
+    } else {
+      return uint32_t(__builtin_amdgcn_raw_buffer_load_b16(tr_buf, offset, row, 0)) |
+             (uint32_t(__builtin_amdgcn_raw_buffer_load_b16(tr_buf, offset + 2, row, 0)) << 16);
+    }
+  };
   auto load_step = [&](auto aligned_tag, int slot, int s) {
     if constexpr (kFixed) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int row = int((2 * s + h) * row_bytes);
-        if constexpr (decltype(aligned_tag)::value) {
-          raw[slot][h] = __builtin_amdgcn_raw_buffer_load_b32(tr_buf, raw_off, row, 0);
+        if constexpr (kGather) {
+          raw[slot][h][0] = load_word(aligned_tag, raw_off, row);
         } else {
-          raw[slot][h] = uint32_t(__builtin_amdgcn_raw_buffer_load_b16(tr_buf, raw_off, row, 0)) |
-                         (uint32_t(__builtin_amdgcn_raw_buffer_load_b16(tr_buf, raw_off + 2, row, 0)) << 16);
+#pragma unroll
+          for (int k = 0; k < kRaw; ++k) {
+            const int offset = (m >> 3) * tile_bytes + 4 * widx[k];
+            raw[slot][h][k] = load_word(aligned_tag, offset, row);
+          }
         }
       }
     }
@@ -708,8 +723,13 @@ __global__ __launch_bounds__(256, kBitsX2 > 0 ? 4 : 2) void moe_gemv(Routing rou
             uint32_t w0[kWords], w1[kWords];
   #pragma unroll
             for (int k = 0; k < kWords; ++k) {
-              w0[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][0])));
-              w1[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][1])));
+              if constexpr (kGather) {
+                w0[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][0][0])));
+                w1[k] = uint32_t(__builtin_amdgcn_ds_bpermute(src[k], int(raw[i][1][0])));
+              } else {
+                w0[k] = raw[i][0][k];
+                w1[k] = raw[i][1][k];
+              }
             }
             load_step(aligned_tag, i, min(s + kDepth, steps - 1));
             decode_words<kBitsX2, 2>(L, w0, q0);
@@ -998,6 +1018,7 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       switch (fixed) {
 #define VQ_MOE(B) case B: hipLaunchKernelGGL(exl3::moe_gemv<B>, grid, dim3(256), 0, s, routing, projection, kp, np, table, workspace, lay, in_off, out_off, 0); break;
         VQ_MOE(2) VQ_MOE(3) VQ_MOE(4) VQ_MOE(5) VQ_MOE(6) VQ_MOE(7) VQ_MOE(8)
+        VQ_MOE(10) VQ_MOE(12) VQ_MOE(14) VQ_MOE(16)
 #undef VQ_MOE
         default:
           hipLaunchKernelGGL(exl3::moe_gemv<0>, grid, dim3(256), 0, s, routing, projection, kp, np,

@@ -57,6 +57,7 @@ SIGNATURES = {
         c_vp, c_vp,                           # out, stream
     ]),
     "exl3_set_gemv_finish": (c_int, [c_int]),
+    "exl3_counter_fallbacks": (c_i64, []),
     "exl3_set_moe_tile_rows": (c_int, [c_int]),
     "exl3_set_tile_precision": (c_int, [c_int]),
     "exl3_set_prefill_kernel": (c_int, [c_int]),
