@@ -381,28 +381,26 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
   //    unconditional, at a clamped (always valid) index, and the value is
   //    selected afterwards: loads under a branch would each wait for their
   //    data before the branch closes.
+  //    Buffer loads: 32-bit offsets, and a load past the resource's end (an
+  //    input at or past logical_in) returns zero, the reference's padding.
+  //    A wavefront's forming tasks lie in one row of x (kRows divides by
+  //    the four wavefronts' task stride, or a task's row is wc % kRows).
   const uint16_t* xs = static_cast<const uint16_t*>(a.x);
+  const __amdgpu_buffer_rsrc_t suh_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.suh), 0, int(2 * a.logical_in), 0x00020000);
   uint32_t xv[kFormTasks][2], sv[kFormTasks][2];
 #pragma unroll
   for (int f = 0; f < kFormTasks; ++f) {
     const int t = wc + 4 * f;
     const int b = min(t / kRows, kBlocks - 1);
-    const int64_t row = int64_t(min(t % kRows, a.rows - 1)) * a.logical_in;
-    const int64_t k_0 = k0 + 128 * b + lane;
-    const int64_t k_1 = k_0 + 64;
-    const int64_t c0 = k_0 < a.logical_in ? k_0 : 0;
-    const int64_t c1 = k_1 < a.logical_in ? k_1 : 0;
-    sv[f][0] = a.suh[c0];
-    sv[f][1] = a.suh[c1];
-    xv[f][0] = xs[row + c0];
-    xv[f][1] = xs[row + c1];
-  }
-#pragma unroll
-  for (int f = 0; f < kFormTasks; ++f) {
-    const int b = min((wc + 4 * f) / kRows, kBlocks - 1);
-    const int64_t k_0 = k0 + 128 * b + lane;
-    if (!(k_0 < a.logical_in)) { sv[f][0] = 0u; xv[f][0] = 0u; }
-    if (!(k_0 + 64 < a.logical_in)) { sv[f][1] = 0u; xv[f][1] = 0u; }
+    const int row = vq::uniform(min(t % kRows, a.rows - 1));
+    const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(xs + int64_t(row) * a.logical_in), 0, int(2 * a.logical_in), 0x00020000);
+    const int k_0 = int(k0) + 128 * b + lane;
+    sv[f][0] = __builtin_amdgcn_raw_buffer_load_b16(suh_rsrc, 2 * k_0, 0, 0);
+    sv[f][1] = __builtin_amdgcn_raw_buffer_load_b16(suh_rsrc, 2 * k_0 + 128, 0, 0);
+    xv[f][0] = __builtin_amdgcn_raw_buffer_load_b16(x_rsrc, 2 * k_0, 0, 0);
+    xv[f][1] = __builtin_amdgcn_raw_buffer_load_b16(x_rsrc, 2 * k_0 + 128, 0, 0);
   }
 
   // b. the first trellis loads.  The wavefront's chunk of tile row 0 is the

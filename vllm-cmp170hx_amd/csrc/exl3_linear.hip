@@ -76,7 +76,8 @@ int dispatch(int64_t bits_x2, int64_t codebook, bool aligned, int load, const Ge
 }
 
 int check_padded(int64_t n) {
-  if (n <= 0 || n % 128 != 0 || n > INT_MAX) {
+  // (the kernels address a row of x, suh or svh in bytes with 32-bit offsets)
+  if (n <= 0 || n % 128 != 0 || n > INT_MAX / 4) {
     return vq::fail("EXL3 padded dimensions must be positive H128 multiples fitting int32");
   }
   return vq::kOk;

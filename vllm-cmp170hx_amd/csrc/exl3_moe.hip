@@ -48,6 +48,7 @@ namespace exl3 {
 namespace {
 
 constexpr int kRouteThreads = 1024;
+constexpr int kRouteBatch = 8;  // assignments a route thread loads at a time
 constexpr int64_t kMaxRouteExperts = 4096;
 // Rows of one expert per GEMV task: every decoded weight operand feeds the
 // MFMAs of up to four 8-row sub-blocks, so a fixed-rate expert's weights
@@ -157,10 +158,32 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
   for (int e = tid; e < experts; e += kRouteThreads) count[e] = 0;
   if (tid == 0) tiles_in_all = 0;
   __syncthreads();
-  for (int64_t a = tid; a < assignments; a += kRouteThreads) {
-    const int64_t e = local_expert(routing, a);
-    if (e >= 0) atomicAdd(&count[e], 1);
-  }
+  // f(a, e) for every assignment a with local expert e >= 0: kRouteBatch
+  // assignments a thread at a time, their id loads issued together, then
+  // their expert-map loads together (one pair of memory round trips per
+  // batch instead of per assignment)
+  auto for_routed = [&](auto&& f) {
+    for (int64_t a0 = tid; a0 < assignments; a0 += int64_t(kRouteThreads) * kRouteBatch) {
+      int64_t g[kRouteBatch];
+#pragma unroll
+      for (int u = 0; u < kRouteBatch; ++u) {
+        const int64_t a = a0 + int64_t(u) * kRouteThreads;
+        g[u] = a < assignments ? integer_at(routing.ids, routing.ids64, a) : -1;
+      }
+      int64_t e[kRouteBatch];
+#pragma unroll
+      for (int u = 0; u < kRouteBatch; ++u) {
+        const bool in = g[u] >= 0 && g[u] < routing.global_experts;
+        const int64_t l = in ? integer_at(routing.expert_map, routing.map64, g[u]) : -1;
+        e[u] = l >= 0 && l < routing.local_experts ? l : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < kRouteBatch; ++u) {
+        if (e[u] >= 0) f(a0 + int64_t(u) * kRouteThreads, int(e[u]));
+      }
+    }
+  };
+  for_routed([&](int64_t, int e) { atomicAdd(&count[e], 1); });
   __syncthreads();
   // each thread a contiguous run of experts
   const int per = (experts + kRouteThreads - 1) / kRouteThreads;
@@ -264,10 +287,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
   for (int e = e0; e < e1; ++e) count[e] = row_begin[e];  // fill cursors
   __syncthreads();
   int* sorted = table + 4;
-  for (int64_t a = tid; a < assignments; a += kRouteThreads) {
-    const int64_t e = local_expert(routing, a);
-    if (e >= 0) sorted[atomicAdd(&count[e], 1)] = int(a);
-  }
+  for_routed([&](int64_t a, int e) { sorted[atomicAdd(&count[e], 1)] = int(a); });
 }
 
 // ---- 2/3. activations in B-operand form ----------------------------------------
