@@ -218,9 +218,9 @@ __device__ __forceinline__ void finish_row_block(const float* __restrict__ parti
 }
 
 // Fused finish of one 128-column block by the first 256 threads of the
-// workgroup (the others only pass its barrier): thread t sums column t & 127
-// over the splits of parity t >> 7 (agent-scope loads, eight in flight, split
-// order), the two parity sums are added (even + odd) through LDS, then
+// workgroup (the others only pass its barrier): each column is summed over
+// the even splits and over the odd splits, each in split order (agent-scope
+// loads), the two parity sums are added (even + odd) through LDS, then
 // wavefront w applies H128 and svh to rows w, w + 4.
 __device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int tid, int cblk) {
   const int col = tid & 127;
@@ -233,7 +233,32 @@ __device__ __forceinline__ void finish_block(const GemvArgs& a, float* red, int 
   const int stride_bytes = 4 * a.rows * int(a.np);
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       a.partial + base, 0, (a.splits - 1) * stride_bytes + 4 * ((a.rows - 1) * int(a.np) + 128), 0x00020000);
-  if (a.splits <= 32 && tid < 256) {
+  if (a.splits <= 16 && tid < 256) {
+    // thread = (4 columns, split parity, row group): one 16-byte load per
+    // split of its parity (index clamped to a valid split, the extra terms
+    // not added), all in flight together: one memory round trip per row of
+    // its group (rows rg, rg + 4)
+    const int cq = tid & 31;
+    const int par = (tid >> 5) & 1;  // differs inside a wavefront: offsets in VGPRs
+    for (int r = tid >> 6; r < a.rows; r += 4) {
+      f32x4_t t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int split_off = min(par + 2 * u, a.splits - 1) * stride_bytes;
+        t[u] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rsrc, split_off + 4 * (r * int(a.np) + 4 * cq), 0, kCachePolicySc1));
+      }
+      // (float vectors throughout: this compiler's __builtin_bit_cast of a
+      // vector element reads element 0 whatever the index)
+      f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (par + 2 * u < a.splits) v += t[u];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[(par * a.rows + r) * 128 + 4 * cq + c] = v[c];
+    }
+  } else if (a.splits <= 32 && tid < 256) {
     // one round of 16 loads per row (the split index clamped to a valid one,
     // the extra terms not added), the next row's loads issued before this
     // row's sum: rows one memory round trip apart in the pipeline, not one
