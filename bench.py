@@ -2,7 +2,7 @@
 """Benchmark of the quantized-weight matmul hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
-                    [--no-extras] [--only prefill|exl3_moe|marlin]
+                    [--no-extras] [--only prefill|exl3_moe|marlin|moe_prefill] [--copy-mb MB]
 
 Headline workload (one "step"): one EXL3 dense linear at the decode-GEMV
 shape, a 4096 x 14336 matrix at 4 bits per weight (bits_x2 8, mul1
@@ -38,6 +38,12 @@ The same line also carries:
              7168, intermediate 2048, top-8 from Zipf(1.1)-skewed logits)
              at 64 decode tokens (and 2048 prefill tokens): tokens/s and
              HBM GB/s;
+  exl3_moe_prefill  moe_out_prefill's served configuration (256 experts,
+             hidden 2560, intermediate 640, bits_x2 10, top-10, bf16) at
+             2048 tokens (and 65, 512, 3460), beside the run-time-format
+             moe_out on the same call;
+  (the many-row EXL3 lines at the default FP16 high + low activation
+  parts, and again with the FP16-only opt-in)
 and the CPU baselines: the reference's CPU dequantize-then-matmul paths
 (oracle/exl3_torch_ref.py, oracle/marlin_torch_ref.py) on this host's
 cores, each on a bounded sample of its workload.
