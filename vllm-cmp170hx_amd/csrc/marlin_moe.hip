@@ -636,16 +636,18 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // up tiles), so the GPU holds every workgroup of a 256-token w13 at once
 // and its VALU dequant spreads over more wavefronts; three half-groups
 // ahead.  The other modes: two tiles per wavefront (each B operand feeds
-// both), one half-group ahead.
-template <int kMode>
+// both) for blocks of more than 16 tokens, one tile for blocks of up to 16
+// (the few-token forwards, whose few routed blocks then give twice the
+// wavefronts streaming weights); one half-group ahead.
+template <int kMode, int kSub>
 struct DirectShape {
-  static constexpr int kTiles = kMode == kSwiglu ? 1 : 2;
+  static constexpr int kTiles = kMode == kSwiglu || kSub == 1 ? 1 : 2;
   static constexpr int kSlots = 2;
   // kSwiglu: the B operands go through LDS too (all four wavefronts read the
   // same rows): two group slots
   static constexpr bool kLdsB = kMode == kSwiglu;
 };
-inline int direct_tiles(int mode) { return mode == kSwiglu ? DirectShape<kSwiglu>::kTiles : DirectShape<kTopk>::kTiles; }
+inline int direct_tiles(int mode, int sub) { return mode == kSwiglu || sub == 1 ? 1 : 2; }
 // The kernel's per-tile arrays have this fixed size (loops run to the mode's
 // tile count): arrays whose size depends on the template arguments, captured
 // by the kernel's lambdas, make the host compilation drop the kernel's launch
@@ -653,8 +655,8 @@ inline int direct_tiles(int mode) { return mode == kSwiglu ? DirectShape<kSwiglu
 constexpr int kMaxDirectTiles = 2;
 template <bool kBF16, int kSub, int kMode>
 __global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direct(GemmArgs g) {
-  constexpr int kDirectTiles = DirectShape<kMode>::kTiles;
-  constexpr int kSlots = DirectShape<kMode>::kSlots;
+  constexpr int kDirectTiles = DirectShape<kMode, kSub>::kTiles;
+  constexpr int kSlots = DirectShape<kMode, kSub>::kSlots;
   // ring slot = [wavefront][tile][step of the half-group][64 lanes] x 16 bytes
   constexpr int kSlotVecs = 4 * kDirectTiles * 2 * 64;
   __shared__ __attribute__((aligned(16))) u32x4_t ring0[kSlotVecs];
@@ -665,7 +667,7 @@ __global__ __launch_bounds__(kThreads, kSub <= 2 ? 3 : 2) void marlin_gemm_direc
   // group (128 k) of the block's rows (the chunk swizzle keeps the 16 rows a
   // B-operand read touches on distinct banks), then per wavefront 256 bytes:
   // its tile's group scales (128 bytes) and zeros
-  constexpr bool kLdsB = DirectShape<kMode>::kLdsB;
+  constexpr bool kLdsB = DirectShape<kMode, kSub>::kLdsB;
   constexpr int kBRowVecs = kSub * 16 * 16;
   constexpr int kBVecs = kLdsB ? kBRowVecs + 4 * 16 : 4;
   __shared__ __attribute__((aligned(16))) u32x4_t bring0[kBVecs];
@@ -1632,9 +1634,9 @@ int launch_gemm(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t
 
 template <bool kBF16, int kSub>
 int launch_direct(const GemmArgs& g, int mode, int blocks, int ksplit, hipStream_t s) {
-  // 4 direct_tiles(mode) tiles per workgroup (kSwiglu: half of them gate
-  // tiles, half the matching up tiles)
-  const int per = 4 * direct_tiles(mode);
+  // 4 direct_tiles(mode, kSub) tiles per workgroup (kSwiglu: half of them
+  // gate tiles, half the matching up tiles)
+  const int per = 4 * direct_tiles(mode, kSub);
   const unsigned gx = unsigned((g.N / 64 + per - 1) / per);
   const dim3 grid(gx, unsigned(blocks), unsigned(ksplit));
   switch (mode) {
