@@ -114,7 +114,8 @@ def test_dequant_bit_exact(mm, device, dtype, K, N):
 
 @pytest.mark.parametrize("T,E,topk,bs", [(1, 8, 2, 8), (5, 16, 4, 16), (64, 128, 8, 8),
                                          (300, 128, 8, 64), (3, 288, 8, 48), (2000, 64, 6, 32),
-                                         (0, 8, 2, 8), (1024, 128, 8, 64), (1025, 128, 8, 64)])
+                                         (0, 8, 2, 8), (1024, 128, 8, 64), (1025, 128, 8, 64),
+                                         (256, 128, 8, 32), (1000, 64, 8, 16), (700, 400, 2, 8)])
 def test_align_matches_oracle(mm, device, T, E, topk, bs):
     print(f"align T={T} E={E} topk={topk} bs={bs}", flush=True)
     rng = np.random.default_rng(T + E)

@@ -1279,16 +1279,115 @@ __device__ __forceinline__ void rank_rows(const int32_t* ids, int64_t numel, int
   }
 }
 
+// Rows a thread holds in registers on the one-pass alignment.
+constexpr int kAlignChunks = 8;
+
+// The alignment of up to kAlignChunks x 1024 rows and 1024 experts in one
+// pass (align mode 2): every row's expert loaded at once (row c * 1024 +
+// tid in register c), each wavefront's rows ranked per expert with ballots
+// and counted per (round c, wavefront, expert) in LDS; one thread per
+// expert turns its counts into exclusive prefixes in (round, wavefront)
+// order, its total and padded size; one scan gives the padded starts.  A
+// row then lands at start + prefix + rank: ascending flat order inside each
+// expert, as the rounds below produce.  Five barriers, one round of loads.
+__device__ __forceinline__ void align_block_onepass(
+    const int32_t* ids, int64_t numel, int experts, int bs, const int32_t* expert_map,
+    int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp) {
+  extern __shared__ int align_shared[];
+  int* start = align_shared;       // experts: padded exclusive starts
+  int* count = start + experts;    // experts: routed rows
+  int* wcnt = count + experts;     // [rounds][16][experts]: counts, then prefixes
+  __shared__ int wave_tot[kAlignThreads / 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int rounds = int((numel + kAlignThreads - 1) / kAlignThreads);
+  int e[kAlignChunks];
+#pragma unroll
+  for (int c = 0; c < kAlignChunks; ++c) {
+    const int64_t i = int64_t(c) * kAlignThreads + tid;
+    e[c] = c < rounds && i < numel ? routed_expert(ids, expert_map, i, experts) : -1;
+  }
+  for (int x = tid; x < rounds * 16 * experts; x += kAlignThreads) wcnt[x] = 0;
+  __syncthreads();
+  const int id_bits = experts > 1 ? 32 - __builtin_clz(unsigned(experts - 1)) : 1;
+  int rank[kAlignChunks];
+#pragma unroll
+  for (int c = 0; c < kAlignChunks; ++c) {
+    rank[c] = 0;
+    if (c < rounds) {
+      // lanes of this wavefront routed to the same expert: one ballot per
+      // bit of the expert id
+      uint64_t same = __ballot(e[c] >= 0);
+      for (int bit = 0; bit < id_bits; ++bit) {
+        const bool set = (e[c] >> bit) & 1;
+        const uint64_t m = __ballot(set);
+        same &= set ? m : ~m;
+      }
+      rank[c] = __builtin_popcountll(same & ((uint64_t(1) << lane) - 1));
+      if (e[c] >= 0 && rank[c] == 0) wcnt[(c * 16 + wave) * experts + e[c]] = __builtin_popcountll(same);
+    }
+  }
+  __syncthreads();
+  int run = 0;  // this thread's expert's padded size
+  if (tid < experts) {
+    int acc = 0;
+    for (int k = 0; k < rounds * 16; ++k) {
+      const int t = wcnt[k * experts + tid];
+      wcnt[k * experts + tid] = acc;
+      acc += t;
+    }
+    count[tid] = acc;
+    run = (acc + bs - 1) / bs * bs;
+  }
+  const int incl = block_inclusive_scan(run, wave_tot);
+  if (tid < experts) start[tid] = incl - run;
+  if (tid == kAlignThreads - 1) wave_tot[0] = incl;  // the padded total
+  __syncthreads();
+  const int total = wave_tot[0];
+  if (tid == 0) ntpp[0] = total;
+#pragma unroll
+  for (int c = 0; c < kAlignChunks; ++c) {
+    if (c < rounds && e[c] >= 0) {
+      const int64_t dest = int64_t(start[e[c]]) + wcnt[(c * 16 + wave) * experts + e[c]] + rank[c];
+      if (dest < sorted_size) sorted[dest] = c * kAlignThreads + tid;
+    }
+  }
+  // the sentinel in each expert's padding and past the padded total
+  if (tid < experts) {
+    const int64_t p1 = min(int64_t(start[tid]) + (count[tid] + bs - 1) / bs * bs, sorted_size);
+    for (int64_t p = int64_t(start[tid]) + count[tid]; p < p1; ++p) sorted[p] = int32_t(numel);
+  }
+  for (int64_t p = total + tid; p < sorted_size; p += kAlignThreads) sorted[p] = int32_t(numel);
+  for (int64_t b = tid; b < blocks; b += kAlignThreads) {
+    int owner = -1;
+    if (b < total / bs) {
+      // last expert whose first block is at or before b
+      int lo = 0, hi = experts;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (start[mid] / bs <= b) lo = mid; else hi = mid;
+      }
+      owner = lo;
+    }
+    eids[b] = owner;
+  }
+}
+
 // One workgroup: counts, padded exclusive scan, expert per block, then the
 // routed rows placed in ascending flat order inside each expert: rounds of
 // 1024 rows; each wavefront ranks its rows per expert with ballots, and a row
 // lands after its expert's rows of earlier rounds and earlier wavefronts
 // (per-wavefront counts in LDS when 16 x experts fit, else the 16 wavefronts
-// take turns at the per-expert cursors).
+// take turns at the per-expert cursors).  Mode 2: align_block_onepass.
 __device__ __forceinline__ void align_block(
     const int32_t* ids, int64_t numel, int experts, int bs, const int32_t* expert_map,
     int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp,
     int wave_counts) {
+  if (wave_counts == 2) {
+    align_block_onepass(ids, numel, experts, bs, expert_map, sorted, sorted_size, eids, blocks, ntpp);
+    return;
+  }
   extern __shared__ int align_shared[];
   int* count = align_shared;          // experts: counts, then cursors
   int* start = count + experts;       // experts: padded exclusive starts
@@ -2050,7 +2149,16 @@ int align_checks(int64_t numel, int64_t num_experts, int64_t block_size, int64_t
   const int64_t need = numel < num_experts ? std::min(numel * block_size, worst) : worst;
   if (sorted_numel < need) return fail("align: sorted_token_ids is smaller than numel + E (bs - 1)");
   if (expert_ids_numel * block_size < need) return fail("align: expert_ids too small");
-  // per-wavefront counts when they fit in 64 KB of LDS with the rest
+  // one pass (mode 2) when every row fits the registers and the per-round
+  // counts fit 64 KB of LDS; else per-wavefront counts when they fit, with
+  // the rest; else turns at the cursors
+  const int64_t rounds = std::max<int64_t>(1, (numel + kAlignThreads - 1) / kAlignThreads);
+  if (rounds <= kAlignChunks && num_experts <= kAlignThreads &&
+      (2 + 16 * rounds) * num_experts * int64_t(sizeof(int)) <= 65536) {
+    wave_counts = 2;
+    lds = size_t(2 + 16 * rounds) * size_t(num_experts) * sizeof(int);
+    return vq::kOk;
+  }
   wave_counts = num_experts <= 960 ? 1 : 0;
   lds = size_t(2 + (wave_counts ? 16 : 0)) * size_t(num_experts) * sizeof(int);
   return vq::kOk;
