@@ -215,7 +215,7 @@ def gpu_gemv(args, torch, inputs):
     ms = time_steps_exact(torch, call, args.warmup, args.steps, GRAPH_CALLS)
     # the same calls in a long loop (informational: replays of 120-call
     # graphs after 12000 untimed calls, the GPU's steady state)
-    steady, _, _ = time_graph(torch, call, GRAPH_CALLS, 12000, 2400)
+    steady = None if args.no_steady else time_graph(torch, call, GRAPH_CALLS, 12000, 2400)[0]
     del mats
     return ms, args.steps, args.warmup, steady
 
@@ -668,6 +668,9 @@ def main() -> int:
     parser.add_argument("--only", choices=("prefill", "exl3_moe", "marlin", "moe_prefill"), default=None,
                         help="profiling runs: only this workload, its JSON on one line (not the "
                              "benchmark line)")
+    parser.add_argument("--no-steady", action="store_true",
+                        help="counter runs: leave out the steady-state loop (14,400 more calls) "
+                             "beside the timed steps")
     parser.add_argument("--copy-mb", type=int, default=0,
                         help="also run 10 plain device copies of this many MiB (the counter "
                              "calibration of FETCH_SIZE / WRITE_SIZE)")
@@ -746,7 +749,7 @@ def main() -> int:
             "k": K_IN, "n": N_OUT, "bits_per_weight": BITS_X2 / 2, "codebook": "mul1",
             "rows": ROWS, "weight_copies": COPIES, "bytes_per_step": nbytes,
         },
-        "steady_state": {
+        "steady_state": None if steady_ms is None else {
             "note": "the same step in a long loop: 2400 timed calls after 12000 untimed ones",
             "us_per_step": round(steady_ms * 1e3, 3),
             "gbs": round(nbytes / (steady_ms * 1e-3) / 1e9, 2),

@@ -2149,11 +2149,12 @@ int align_checks(int64_t numel, int64_t num_experts, int64_t block_size, int64_t
   const int64_t need = numel < num_experts ? std::min(numel * block_size, worst) : worst;
   if (sorted_numel < need) return fail("align: sorted_token_ids is smaller than numel + E (bs - 1)");
   if (expert_ids_numel * block_size < need) return fail("align: expert_ids too small");
-  // one pass (mode 2) when every row fits the registers and the per-round
-  // counts fit 64 KB of LDS; else per-wavefront counts when they fit, with
-  // the rest; else turns at the cursors
-  const int64_t rounds = std::max<int64_t>(1, (numel + kAlignThreads - 1) / kAlignThreads);
-  if (rounds <= kAlignChunks && num_experts <= kAlignThreads &&
+  // one pass (mode 2) over 2-8 rounds of rows when every row fits the
+  // registers and the per-round counts fit 64 KB of LDS (one round: the
+  // rounds below measured as fast); else per-wavefront counts when they
+  // fit, with the rest; else turns at the cursors
+  const int64_t rounds = (numel + kAlignThreads - 1) / kAlignThreads;
+  if (rounds >= 2 && rounds <= kAlignChunks && num_experts <= kAlignThreads &&
       (2 + 16 * rounds) * num_experts * int64_t(sizeof(int)) <= 65536) {
     wave_counts = 2;
     lds = size_t(2 + 16 * rounds) * size_t(num_experts) * sizeof(int);
