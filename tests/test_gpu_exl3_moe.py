@@ -398,11 +398,13 @@ def tile_fp16():
 
 
 @pytest.mark.parametrize("bits_x2", [2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16])
-@pytest.mark.parametrize("rows,dtype", [(5, "bf16"), (40, "fp16")])
+@pytest.mark.parametrize("rows,dtype", [(5, "bf16"), (40, "fp16"), (96, "bf16"), (120, "fp16")])
 def test_moe_tile_path_matches_oracle_and_gemv(ops, device, tile_rows, bits_x2, rows, dtype):
     """Every expert on the many-row tile GEMM (threshold forced to 1 row),
     at every mul1 rate: against the oracle, and against the small-M GEMV
-    path to the same bar (the two sum in different FP32 orders)."""
+    path to the same bar (the two sum in different FP32 orders).  Experts
+    of ~3, ~27, ~64 and ~80 routed rows: the task loops of 2, 4, 5, 6 and 8
+    row blocks."""
     print(f"moe tile path bits_x2={bits_x2} rows={rows} {dtype}", flush=True)
     rng = np.random.default_rng(3000 * bits_x2 + rows)
     hidden, intermediate, experts, topk = 384, 256 + 128, 6, 4

@@ -381,7 +381,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   // an iteration: steps is a multiple of 4): the MFMAs of kRB row blocks of
   // step s on b_cur (high parts, then low parts), with the words of step
   // s + 1 read and decoded between them
-  auto step = [&](int s, auto slot, auto row_blocks) {
+  auto step = [&](int s, auto slot, auto row_blocks) __attribute__((always_inline)) {
     constexpr int kS = decltype(slot)::value;
     constexpr int kRB = decltype(row_blocks)::value;
     static_assert(kRB >= 2, "two row blocks read ahead");
@@ -441,10 +441,11 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     asm volatile("" ::: "memory");
   };
   // Row blocks past the tile's rows hold copies of its last row: a tile of
-  // up to half the rows runs the half-height loop (an MoE task of up to a
-  // quarter, the quarter-height one), any other the full one; none branches
-  // around an MFMA.
-  auto run = [&](auto row_blocks) {
+  // up to half the rows runs the half-height loop, any other the full one;
+  // an MoE task (an expert's rows, often well under 128) the loop of its
+  // height rounded up to 2, 4, 5, 6 or 8 row blocks.  None branches around
+  // an MFMA.
+  auto run = [&](auto row_blocks) __attribute__((always_inline)) {
     for (int s = 0; s < steps; s += kTileRing) {
       step(s, std::integral_constant<int, 0>{}, row_blocks);
       step(s + 1, std::integral_constant<int, 1>{}, row_blocks);
@@ -452,12 +453,23 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
       step(s + 3, std::integral_constant<int, 3>{}, row_blocks);
     }
   };
-  if (nblocks > kBlocks / 2) {
+  static_assert(kBlocks == 8, "row-block heights below");
+  if constexpr (kMoe) {
+    if (nblocks > 6) {
+      run(std::integral_constant<int, 8>{});
+    } else if (nblocks > 5) {
+      run(std::integral_constant<int, 6>{});
+    } else if (nblocks > 4) {
+      run(std::integral_constant<int, 5>{});
+    } else if (nblocks > 2) {
+      run(std::integral_constant<int, 4>{});
+    } else {
+      run(std::integral_constant<int, 2>{});
+    }
+  } else if (nblocks > kBlocks / 2) {
     run(std::integral_constant<int, kBlocks>{});
-  } else if (!kMoe || nblocks > kBlocks / 4) {
-    run(std::integral_constant<int, kBlocks / 2>{});
   } else {
-    run(std::integral_constant<int, kBlocks / 4>{});  // MoE tasks of up to 32 rows
+    run(std::integral_constant<int, kBlocks / 2>{});
   }
 
   // ---- epilogue ----
@@ -490,6 +502,9 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
   static_assert(sizeof(a_lds) >= 16 * kTileRedStride * sizeof(float), "epilogue rows fit");
 #pragma unroll
   for (int rb = 0; rb < kBlocks; ++rb) {
+    // (row blocks past the tile's rows store nothing: the workgroup stops
+    // there, all its threads together)
+    if (rb > 0 && 16 * rb >= nrows) break;
     // lane (g, m) holds rows 4 g + i of the block, column m of each MFMA
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
