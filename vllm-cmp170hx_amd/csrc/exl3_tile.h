@@ -359,23 +359,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     b[p][1] = __builtin_bit_cast(half8_t, u32x4_t{q0[2], q0[3], q1[2], q1[3]});
   };
 
-  // ---- prologue: T(0), T(1), A(0), T(2), A(1), T(3) in that order ----
-  asm volatile("" ::: "memory");
-  load_trellis(0);
-  load_trellis(min(1, last));
-  load_act(0);
-  load_trellis(min(2, last));
-  load_act(min(1, last));
-  load_trellis(min(3, last));
-  vq::wait_vmcnt<kAL + 2 * kTL>();  // T(0), T(1) and A(0) of this wavefront landed
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  read_words(std::integral_constant<int, 0>{});
-  tile_lgkm<0>();
-  tile_ready(words);
-  half8_t b_cur[2][2];              // step s's B operands
-  decode_pair(words, 0, b_cur);
-  decode_pair(words, 1, b_cur);
+  half8_t b_cur[2][2];  // step s's B operands
 
   // step s, its trellis in ring slot kS = s % 4 (the loop runs four steps
   // an iteration: steps is a multiple of 4): the MFMAs of kRB row blocks of
@@ -454,22 +438,58 @@ __global__ __launch_bounds__(kTileThreads, 2) void tile_gemm(TileArgs a) {
     }
   };
   static_assert(kBlocks == 8, "row-block heights below");
-  if constexpr (kMoe) {
-    if (nblocks > 6) {
-      run(std::integral_constant<int, 8>{});
-    } else if (nblocks > 5) {
-      run(std::integral_constant<int, 6>{});
-    } else if (nblocks > 4) {
-      run(std::integral_constant<int, 5>{});
-    } else if (nblocks > 2) {
-      run(std::integral_constant<int, 4>{});
-    } else {
-      run(std::integral_constant<int, 2>{});
+  // A wavefront whose tile columns all lie past the matrix (in the last
+  // column tile of a projection whose width is no multiple of 256) only
+  // loads its share of the activation tiles and meets every barrier: its
+  // SIMD serves the CU's other wavefronts meanwhile.
+  const bool idle = tc0 >= tiles_n;
+  if (idle) {
+    asm volatile("" ::: "memory");
+    load_act(0);
+    load_act(min(1, last));
+    vq::wait_vmcnt<kAL>();  // A(0) of this wavefront landed
+    __builtin_amdgcn_s_barrier();
+    for (int s = 0; s < steps; ++s) {
+      asm volatile("" ::: "memory");
+      load_act(min(s + 2, last));
+      vq::wait_vmcnt<kAL>();  // A(s + 1) of this wavefront landed
+      __builtin_amdgcn_s_barrier();
     }
-  } else if (nblocks > kBlocks / 2) {
-    run(std::integral_constant<int, kBlocks>{});
+    asm volatile("" ::: "memory");
   } else {
-    run(std::integral_constant<int, kBlocks / 2>{});
+    // ---- prologue: T(0), T(1), A(0), T(2), A(1), T(3) in that order ----
+    asm volatile("" ::: "memory");
+    load_trellis(0);
+    load_trellis(min(1, last));
+    load_act(0);
+    load_trellis(min(2, last));
+    load_act(min(1, last));
+    load_trellis(min(3, last));
+    vq::wait_vmcnt<kAL + 2 * kTL>();  // T(0), T(1) and A(0) of this wavefront landed
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read_words(std::integral_constant<int, 0>{});
+    tile_lgkm<0>();
+    tile_ready(words);
+    decode_pair(words, 0, b_cur);
+    decode_pair(words, 1, b_cur);
+    if constexpr (kMoe) {
+      if (nblocks > 6) {
+        run(std::integral_constant<int, 8>{});
+      } else if (nblocks > 5) {
+        run(std::integral_constant<int, 6>{});
+      } else if (nblocks > 4) {
+        run(std::integral_constant<int, 5>{});
+      } else if (nblocks > 2) {
+        run(std::integral_constant<int, 4>{});
+      } else {
+        run(std::integral_constant<int, 2>{});
+      }
+    } else if (nblocks > kBlocks / 2) {
+      run(std::integral_constant<int, kBlocks>{});
+    } else {
+      run(std::integral_constant<int, kBlocks / 2>{});
+    }
   }
 
   // ---- epilogue ----
