@@ -337,3 +337,38 @@ def test_moe_out_row_chunks_match_one_call(device):
             outs.append(out)
         torch.cuda.synchronize()
         assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), f"v2={v2}"
+
+
+def test_moe_route_over_many_workgroups_matches_row_chunks(device):
+    """A call of 8192 or more routed slots groups its rows by expert over
+    many workgroups (per-part counts and places, the tables from the summed
+    histograms, then each slot to its row); its outputs equal, bitwise,
+    those of the same call in row chunks of fewer slots, which the
+    one-workgroup route groups.  moe_out's run-time-format GEMV keeps every
+    token independent of the others."""
+    from vllm_mi355x.kernels.exl3 import ops
+    ops.ensure_extension()
+    rng = np.random.default_rng(83)
+    hidden, intermediate, experts, topk, rows = 256, 128, 16, 8, 2300
+    chunk = 700
+    assert rows * topk >= 8192 and chunk * topk < 8192
+    layer = Layer(rng, experts, hidden, intermediate, [(4, 2)], device, scales="sign")
+    ids_np = np.stack([rng.permutation(experts)[:topk] for _ in range(rows)])
+    ids_np[::7, 3] = -1  # masked slots
+    ids = _dev(ids_np, device)
+    weights = _dev(rng.random((rows, topk)).astype(np.float32), device)
+    emap_np = np.arange(experts, dtype=np.int64)
+    emap_np[5] = -1  # a remote expert
+    emap = _dev(emap_np, device)
+    _, _, x = _acts(rng, rows, hidden, "bf16", device)
+    ws = torch.empty(ops.moe_workspace_size(rows, hidden, intermediate, topk, experts),
+                     dtype=torch.float32, device=device)
+    outs = []
+    for row_chunk in (None, chunk):
+        out = torch.empty_like(x)
+        ops.moe_out(x, ids, weights, layer.ptrs, layer.meta, emap, intermediate, out, ws,
+                    row_chunk=row_chunk)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[0].float()).all()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))

@@ -3,10 +3,12 @@
 // grouped small-M MFMA kernel.
 //
 // Launch sequence on the caller's stream (as the reference's run_moe_out):
-//  1. moe_route: one workgroup groups the local assignments by local expert
-//     (counts, scan, sorted list: the GEMV experts' rows, then the tile
-//     experts' rows) and cuts each expert's rows into tasks of at most 32
-//     rows (8 for the run-time-format decode: the per-expert token sort).
+//  1. moe_route groups the local assignments by local expert (counts,
+//     scan, sorted list: the GEMV experts' rows, then the tile experts'
+//     rows) and cuts each expert's rows into tasks of at most 32 rows (8 for
+//     the run-time-format decode: the per-expert token sort): one workgroup
+//     below 8192 routed slots, else moe_route_count / moe_route /
+//     moe_route_fill over many workgroups.
 //  2. per projection (gate, up): moe_form builds t = H128(x[a / topk] * suh)
 //     of every local assignment, as FP16 high/low parts in MFMA B-operand
 //     order with one power-of-two scale per assignment row (the high parts
@@ -48,7 +50,6 @@ namespace exl3 {
 namespace {
 
 constexpr int kRouteThreads = 1024;
-constexpr int kRouteBatch = 8;  // assignments a route thread loads at a time
 constexpr int64_t kMaxRouteExperts = 4096;
 // Rows of one expert per GEMV task: every decoded weight operand feeds the
 // MFMAs of up to four 8-row sub-blocks, so a fixed-rate expert's weights
@@ -140,50 +141,137 @@ __device__ __forceinline__ bool tile_expert(const Routing& r, int e, int rows, i
 // tile_rows: the routed-row threshold of the tile GEMM (0: no tile tasks);
 // with fewer than min_tile_tasks tile tasks in all (too few workgroups to
 // fill the chip: each runs the whole K range), every expert takes the GEMV.
+
+// Local expert of global id g, or -1.
+__device__ __forceinline__ int local_of(const Routing& r, int64_t g) {
+  const bool in = g >= 0 && g < r.global_experts;
+  const int64_t l = in ? integer_at(r.expert_map, r.map64, g) : -1;
+  return l >= 0 && l < r.local_experts ? int(l) : -1;
+}
+
+// Calls of at least kRouteSplitMin routed slots group their rows over many
+// workgroups in three launches: moe_route_count (per part of kRoutePart
+// slots: each slot's expert and place among the part's rows of that expert,
+// and the part's histogram), moe_route with parts > 0 (counts summed from
+// the histograms, the tables, and each (part, expert)'s first sorted row
+// written back over its histogram entry), moe_route_fill (each slot to its
+// sorted row).  The packed slots and the histograms live in the workspace's
+// gate-result region, which no launch reads before the gate projection
+// writes it.
+constexpr int64_t kRouteSplitMin = 8192;
+constexpr int kRoutePartThreads = 256;
+constexpr int kRoutePartSlots = 8;  // slots a thread of a part takes
+constexpr int kRoutePart = kRoutePartThreads * kRoutePartSlots;
+// the one-workgroup route: slots a thread holds; histogram entries loaded
+// at a time
+constexpr int kRouteHeld = int(kRouteSplitMin / kRouteThreads);
+constexpr int kRouteBatch = 8;
+
+// packed[a] = expert << 16 | place of slot a among its part's rows of that
+// expert (or -1: not routed here); hist[part][expert] = the part's rows.
+__global__ __launch_bounds__(kRoutePartThreads) void moe_route_count(Routing routing, int64_t assignments,
+                                                                     int* packed, int* hist) {
+  extern __shared__ int part_count[];
+  const int experts = int(routing.local_experts);
+  for (int e = threadIdx.x; e < experts; e += kRoutePartThreads) part_count[e] = 0;
+  __syncthreads();
+  const int64_t a0 = int64_t(blockIdx.x) * kRoutePart + threadIdx.x;
+  int64_t g[kRoutePartSlots];
+#pragma unroll
+  for (int u = 0; u < kRoutePartSlots; ++u) {
+    const int64_t a = a0 + u * kRoutePartThreads;
+    g[u] = a < assignments ? integer_at(routing.ids, routing.ids64, a) : -1;
+  }
+  int e[kRoutePartSlots];
+#pragma unroll
+  for (int u = 0; u < kRoutePartSlots; ++u) e[u] = local_of(routing, g[u]);
+#pragma unroll
+  for (int u = 0; u < kRoutePartSlots; ++u) {
+    const int64_t a = a0 + u * kRoutePartThreads;
+    const int v = e[u] >= 0 ? (e[u] << 16) | atomicAdd(&part_count[e[u]], 1) : -1;
+    if (a < assignments) packed[a] = v;
+  }
+  __syncthreads();
+  for (int x = threadIdx.x; x < experts; x += kRoutePartThreads) {
+    hist[int64_t(blockIdx.x) * experts + x] = part_count[x];
+  }
+}
+
+// sorted[first row of (part, expert) + place] = a for every routed slot a.
+__global__ __launch_bounds__(kRoutePartThreads) void moe_route_fill(int64_t assignments, int experts,
+                                                                    const int* packed, const int* first,
+                                                                    int* sorted) {
+  const int64_t a0 = int64_t(blockIdx.x) * kRoutePart + threadIdx.x;
+  const int* part_first = first + int64_t(blockIdx.x) * experts;
+  int v[kRoutePartSlots];
+#pragma unroll
+  for (int u = 0; u < kRoutePartSlots; ++u) {
+    const int64_t a = a0 + u * kRoutePartThreads;
+    v[u] = a < assignments ? packed[a] : -1;
+  }
+#pragma unroll
+  for (int u = 0; u < kRoutePartSlots; ++u) {
+    if (v[u] >= 0) sorted[part_first[v[u] >> 16] + (v[u] & 0xffff)] = int(a0 + u * kRoutePartThreads);
+  }
+}
+
+// The route in one workgroup.  parts == 0 (calls of fewer than
+// kRouteSplitMin slots): from the ids, each thread's slots held in
+// registers: one round of id loads, one of expert-map loads, and the
+// counting atomic returns each slot's place among its expert's rows, so the
+// sorted list is written without a second pass.  parts > 0: the counts are
+// the sums of moe_route_count's histograms, each of whose entries is
+// replaced by the first sorted row of that (part, expert), and
+// moe_route_fill writes the sorted list.
 __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int64_t assignments,
                                                            int task_rows, int tile_rows,
-                                                           int min_tile_tasks, int* table) {
+                                                           int min_tile_tasks, int* table, int* hist,
+                                                           int parts) {
   extern __shared__ int route_shared[];
   const int experts = int(routing.local_experts);
-  int* count = route_shared;               // counts, then fill cursors
+  int* count = route_shared;               // rows per expert
   int* row_begin = count + experts;
   int* task_begin = row_begin + experts;   // GEMV tasks, experts + 1 entries
   int* tile_begin = task_begin + experts + 1;  // tile tasks, experts + 1 entries
-  __shared__ int scan_rows[kRouteThreads];   // GEMV experts' rows
-  __shared__ int scan_trows[kRouteThreads];  // tile experts' rows
-  __shared__ int scan_tasks[kRouteThreads];
-  __shared__ int scan_tiles[kRouteThreads];
+  constexpr int kWaves = kRouteThreads / 64;
+  __shared__ int wave_sums[kWaves][4];     // per wavefront: GEMV rows, tile rows, GEMV tasks, tile tasks
   __shared__ int tiles_in_all;
   const int tid = threadIdx.x;
-  for (int e = tid; e < experts; e += kRouteThreads) count[e] = 0;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (parts > 0) {
+    for (int e = tid; e < experts; e += kRouteThreads) {
+      int c = 0;
+      for (int p0 = 0; p0 < parts; p0 += kRouteBatch) {
+        int n[kRouteBatch];  // a batch of parts' loads in flight together
+#pragma unroll
+        for (int u = 0; u < kRouteBatch; ++u) n[u] = p0 + u < parts ? hist[int64_t(p0 + u) * experts + e] : 0;
+#pragma unroll
+        for (int u = 0; u < kRouteBatch; ++u) c += n[u];
+      }
+      count[e] = c;
+    }
+  } else {
+    for (int e = tid; e < experts; e += kRouteThreads) count[e] = 0;
+  }
   if (tid == 0) tiles_in_all = 0;
   __syncthreads();
-  // f(a, e) for every assignment a with local expert e >= 0: kRouteBatch
-  // assignments a thread at a time, their id loads issued together, then
-  // their expert-map loads together (one pair of memory round trips per
-  // batch instead of per assignment)
-  auto for_routed = [&](auto&& f) {
-    for (int64_t a0 = tid; a0 < assignments; a0 += int64_t(kRouteThreads) * kRouteBatch) {
-      int64_t g[kRouteBatch];
+  // parts == 0: slot tid + kRouteThreads * u as (expert << 16 | its place
+  // among that expert's rows), or -1
+  int hv[kRouteHeld];
+  if (parts == 0) {
+    int64_t g[kRouteHeld];
 #pragma unroll
-      for (int u = 0; u < kRouteBatch; ++u) {
-        const int64_t a = a0 + int64_t(u) * kRouteThreads;
-        g[u] = a < assignments ? integer_at(routing.ids, routing.ids64, a) : -1;
-      }
-      int64_t e[kRouteBatch];
-#pragma unroll
-      for (int u = 0; u < kRouteBatch; ++u) {
-        const bool in = g[u] >= 0 && g[u] < routing.global_experts;
-        const int64_t l = in ? integer_at(routing.expert_map, routing.map64, g[u]) : -1;
-        e[u] = l >= 0 && l < routing.local_experts ? l : -1;
-      }
-#pragma unroll
-      for (int u = 0; u < kRouteBatch; ++u) {
-        if (e[u] >= 0) f(a0 + int64_t(u) * kRouteThreads, int(e[u]));
-      }
+    for (int u = 0; u < kRouteHeld; ++u) {
+      const int64_t a = tid + int64_t(u) * kRouteThreads;
+      g[u] = a < assignments ? integer_at(routing.ids, routing.ids64, a) : -1;
     }
-  };
-  for_routed([&](int64_t, int e) { atomicAdd(&count[e], 1); });
+    int e[kRouteHeld];
+#pragma unroll
+    for (int u = 0; u < kRouteHeld; ++u) e[u] = local_of(routing, g[u]);
+#pragma unroll
+    for (int u = 0; u < kRouteHeld; ++u) hv[u] = e[u] >= 0 ? (e[u] << 16) | atomicAdd(&count[e[u]], 1) : -1;
+  }
   __syncthreads();
   // each thread a contiguous run of experts
   const int per = (experts + kRouteThreads - 1) / kRouteThreads;
@@ -199,46 +287,67 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
     if (tiles_in_all < min_tile_tasks) tile_rows = 0;
   }
   // exclusive scan of (GEMV rows, tile rows, GEMV tasks, tile tasks) over
-  // experts
-  int rows = 0, trows = 0, tasks = 0, tile_tasks = 0;
+  // experts: within each wavefront, then over the wavefronts' sums
+  int own[4] = {0, 0, 0, 0};
   for (int e = e0; e < e1; ++e) {
     const int c = count[e];
     if (tile_rows > 0 && tile_expert(routing, e, c, tile_rows)) {
-      trows += c;
-      tile_tasks += (c + kTileRows - 1) / kTileRows;
+      own[1] += c;
+      own[3] += (c + kTileRows - 1) / kTileRows;
     } else {
-      rows += c;
-      tasks += (c + task_rows - 1) / task_rows;
+      own[0] += c;
+      own[2] += (c + task_rows - 1) / task_rows;
     }
   }
-  scan_rows[tid] = rows;
-  scan_trows[tid] = trows;
-  scan_tasks[tid] = tasks;
-  scan_tiles[tid] = tile_tasks;
-  __syncthreads();
-  for (int d = 1; d < kRouteThreads; d <<= 1) {
-    const int r = tid >= d ? scan_rows[tid - d] : 0;
-    const int q = tid >= d ? scan_trows[tid - d] : 0;
-    const int t = tid >= d ? scan_tasks[tid - d] : 0;
-    const int u = tid >= d ? scan_tiles[tid - d] : 0;
-    __syncthreads();
-    scan_rows[tid] += r;
-    scan_trows[tid] += q;
-    scan_tasks[tid] += t;
-    scan_tiles[tid] += u;
-    __syncthreads();
+  int inc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    inc[i] = own[i];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(inc[i], d, 64);
+      if (lane >= d) inc[i] += v;
+    }
   }
-  const int gemv_rows = scan_rows[kRouteThreads - 1];
-  int row_at = scan_rows[tid] - rows;
-  int trow_at = gemv_rows + scan_trows[tid] - trows;
-  int task_at = scan_tasks[tid] - tasks;
-  int tile_at = scan_tiles[tid] - tile_tasks;
+  if (lane == 63) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wave_sums[wave][i] = inc[i];
+  }
+  __syncthreads();
+  int before[4] = {0, 0, 0, 0}, total[4] = {0, 0, 0, 0};
+  for (int w = 0; w < kWaves; ++w) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = wave_sums[w][i];
+      if (w < wave) before[i] += v;
+      total[i] += v;
+    }
+  }
+  const int gemv_rows = total[0];
+  int row_at = before[0] + inc[0] - own[0];
+  int trow_at = gemv_rows + before[1] + inc[1] - own[1];
+  int task_at = before[2] + inc[2] - own[2];
+  int tile_at = before[3] + inc[3] - own[3];
   for (int e = e0; e < e1; ++e) {
     const int c = count[e];
     const bool tile = tile_rows > 0 && tile_expert(routing, e, c, tile_rows);
     row_begin[e] = tile ? trow_at : row_at;
     task_begin[e] = task_at;
     tile_begin[e] = tile_at;
+    if (parts > 0) {
+      // the parts' rows of this expert follow each other in part order
+      int at = row_begin[e];
+      for (int p0 = 0; p0 < parts; p0 += kRouteBatch) {
+        int n[kRouteBatch];
+#pragma unroll
+        for (int u = 0; u < kRouteBatch; ++u) n[u] = p0 + u < parts ? hist[int64_t(p0 + u) * experts + e] : 0;
+#pragma unroll
+        for (int u = 0; u < kRouteBatch; ++u) {
+          if (p0 + u < parts) hist[int64_t(p0 + u) * experts + e] = at;
+          at += n[u];
+        }
+      }
+    }
     if (tile) {
       trow_at += c;
       tile_at += (c + kTileRows - 1) / kTileRows;
@@ -247,9 +356,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
       task_at += (c + task_rows - 1) / task_rows;
     }
   }
-  const int total_rows = gemv_rows + scan_trows[kRouteThreads - 1];
-  const int total_tasks = scan_tasks[kRouteThreads - 1];
-  const int total_tiles = scan_tiles[kRouteThreads - 1];
+  const int total_rows = gemv_rows + total[1];
+  const int total_tasks = total[2];
+  const int total_tiles = total[3];
   if (tid == 0) {
     task_begin[experts] = total_tasks;
     tile_begin[experts] = total_tiles;
@@ -283,11 +392,12 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
     const int end = row_begin[e] + count[e];
     task_table[total_tasks + t] = make_int4(e, first, min(kTileRows, end - first), 0);
   }
-  __syncthreads();
-  for (int e = e0; e < e1; ++e) count[e] = row_begin[e];  // fill cursors
-  __syncthreads();
+  if (parts > 0) return;  // moe_route_fill writes the sorted list
   int* sorted = table + 4;
-  for_routed([&](int64_t a, int e) { sorted[atomicAdd(&count[e], 1)] = int(a); });
+#pragma unroll
+  for (int u = 0; u < kRouteHeld; ++u) {
+    if (hv[u] >= 0) sorted[row_begin[hv[u] >> 16] + (hv[u] & 0xffff)] = int(tid + u * kRouteThreads);
+  }
 }
 
 // ---- 2/3. activations in B-operand form ----------------------------------------
@@ -1004,10 +1114,28 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   }
   if (any) {
     int* table = reinterpret_cast<int*>(workspace + lay.ints());
-    hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads),
-                       size_t(4 * local_experts + 2) * sizeof(int), s, routing, assignments, task_rows,
-                       tiles ? tile_rows : 0, min_tile_tasks, table);
-    if (int rc = check_launch("exl3 moe_route")) return rc;
+    const size_t route_lds = size_t(4 * local_experts + 2) * sizeof(int);
+    if (assignments >= exl3::kRouteSplitMin) {
+      // packed slots, then the parts' histograms, in the gate-result region
+      // (A * ipad floats, ipad >= 128: room for A + parts * experts ints)
+      const int64_t parts = (assignments + exl3::kRoutePart - 1) / exl3::kRoutePart;
+      int* packed = reinterpret_cast<int*>(workspace + lay.gate());
+      int* hist = packed + (assignments + 3) / 4 * 4;
+      hipLaunchKernelGGL(exl3::moe_route_count, dim3(unsigned(parts)), dim3(exl3::kRoutePartThreads),
+                         size_t(local_experts) * sizeof(int), s, routing, assignments, packed, hist);
+      if (int rc = check_launch("exl3 moe_route_count")) return rc;
+      hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads), route_lds, s, routing,
+                         assignments, task_rows, tiles ? tile_rows : 0, min_tile_tasks, table, hist,
+                         int(parts));
+      if (int rc = check_launch("exl3 moe_route")) return rc;
+      hipLaunchKernelGGL(exl3::moe_route_fill, dim3(unsigned(parts)), dim3(exl3::kRoutePartThreads), 0, s,
+                         assignments, int(local_experts), packed, hist, table + 4);
+      if (int rc = check_launch("exl3 moe_route_fill")) return rc;
+    } else {
+      hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads), route_lds, s, routing,
+                         assignments, task_rows, tiles ? tile_rows : 0, min_tile_tasks, table, nullptr, 0);
+      if (int rc = check_launch("exl3 moe_route")) return rc;
+    }
     auto tile = [&](int projection, int64_t kp, int64_t np, int64_t in_off, int64_t out_off) {
       exl3::TileArgs t{};
       t.act = reinterpret_cast<const uint8_t*>(workspace + in_off);
