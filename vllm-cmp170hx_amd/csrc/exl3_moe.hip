@@ -441,16 +441,25 @@ __device__ __forceinline__ void store8(__amdgpu_buffer_rsrc_t dst, int kp, int k
 // kActivate false: gate/up input, t = H128(x[a / topk] * suh_projection);
 // true: down input from the gate/up results (already H128 * svh):
 // clamp, SiLU(g) * u * suh_down, H128, into the act region.
-// One workgroup per local assignment.  A wavefront forms four blocks at a
-// time (block group G: blocks 4 G .. 4 G + 3, one per 16-lane row, eight
-// inputs a lane); wavefront w takes groups w, w + 4, ... (the first kCache
-// of them kept in registers, their loads issued together at clamped group
-// indices) for the row maximum of |t|, then writes the high / low parts at
-// the row's one power-of-two scale, so the expert GEMV sums the whole row
-// before it unscales; groups past the register cache are formed again (the
-// same operations, so the same values).  An expert whose matrix is not kp
-// rows long gets NaN operands (its suh is not read).
-template <bool kActivate, int kCache>
+// A wavefront forms four blocks at a time (block group G: blocks 4 G ..
+// 4 G + 3, one per 16-lane row, eight inputs a lane), the first kCache
+// groups it takes kept in registers (their loads issued together at clamped
+// group indices), for the row maximum of |t|, then writes the high / low
+// parts at the row's one power-of-two scale, so the expert GEMV sums the
+// whole row before it unscales; groups past the register cache are formed
+// again (the same operations, so the same values).  kWaveRow: each
+// wavefront forms a sorted row of its own (four rows a workgroup: rows of
+// up to 4 kCache groups, whose chains of dependent loads then overlap four
+// times as deep); otherwise one workgroup a row, wavefront w taking groups
+// w, w + 4, ... and the maximum met in LDS.  An expert whose matrix is not
+// kp rows long gets NaN operands (its suh is not read).
+// The longest rows formed one wavefront a row: gate / up inputs, and the
+// down input (whose SwiGLU makes a row's groups VALU work better spread over
+// four wavefronts beyond two groups); the fewest routed slots formed so.
+constexpr int64_t kFormRowGroups = 6;
+constexpr int64_t kFormRowGroupsActivate = 2;
+constexpr int64_t kFormRowMin = 8192;
+template <bool kActivate, int kCache, bool kWaveRow>
 __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, int x_dtype,
                                                 int64_t hidden, int64_t intermediate, int projection,
                                                 const int* table, float* ws, MoeLayout lay,
@@ -463,15 +472,19 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   const int64_t kp = kActivate ? lay.ipad : lay.hpad;
   const int64_t blocks = kp / 128;
   const int64_t groups = (blocks + 3) / 4;
-  if (int64_t(blockIdx.x) >= int64_t(table[0])) return;
-  const int64_t a = table[4 + blockIdx.x];
+  // the sorted row, the wavefront's first group and its group stride
+  const int row = kWaveRow ? int(blockIdx.x) * 4 + wave : int(blockIdx.x);
+  const int g0 = kWaveRow ? 0 : wave;
+  constexpr int kStride = kWaveRow ? 1 : 4;
+  if (row >= table[0]) return;
+  const int64_t a = table[4 + row];
   const int64_t e = local_expert(routing, a);
   const int64_t* ptrs = routing.ptrs + e * 9;
   // the tile experts' rows (sorted rows from the first tile task's first
   // on) feed only the tile GEMM, which reads the low parts unless it runs
   // at FP16 precision
   const bool lo = tile_lo || table[2] == 0 ||
-                  int(blockIdx.x) < reinterpret_cast<const int4*>(table + lay.tasks())[table[3]].y;
+                  row < reinterpret_cast<const int4*>(table + lay.tasks())[table[3]].y;
   int* exps = reinterpret_cast<int*>(ws + lay.ints()) + lay.exps() + a * (lay.kmax() / 128);
   const __amdgpu_buffer_rsrc_t dst =
       make_rsrc(ws + (kActivate ? lay.act() : lay.input()) + a * kp, uint32_t(kp) * 4u);
@@ -548,22 +561,24 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
     vq::h128_rows(v, l);
   };
   auto live = [&](int64_t G) { return 4 * G + q < blocks; };
-  if (threadIdx.x == 0) row_max = 0u;
-  __syncthreads();
+  if constexpr (!kWaveRow) {
+    if (threadIdx.x == 0) row_max = 0u;
+    __syncthreads();
+  }
   float mx = 0.0f;
   float c[kCache][8];
 #pragma unroll
   for (int i = 0; i < kCache; ++i) {
-    form(min(int64_t(wave + 4 * i), groups - 1), c[i]);
+    form(min(int64_t(g0 + kStride * i), groups - 1), c[i]);
   }
 #pragma unroll
   for (int i = 0; i < kCache; ++i) {
-    if (wave + 4 * i < groups && live(wave + 4 * i)) {
+    if (g0 + kStride * i < groups && live(g0 + kStride * i)) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(c[i][j]));
     }
   }
-  for (int64_t G = wave + 4 * kCache; G < groups; G += 4) {
+  for (int64_t G = g0 + kStride * kCache; G < groups; G += kStride) {
     float v[8];
     form(G, v);
     if (live(G)) {
@@ -572,15 +587,21 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
     }
   }
   mx = vq::wave_max(mx, lane);
-  if (lane == 0) atomicMax(&row_max, __builtin_bit_cast(uint32_t, mx));
-  __syncthreads();
-  const int ex = scale_exponent(row_max);
-  if (threadIdx.x == 0) exps[0] = ex;
+  int ex;
+  if constexpr (kWaveRow) {
+    ex = scale_exponent(__builtin_bit_cast(uint32_t, mx));
+    if (lane == 0) exps[0] = ex;
+  } else {
+    if (lane == 0) atomicMax(&row_max, __builtin_bit_cast(uint32_t, mx));
+    __syncthreads();
+    ex = scale_exponent(row_max);
+    if (threadIdx.x == 0) exps[0] = ex;
+  }
 #pragma unroll
   for (int i = 0; i < kCache; ++i) {
-    if (wave + 4 * i < groups && live(wave + 4 * i)) store8(dst, int(kp), first_k(wave + 4 * i), c[i], ex, lo);
+    if (g0 + kStride * i < groups && live(g0 + kStride * i)) store8(dst, int(kp), first_k(g0 + kStride * i), c[i], ex, lo);
   }
-  for (int64_t G = wave + 4 * kCache; G < groups; G += 4) {
+  for (int64_t G = g0 + kStride * kCache; G < groups; G += kStride) {
     float v[8];
     form(G, v);
     if (live(G)) store8(dst, int(kp), first_k(G), v, ex, lo);
@@ -1174,19 +1195,36 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
       }
       return check_launch("exl3 moe_gemv");
     };
-    // moe_form: one workgroup per assignment (the routed ones do work), its
-    // register cache sized to the 4-block groups a wavefront forms
+    // moe_form: calls of kFormRowMin rows or more whose rows have few
+    // enough 4-block groups one wavefront a row (four rows a workgroup),
+    // others one workgroup a row (fewer rows: each row's groups over four
+    // wavefronts finish sooner); the register cache sized to the groups a
+    // wavefront forms
     auto form = [&](bool activate, int projection) {
       const int64_t groups = ((activate ? lay.ipad : lay.hpad) / 128 + 3) / 4;
       const int64_t per_wave = (groups + 3) / 4;
       const dim3 grid{unsigned(assignments), 1u, 1u};
-#define VQ_FORM(A, C)                                                                              \
-  hipLaunchKernelGGL((exl3::moe_form<A, C>), grid, dim3(256), 0, s, routing, x, x_dtype, hidden, \
-                     intermediate_size, projection, table, workspace, lay, swiglu_limit, tile_lo)
-      if (activate) {
-        if (per_wave <= 1) VQ_FORM(true, 1); else if (per_wave <= 2) VQ_FORM(true, 2); else VQ_FORM(true, 4);
+      const dim3 row_grid{unsigned((assignments + 3) / 4), 1u, 1u};
+#define VQ_FORM(A, C, W)                                                                            \
+  hipLaunchKernelGGL((exl3::moe_form<A, C, W>), W ? row_grid : grid, dim3(256), 0, s, routing, x,   \
+                     x_dtype, hidden, intermediate_size, projection, table, workspace, lay,         \
+                     swiglu_limit, tile_lo)
+      if (groups <= (activate ? exl3::kFormRowGroupsActivate : exl3::kFormRowGroups) &&
+          assignments >= exl3::kFormRowMin) {
+        switch (int(groups) + (activate ? 8 : 0)) {
+          case 1: VQ_FORM(false, 1, true); break;
+          case 2: VQ_FORM(false, 2, true); break;
+          case 3: VQ_FORM(false, 3, true); break;
+          case 4: VQ_FORM(false, 4, true); break;
+          case 5: VQ_FORM(false, 5, true); break;
+          case 6: VQ_FORM(false, 6, true); break;
+          case 9: VQ_FORM(true, 1, true); break;
+          default: VQ_FORM(true, 2, true); break;
+        }
+      } else if (activate) {
+        if (per_wave <= 1) VQ_FORM(true, 1, false); else if (per_wave <= 2) VQ_FORM(true, 2, false); else VQ_FORM(true, 4, false);
       } else {
-        if (per_wave <= 1) VQ_FORM(false, 1); else if (per_wave <= 2) VQ_FORM(false, 2); else VQ_FORM(false, 4);
+        if (per_wave <= 1) VQ_FORM(false, 1, false); else if (per_wave <= 2) VQ_FORM(false, 2, false); else VQ_FORM(false, 4, false);
       }
 #undef VQ_FORM
       return check_launch("exl3 moe_form");
