@@ -27,7 +27,8 @@ def _bf16(rng, shape, scale=1.0):
 
 @pytest.mark.parametrize("M_,E,K,topk,bs,scoring", [
     (1, 288, 4096, 8, 8, "sigmoid"), (4, 288, 4096, 8, 8, "sigmoid"), (64, 288, 4096, 8, 16, "sigmoid"),
-    (33, 128, 2048, 8, 8, "softmax"), (300, 64, 1024, 6, 32, "softmax"), (7, 257, 7168, 8, 8, "sigmoid")])
+    (33, 128, 2048, 8, 8, "softmax"), (300, 64, 1024, 6, 32, "softmax"), (7, 257, 7168, 8, 8, "sigmoid"),
+    (2048, 288, 4096, 8, 16, "sigmoid")])
 def test_route_matches_oracle(device, M_, E, K, topk, bs, scoring):
     from vllm_mi355x.kernels.moe import route
     print(f"moe_route M={M_} E={E} K={K} topk={topk} bs={bs} {scoring}", flush=True)
@@ -89,3 +90,30 @@ def test_route_is_deterministic_and_takes_out(device):
     for a, b in zip(first, second):
         assert torch.equal(a, b)
     assert second[0].data_ptr() == out[0].data_ptr()
+
+
+def test_route_rows_independent_of_the_call(device):
+    """Each row's weights and ids depend on that row alone: the first 64 rows
+    of a 200-row call equal, bitwise, a call of those 64 rows (the selection
+    runs one wavefront a row over as many workgroups as the rows need), and
+    the alignment equals the alignment oracle on the ids."""
+    from vllm_mi355x.kernels.moe import route
+    rng = np.random.default_rng(11)
+    M_, E, K, topk, bs = 200, 288, 4096, 8, 16
+    xb, _ = _bf16(rng, (M_, K))
+    wb, _ = _bf16(rng, (E, K), 0.02)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    x = to(xb.view(np.int16)).view(torch.bfloat16)
+    w = to(wb.view(np.int16)).view(torch.bfloat16)
+    _, tw_all, tid_all, sorted_ids, eids, ntpp = route.moe_route(x, w, to(bias), topk=topk, block_size=bs,
+                                                                  num_experts=E)
+    _, tw_64, tid_64, _, _, _ = route.moe_route(x[:64].contiguous(), w, to(bias), topk=topk, block_size=bs,
+                                                num_experts=E)
+    torch.cuda.synchronize()
+    assert torch.equal(tid_all[:64], tid_64)
+    assert torch.equal(tw_all[:64].view(torch.int32), tw_64.view(torch.int32))
+    es, eeids, entpp = M.align(tid_all.cpu().numpy(), E, bs)
+    assert int(ntpp.item()) == int(entpp[0])
+    assert np.array_equal(sorted_ids.cpu().numpy(), es)
+    assert np.array_equal(eids.cpu().numpy(), eeids)

@@ -1507,22 +1507,51 @@ __device__ __forceinline__ int32_t monotone(float v) {
 
 constexpr int kRouteMaxExperts = 1024;
 
-// One workgroup: wavefront w routes rows w, w + 16, ...: scores of every
-// expert (sigmoid: 0.5 tanh(0.5 l) + 0.5, the key adding the bias; softmax:
+// 64-bit maximum over the wavefront, in scalar registers: within each
+// 16-lane row by DPP (quad swaps, then the half-row and row mirrors), then
+// over the four rows' maxima.  Every lane must be active.
+__device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
+  auto step = [&](auto ctrl) {
+    constexpr int c = decltype(ctrl)::value;
+    const uint64_t u = uint64_t(v);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_mov_dpp(int(uint32_t(u)), c, 0xF, 0xF, false));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_mov_dpp(int(uint32_t(u >> 32)), c, 0xF, 0xF, false));
+    const int64_t o = int64_t((uint64_t(hi) << 32) | lo);
+    v = o > v ? o : v;
+  };
+  step(std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  step(std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  step(std::integral_constant<int, 0x141>{});  // row_half_mirror
+  step(std::integral_constant<int, 0x140>{});  // row_mirror
+  int64_t best = INT64_MIN;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint64_t u = uint64_t(v);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(u)), 16 * r));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(u >> 32)), 16 * r));
+    const int64_t o = int64_t((uint64_t(hi) << 32) | lo);
+    best = o > best ? o : best;
+  }
+  return best;
+}
+
+// One wavefront a row (four rows a workgroup, the grid looping over more),
+// kPer experts a lane (expert lane + 64 j): scores of every expert
+// (sigmoid: 0.5 tanh(0.5 l) + 0.5, the key adding the bias; softmax:
 // exp(l - max) / sum, the key the probability), top-k by the packed
 // (monotone(key) << 32 | E - 1 - e) maximum (the lower expert wins an exact
 // tie), weights = the selected scores, renormalized (/ (sum + 1e-20)) if
-// asked, times `scale`; padding rows (is_padding != 0) route to -1.  Then
-// the block alignment of the ids, in the same workgroup.
-__global__ __launch_bounds__(kAlignThreads) void route_select_align_kernel(
-    const float* logits, const float* bias, int64_t M, int E, int topk, int sigmoid, int renorm,
-    float scale, const uint8_t* is_padding, float* topk_w, int32_t* topk_ids, int bs,
-    int32_t* sorted, int64_t sorted_size, int32_t* eids, int64_t blocks, int32_t* ntpp,
-    int wave_counts) {
+// asked, times `scale`; padding rows (is_padding != 0) route to -1.  The
+// block alignment of the ids follows as a launch of its own.
+template <int kPer>
+__global__ __launch_bounds__(256) void route_select_kernel(const float* logits, const float* bias,
+                                                           int64_t M, int E, int topk, int sigmoid,
+                                                           int renorm, float scale,
+                                                           const uint8_t* is_padding, float* topk_w,
+                                                           int32_t* topk_ids) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  constexpr int kPer = kRouteMaxExperts / 64;
-  for (int64_t m = wave; m < M; m += kAlignThreads / 64) {
+  const int64_t stride = int64_t(gridDim.x) * 4;
+  for (int64_t m = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); m < M; m += stride) {
     const float* lrow = logits + m * E;
     float score[kPer];
     int64_t packed[kPer];
@@ -1545,7 +1574,7 @@ __global__ __launch_bounds__(kAlignThreads) void route_select_align_kernel(
     }
     if (!sigmoid) {
       // the softmax denominator: a fixed-order sum (per lane in expert
-      // order, then the butterfly)
+      // order, then the butterfly, whose partners add the same two values)
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) sum += __shfl_xor(sum, d);
 #pragma unroll
@@ -1564,11 +1593,7 @@ __global__ __launch_bounds__(kAlignThreads) void route_select_align_kernel(
       int64_t best = INT64_MIN;
 #pragma unroll
       for (int j = 0; j < kPer; ++j) best = packed[j] > best ? packed[j] : best;
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) {
-        const int64_t o = __shfl_xor(best, d);
-        best = o > best ? o : best;
-      }
+      best = wave_max_i64(best);  // uniform
       const int e = E - 1 - int(best & 0xffffffff);
       float v_own = 0.0f;
 #pragma unroll
@@ -1576,7 +1601,7 @@ __global__ __launch_bounds__(kAlignThreads) void route_select_align_kernel(
         if (j == e / 64) v_own = score[j];
         if (packed[j] == best) packed[j] = INT64_MIN;
       }
-      const float chosen = __shfl(v_own, e % 64);
+      const float chosen = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v_own), e % 64));
       total += chosen;
       if (lane == k) {
         sel_w = chosen;
@@ -1591,10 +1616,6 @@ __global__ __launch_bounds__(kAlignThreads) void route_select_align_kernel(
       topk_ids[m * topk + lane] = pad ? -1 : sel_e;
     }
   }
-  // the ids are read back by this workgroup's alignment
-  __threadfence();
-  __syncthreads();
-  align_block(topk_ids, M * topk, E, bs, nullptr, sorted, sorted_size, eids, blocks, ntpp, wave_counts);
 }
 
 // ---- split-cover alignment (marlin_moe/split_align.py:173-224's layout) ----------------
@@ -2258,11 +2279,22 @@ extern "C" int moe_route(const void* x, int x_dtype, int64_t M, int64_t K, int64
                        M, K, num_experts, logits);
   }
   if (int rc = check_launch("moe_route logits")) return rc;
-  hipLaunchKernelGGL(marlin::route_select_align_kernel, dim3(1), dim3(marlin::kAlignThreads), lds, s,
-                     logits, bias, M, int(num_experts), int(topk), scoring, renormalize, scale,
-                     is_padding, topk_weights, topk_ids, int(block_size), sorted, sorted_numel,
-                     expert_ids, expert_ids_numel, ntpp, wave_counts);
-  return check_launch("moe_route select_align");
+  // four rows a workgroup, at most 64 Ki workgroups (rows beyond loop);
+  // kPer = experts a lane
+  const unsigned select_groups = unsigned(std::min<int64_t>((M + 3) / 4, 65536));
+  const int per = int((num_experts + 63) / 64);
+#define VQ_SELECT(P)                                                                                \
+  hipLaunchKernelGGL(marlin::route_select_kernel<P>, dim3(select_groups), dim3(256), 0, s, logits, bias, \
+                     M, int(num_experts), int(topk), scoring, renormalize, scale, is_padding,          \
+                     topk_weights, topk_ids)
+  if (per <= 1) VQ_SELECT(1); else if (per <= 2) VQ_SELECT(2); else if (per <= 4) VQ_SELECT(4);
+  else if (per <= 5) VQ_SELECT(5); else if (per <= 8) VQ_SELECT(8); else VQ_SELECT(16);
+#undef VQ_SELECT
+  if (int rc = check_launch("moe_route select")) return rc;
+  hipLaunchKernelGGL(marlin::moe_align_kernel, dim3(1), dim3(marlin::kAlignThreads), lds, s, topk_ids,
+                     M * topk, int(num_experts), int(block_size), nullptr, sorted, sorted_numel, expert_ids,
+                     expert_ids_numel, ntpp, wave_counts);
+  return check_launch("moe_route align");
 }
 
 extern "C" int marlin_moe_align_permute(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
