@@ -93,24 +93,26 @@ def test_route_is_deterministic_and_takes_out(device):
 
 
 def test_route_rows_independent_of_the_call(device):
-    """Each row's weights and ids depend on that row alone: the first 64 rows
-    of a 200-row call equal, bitwise, a call of those 64 rows (the selection
-    runs one wavefront a row over as many workgroups as the rows need), and
-    the alignment equals the alignment oracle on the ids."""
+    """Each row's logits, weights and ids depend on that row alone: the first
+    64 rows of a 300-row call (router GEMV on 64 x 64 tiles) equal, bitwise,
+    a call of those 64 rows (16 x 16 tiles; the selection runs one wavefront
+    a row over as many workgroups as the rows need), and the alignment
+    equals the alignment oracle on the ids."""
     from vllm_mi355x.kernels.moe import route
     rng = np.random.default_rng(11)
-    M_, E, K, topk, bs = 200, 288, 4096, 8, 16
+    M_, E, K, topk, bs = 300, 288, 4096, 8, 16
     xb, _ = _bf16(rng, (M_, K))
     wb, _ = _bf16(rng, (E, K), 0.02)
     bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
     to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
     x = to(xb.view(np.int16)).view(torch.bfloat16)
     w = to(wb.view(np.int16)).view(torch.bfloat16)
-    _, tw_all, tid_all, sorted_ids, eids, ntpp = route.moe_route(x, w, to(bias), topk=topk, block_size=bs,
-                                                                  num_experts=E)
-    _, tw_64, tid_64, _, _, _ = route.moe_route(x[:64].contiguous(), w, to(bias), topk=topk, block_size=bs,
-                                                num_experts=E)
+    lg_all, tw_all, tid_all, sorted_ids, eids, ntpp = route.moe_route(x, w, to(bias), topk=topk,
+                                                                       block_size=bs, num_experts=E)
+    lg_64, tw_64, tid_64, _, _, _ = route.moe_route(x[:64].contiguous(), w, to(bias), topk=topk,
+                                                    block_size=bs, num_experts=E)
     torch.cuda.synchronize()
+    assert torch.equal(lg_all[:64].view(torch.int32), lg_64.view(torch.int32))
     assert torch.equal(tid_all[:64], tid_64)
     assert torch.equal(tw_all[:64].view(torch.int32), tw_64.view(torch.int32))
     es, eeids, entpp = M.align(tid_all.cpu().numpy(), E, bs)

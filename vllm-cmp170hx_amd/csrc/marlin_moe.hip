@@ -1453,51 +1453,93 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
 typedef short bf16raw8_t __attribute__((ext_vector_type(8)));
 
 // logits[m][e] = sum_k x[m][k] W[e][k] in FP32 (bf16 or fp16 products are
-// exact in FP32).  Workgroup = 16 experts x 16 rows: its four wavefronts
-// take a quarter of K each on v_mfma_f32_16x16x32 (A = 16 rows x 32 k, B =
-// 32 k x 16 experts, every lane 8 consecutive k of its row / expert), and the
-// quarters are added in wavefront order: one fixed order, so the logits are
-// bitwise reproducible and independent of M.  Rows past M and experts past
+// exact in FP32).  Workgroup = 16 kEB experts x 16 kRB rows: its four
+// wavefronts take a quarter of K each on v_mfma_f32_16x16x32 (A = 16 rows x
+// 32 k, B = 32 k x 16 experts, every lane 8 consecutive k of its row /
+// expert), each 16 x 16 block of the tile its own accumulator, and the
+// quarters are added in wavefront order.  Every logit is then the same
+// sequence of operations whatever the tile and M, so the logits are
+// bitwise reproducible and independent of M; larger tiles (large M) read
+// the router matrix and the rows fewer times.  Rows past M and experts past
 // E read a valid row and are not stored.
-template <bool kBF16>
+template <bool kBF16, int kRB, int kEB>
 __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* x, int64_t x_stride,
                                                            const uint16_t* w, int64_t M, int64_t K,
                                                            int64_t E, float* logits) {
-  __shared__ f32x4_t red[3][64];
+  __shared__ f32x4_t red[3][kRB * kEB][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t e0 = int64_t(blockIdx.x) * 16;
-  const int64_t m0 = int64_t(blockIdx.y) * 16;
+  const int64_t e0 = int64_t(blockIdx.x) * 16 * kEB;
+  const int64_t m0 = int64_t(blockIdx.y) * 16 * kRB;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int64_t row = min(m0 + r, M - 1);
-  const int64_t ex = min(e0 + r, E - 1);
   const int64_t kq = K / 4;
-  const uint16_t* xa = x + row * x_stride + wave * kq + 8 * g;
-  const uint16_t* wb = w + ex * K + wave * kq + 8 * g;
-  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const uint16_t* xa[kRB];
+  const uint16_t* wb[kEB];
+#pragma unroll
+  for (int i = 0; i < kRB; ++i) xa[i] = x + min(m0 + 16 * i + r, M - 1) * x_stride + wave * kq + 8 * g;
+#pragma unroll
+  for (int j = 0; j < kEB; ++j) wb[j] = w + min(e0 + 16 * j + r, E - 1) * K + wave * kq + 8 * g;
+  f32x4_t acc[kRB][kEB];
+#pragma unroll
+  for (int i = 0; i < kRB; ++i)
+#pragma unroll
+    for (int j = 0; j < kEB; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // the next step's fragments are loaded before this step's products
+  u32x4_t a[kRB], b[kEB];
+#pragma unroll
+  for (int i = 0; i < kRB; ++i) a[i] = *reinterpret_cast<const u32x4_t*>(xa[i]);
+#pragma unroll
+  for (int j = 0; j < kEB; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(wb[j]);
   for (int64_t k = 0; k < kq; k += 32) {
-    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa + k);
-    const u32x4_t b = *reinterpret_cast<const u32x4_t*>(wb + k);
-    acc = mfma<kBF16>(b, a, acc);  // C[e][m]: lane holds experts 4g..4g+3 of row r
+    const int64_t kn = k + 32 < kq ? k + 32 : k;  // the last step reloads its own
+    u32x4_t an[kRB], bn[kEB];
+#pragma unroll
+    for (int i = 0; i < kRB; ++i) an[i] = *reinterpret_cast<const u32x4_t*>(xa[i] + kn);
+#pragma unroll
+    for (int j = 0; j < kEB; ++j) bn[j] = *reinterpret_cast<const u32x4_t*>(wb[j] + kn);
+#pragma unroll
+    for (int i = 0; i < kRB; ++i)
+#pragma unroll
+      for (int j = 0; j < kEB; ++j) acc[i][j] = mfma<kBF16>(b[j], a[i], acc[i][j]);  // C[e][m]
+#pragma unroll
+    for (int i = 0; i < kRB; ++i) a[i] = an[i];
+#pragma unroll
+    for (int j = 0; j < kEB; ++j) b[j] = bn[j];
   }
-  if (wave > 0) red[wave - 1][lane] = acc;
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < kRB; ++i)
+#pragma unroll
+      for (int j = 0; j < kEB; ++j) red[wave - 1][i * kEB + j][lane] = acc[i][j];
+  }
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
-      const f32x4_t o = red[q][lane];
+    for (int i = 0; i < kRB; ++i) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] += o[i];
-    }
-    const int64_t m = m0 + r;
+      for (int j = 0; j < kEB; ++j) {
+        f32x4_t v = acc[i][j];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t e = e0 + 4 * g + i;
-      if (m < M && e < E) logits[m * E + e] = acc[i];
+        for (int q = 0; q < 3; ++q) {
+          const f32x4_t o = red[q][i * kEB + j][lane];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[c] += o[c];
+        }
+        // lane holds experts 4 g .. 4 g + 3 of row r of block (i, j)
+        const int64_t m = m0 + 16 * i + r;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int64_t e = e0 + 16 * j + 4 * g + c;
+          if (m < M && e < E) logits[m * E + e] = v[c];
+        }
+      }
     }
   }
 }
+
+constexpr int64_t kLogitsTile32Rows = 256;
+constexpr int64_t kLogitsTile64Rows = 1024;
 
 // An FP32 key as a signed integer of the same order.
 __device__ __forceinline__ int32_t monotone(float v) {
@@ -2268,16 +2310,20 @@ extern "C" int moe_route(const void* x, int x_dtype, int64_t M, int64_t K, int64
     return rc;
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(unsigned((num_experts + 15) / 16), unsigned((M + 15) / 16));
+  // tiles of 16 x 16 (the most workgroups) for few rows, 32 x 32 and then
+  // 64 x 64 (the router matrix read once per 32 / 64 rows) for more
+  const int tile = M > marlin::kLogitsTile64Rows ? 4 : (M > marlin::kLogitsTile32Rows ? 2 : 1);
+  const dim3 grid(unsigned((num_experts + 16 * tile - 1) / (16 * tile)), unsigned((M + 16 * tile - 1) / (16 * tile)));
+#define VQ_LOGITS(B, T)                                                                            \
+  hipLaunchKernelGGL((marlin::route_logits_kernel<B, T, T>), grid, dim3(256), 0, s,                 \
+                     static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(weight), \
+                     M, K, num_experts, logits)
   if (x_dtype == kBF16) {
-    hipLaunchKernelGGL(marlin::route_logits_kernel<true>, grid, dim3(256), 0, s,
-                       static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(weight),
-                       M, K, num_experts, logits);
+    if (tile == 4) VQ_LOGITS(true, 4); else if (tile == 2) VQ_LOGITS(true, 2); else VQ_LOGITS(true, 1);
   } else {
-    hipLaunchKernelGGL(marlin::route_logits_kernel<false>, grid, dim3(256), 0, s,
-                       static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(weight),
-                       M, K, num_experts, logits);
+    if (tile == 4) VQ_LOGITS(false, 4); else if (tile == 2) VQ_LOGITS(false, 2); else VQ_LOGITS(false, 1);
   }
+#undef VQ_LOGITS
   if (int rc = check_launch("moe_route logits")) return rc;
   // four rows a workgroup, at most 64 Ki workgroups (rows beyond loop);
   // kPer = experts a lane
