@@ -52,7 +52,7 @@ def test_workspace_size_functions():
     assert lib.exl3_moe_workspace_size(4, 256, 200, 2, 0) == 0
     size = lib.exl3_moe_workspace_size(4, 256, 200, 2, 3)
     a, hpad, ipad = 8, 256, 256
-    ints = 4 + (a + 3) // 4 * 4 + 4 * a + a * max(hpad, ipad) // 128
+    ints = 4 + (a + 3) // 4 * 4 + 4 * a + a * max(hpad, ipad) // 128 + a
     assert size == a * (hpad + 3 * ipad) + ints
     assert lib.exl3_moe_workspace_size(4, 0, 200, 2, 3) == -1
 

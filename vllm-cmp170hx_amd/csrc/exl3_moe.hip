@@ -100,11 +100,12 @@ struct MoeLayout {
   __host__ __device__ int64_t act() const { return up() + assignments * ipad; }
   __host__ __device__ int64_t ints() const { return act() + assignments * ipad; }
   // int32 offsets from ints(): header[4], sorted[A rounded to 4], tasks[A] (int4),
-  // exponents[A][kmax / 128]
+  // exponents[A][kmax / 128], the local expert of each sorted row[A]
   __host__ __device__ int64_t sorted() const { return 4; }
   __host__ __device__ int64_t tasks() const { return 4 + (assignments + 3) / 4 * 4; }
   __host__ __device__ int64_t exps() const { return tasks() + 4 * assignments; }
-  __host__ __device__ int64_t total() const { return ints() + exps() + assignments * (kmax() / 128); }
+  __host__ __device__ int64_t row_experts() const { return exps() + assignments * (kmax() / 128); }
+  __host__ __device__ int64_t total() const { return ints() + row_experts() + assignments; }
 };
 
 // ---- 1. route ------------------------------------------------------------------
@@ -197,10 +198,11 @@ __global__ __launch_bounds__(kRoutePartThreads) void moe_route_count(Routing rou
   }
 }
 
-// sorted[first row of (part, expert) + place] = a for every routed slot a.
+// sorted[first row of (part, expert) + place] = a for every routed slot a,
+// and row_expert[that row] = its expert.
 __global__ __launch_bounds__(kRoutePartThreads) void moe_route_fill(int64_t assignments, int experts,
                                                                     const int* packed, const int* first,
-                                                                    int* sorted) {
+                                                                    int* sorted, int* row_expert) {
   const int64_t a0 = int64_t(blockIdx.x) * kRoutePart + threadIdx.x;
   const int* part_first = first + int64_t(blockIdx.x) * experts;
   int v[kRoutePartSlots];
@@ -211,7 +213,11 @@ __global__ __launch_bounds__(kRoutePartThreads) void moe_route_fill(int64_t assi
   }
 #pragma unroll
   for (int u = 0; u < kRoutePartSlots; ++u) {
-    if (v[u] >= 0) sorted[part_first[v[u] >> 16] + (v[u] & 0xffff)] = int(a0 + u * kRoutePartThreads);
+    if (v[u] >= 0) {
+      const int row = part_first[v[u] >> 16] + (v[u] & 0xffff);
+      sorted[row] = int(a0 + u * kRoutePartThreads);
+      row_expert[row] = v[u] >> 16;
+    }
   }
 }
 
@@ -225,8 +231,8 @@ __global__ __launch_bounds__(kRoutePartThreads) void moe_route_fill(int64_t assi
 // moe_route_fill writes the sorted list.
 __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int64_t assignments,
                                                            int task_rows, int tile_rows,
-                                                           int min_tile_tasks, int* table, int* hist,
-                                                           int parts) {
+                                                           int min_tile_tasks, int* table, int* row_expert,
+                                                           int* hist, int parts) {
   extern __shared__ int route_shared[];
   const int experts = int(routing.local_experts);
   int* count = route_shared;               // rows per expert
@@ -396,7 +402,11 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route(Routing routing, int6
   int* sorted = table + 4;
 #pragma unroll
   for (int u = 0; u < kRouteHeld; ++u) {
-    if (hv[u] >= 0) sorted[row_begin[hv[u] >> 16] + (hv[u] & 0xffff)] = int(tid + u * kRouteThreads);
+    if (hv[u] >= 0) {
+      const int row = row_begin[hv[u] >> 16] + (hv[u] & 0xffff);
+      sorted[row] = int(tid + u * kRouteThreads);
+      row_expert[row] = hv[u] >> 16;
+    }
   }
 }
 
@@ -478,7 +488,7 @@ __global__ __launch_bounds__(256) void moe_form(Routing routing, const void* x, 
   constexpr int kStride = kWaveRow ? 1 : 4;
   if (row >= table[0]) return;
   const int64_t a = table[4 + row];
-  const int64_t e = local_expert(routing, a);
+  const int64_t e = reinterpret_cast<const int*>(ws + lay.ints())[lay.row_experts() + row];
   const int64_t* ptrs = routing.ptrs + e * 9;
   // the tile experts' rows (sorted rows from the first tile task's first
   // on) feed only the tile GEMM, which reads the low parts unless it runs
@@ -1136,6 +1146,7 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
   if (any) {
     int* table = reinterpret_cast<int*>(workspace + lay.ints());
     const size_t route_lds = size_t(4 * local_experts + 2) * sizeof(int);
+    int* row_expert = table + lay.row_experts();
     if (assignments >= exl3::kRouteSplitMin) {
       // packed slots, then the parts' histograms, in the gate-result region
       // (A * ipad floats, ipad >= 128: room for A + parts * experts ints)
@@ -1146,15 +1157,16 @@ extern "C" int exl3_moe_out(const void* x, int x_dtype, int64_t rows, int64_t hi
                          size_t(local_experts) * sizeof(int), s, routing, assignments, packed, hist);
       if (int rc = check_launch("exl3 moe_route_count")) return rc;
       hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads), route_lds, s, routing,
-                         assignments, task_rows, tiles ? tile_rows : 0, min_tile_tasks, table, hist,
-                         int(parts));
+                         assignments, task_rows, tiles ? tile_rows : 0, min_tile_tasks, table, row_expert,
+                         hist, int(parts));
       if (int rc = check_launch("exl3 moe_route")) return rc;
       hipLaunchKernelGGL(exl3::moe_route_fill, dim3(unsigned(parts)), dim3(exl3::kRoutePartThreads), 0, s,
-                         assignments, int(local_experts), packed, hist, table + 4);
+                         assignments, int(local_experts), packed, hist, table + 4, row_expert);
       if (int rc = check_launch("exl3 moe_route_fill")) return rc;
     } else {
       hipLaunchKernelGGL(exl3::moe_route, dim3(1), dim3(exl3::kRouteThreads), route_lds, s, routing,
-                         assignments, task_rows, tiles ? tile_rows : 0, min_tile_tasks, table, nullptr, 0);
+                         assignments, task_rows, tiles ? tile_rows : 0, min_tile_tasks, table, row_expert,
+                         nullptr, 0);
       if (int rc = check_launch("exl3 moe_route")) return rc;
     }
     auto tile = [&](int projection, int64_t kp, int64_t np, int64_t in_off, int64_t out_off) {
