@@ -134,7 +134,8 @@ int exl3_linear_out(const void* x, int x_dtype, int64_t rows, int64_t x_cols,
  * hpad / ipad the hidden / intermediate sizes rounded up to 128,
  * A * (hpad + 3 * ipad) (activations, gate, up and down-input rows) plus the int32
  * routing table (4 + A rounded up to 4 + 4 A) plus A * max(hpad, ipad) / 128
- * int32 scale exponents; 0 when local_experts is 0; -1 (with an error
+ * int32 scale exponents plus A int32 experts of the sorted rows; 0 when
+ * local_experts is 0; -1 (with an error
  * message) for negative counts or nonpositive sizes.
  * Replaces _exl3_C::moe_workspace_size and moe_workspace_size_v2
  * (csrc/exl3/moe.cu:304-317, csrc/exl3/moe_v2.cu:2041-2061).
