@@ -28,7 +28,8 @@ def _bf16(rng, shape, scale=1.0):
 @pytest.mark.parametrize("M_,E,K,topk,bs,scoring", [
     (1, 288, 4096, 8, 8, "sigmoid"), (4, 288, 4096, 8, 8, "sigmoid"), (64, 288, 4096, 8, 16, "sigmoid"),
     (33, 128, 2048, 8, 8, "softmax"), (300, 64, 1024, 6, 32, "softmax"), (7, 257, 7168, 8, 8, "sigmoid"),
-    (2048, 288, 4096, 8, 16, "sigmoid")])
+    (2048, 288, 4096, 8, 16, "sigmoid"), (8, 256, 1024, 8, 8, "sigmoid"), (100, 512, 1024, 8, 16, "sigmoid"),
+    (5, 1024, 1024, 8, 16, "softmax"), (3, 40, 512, 4, 8, "softmax")])
 def test_route_matches_oracle(device, M_, E, K, topk, bs, scoring):
     from vllm_mi355x.kernels.moe import route
     print(f"moe_route M={M_} E={E} K={K} topk={topk} bs={bs} {scoring}", flush=True)
