@@ -248,7 +248,7 @@ def test_linear_fused_and_separate_finish_agree(ops, device, shape, rows):
 
 @pytest.mark.parametrize("blocks,groups", [(1, 1), (2, 1), (4, 1), (8, 1), (1, 4), (2, 4), (4, 4)])
 @pytest.mark.parametrize("bits_x2,codebook", [(8, 2), (4, 1), (3, 2), (2, 2), (10, 2), (16, 1)])
-@pytest.mark.parametrize("rows", [1, 3, 8])
+@pytest.mark.parametrize("rows", [1, 3, 6, 8])
 def test_linear_workgroup_shapes_match_oracle(ops, device, blocks, groups, bits_x2, codebook, rows):
     """Every (blocks per group, groups per workgroup) shape of the small-M
     kernel, forced through the tuning switches: same bar as the automatic
@@ -270,6 +270,30 @@ def test_linear_workgroup_shapes_match_oracle(ops, device, blocks, groups, bits_
         _native.check(lib.exl3_set_gemv_groups(0))
     want = O.linear_out(x, code, trellis, suh, svh, bits_x2, codebook, logical_out, O.FP32)
     _assert_fp32_close(_out_np(got), want, f"blocks={blocks} groups={groups} bits_x2={bits_x2}")
+
+
+@pytest.mark.parametrize("rows", [5, 8])
+@pytest.mark.parametrize("blocks", [2, 4])
+def test_linear_row_form_equals_task_form(ops, device, rows, blocks):
+    """The 8-row kernel forms its activations eight inputs a lane (16-byte
+    loads) when logical_in is a multiple of 8, and two inputs a lane per
+    (block, row) otherwise.  The same inputs through both (logical_in 2040,
+    and 2041 with a zero last input) give the same outputs, bitwise."""
+    from vllm_mi355x import _native
+    rng = np.random.default_rng(40 + rows + blocks)
+    trellis, suh, svh = random_matrix(rng, 2048, 384, 8, scales="test")
+    x, code = random_acts(rng, rows, 2040, "fp16")
+    x_pad = np.concatenate([x, np.zeros((rows, 1), x.dtype)], 1)
+    lib = _native.load()
+    try:
+        _native.check(lib.exl3_set_gemv_blocks(blocks))
+        a = _run_linear(ops, device, trellis, suh, svh, x, code, 8, 2, 380, torch.float32)
+        b = _run_linear(ops, device, trellis, suh, svh, x_pad, code, 8, 2, 380, torch.float32)
+    finally:
+        _native.check(lib.exl3_set_gemv_blocks(0))
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    want = O.linear_out(x, code, trellis, suh, svh, 8, 2, 380, O.FP32)
+    _assert_fp32_close(_out_np(a), want, f"rows={rows} blocks={blocks}")
 
 
 @pytest.mark.parametrize("offset_bytes", [2, 4, 8])

@@ -360,6 +360,12 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
   constexpr int kActHalves = kSteps * 4 * kCols * 8;      // B operands of the range
   constexpr int kTasks = kBlocks * kRows;                 // (block, row) forming tasks
   constexpr int kFormTasks = (kTasks + 3) / 4;            // per wavefront
+  // 8-row kernels over pairs of blocks form four tasks a wavefront at a
+  // time, one per 16-lane row, eight inputs a lane (h128_rows: the same
+  // additions in the same order as h128_wave, so the same operands): pass p
+  // of wavefront w is block 2 p + w / 2, rows 4 (w & 1) .. + 3
+  constexpr bool kRowForm = kRows == 8 && kGroups == 1 && kBlocks % 2 == 0;
+  constexpr int kPasses = kRowForm ? kBlocks / 2 : 1;
   // LDS stream: loads of the range, loads in flight per wavefront
   constexpr int kP = G::kStepsPerLoad;
   constexpr int kLoads = kSteps / kP;
@@ -413,9 +419,29 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
   const uint16_t* xs = static_cast<const uint16_t*>(a.x);
   const __amdgpu_buffer_rsrc_t suh_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.suh), 0, int(2 * a.logical_in), 0x00020000);
+  //    8-row kernels whose input rows are whole 16-byte chunks (logical_in
+  //    a multiple of 8) take the row form: a lane's eight inputs, all below
+  //    logical_in or all past it (zeros), in one 16-byte load each of x and
+  //    suh.  (Eight 2-byte loads a lane, each spread over four rows, were
+  //    slower than the per-task form, which the others keep.)
+  const bool row_form = kRowForm && (a.logical_in & 7) == 0;
   uint32_t xv[kFormTasks][2], sv[kFormTasks][2];
+  u32x4_t xq[kPasses], sq[kPasses];  // row form: a lane's eight inputs of each pass
+  const int rl = lane & 15;          // row form: the lane's place in its 16-lane row
+  if (row_form) {
 #pragma unroll
-  for (int f = 0; f < kFormTasks; ++f) {
+    for (int p = 0; p < kPasses; ++p) {
+      const int b = 2 * p + (wc >> 1);
+      const int row = min(4 * (wc & 1) + (lane >> 4), a.rows - 1);
+      const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(xs + int64_t(row) * a.logical_in), 0, int(2 * a.logical_in), 0x00020000);
+      const int k_0 = int(k0) + 128 * b + 8 * rl;
+      sq[p] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(suh_rsrc, 2 * k_0, 0, 0));
+      xq[p] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, 2 * k_0, 0, 0));
+    }
+  }
+#pragma unroll
+  for (int f = 0; f < kFormTasks && !row_form; ++f) {
     const int t = wc + 4 * f;
     const int b = min(t / kRows, kBlocks - 1);
     const int row = vq::uniform(min(t % kRows, a.rows - 1));
@@ -525,8 +551,31 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
   //    stores bypass the compiler's LDS-DMA tracking (they never touch a
   //    ring slot), so they do not wait for the trellis loads in flight.
   float fv[kFormTasks][2];
+  float fr[kPasses][8];
+  if (row_form) {
 #pragma unroll
-  for (int f = 0; f < kFormTasks; ++f) {
+    for (int p = 0; p < kPasses; ++p) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t xw = xq[p][j >> 1], sw = sq[p][j >> 1];
+        fr[p][j] = u16_act(uint16_t(xw >> (16 * (j & 1))), a.x_dtype) * vq::f16_to_f32(uint16_t(sw >> (16 * (j & 1))));
+      }
+      vq::h128_rows(fr[p], rl);
+      float mx = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(fr[p][j]));
+      mx = fmaxf(mx, vq::xor_lanes<1>(mx, lane));
+      mx = fmaxf(mx, vq::xor_lanes<2>(mx, lane));
+      mx = fmaxf(mx, vq::xor_lanes<4>(mx, lane));
+      mx = fmaxf(mx, vq::xor_lanes<8>(mx, lane));
+      if (rl == 0) {
+        vq::lds_store_b32(vq::lds_address(&block_max[0][2 * p + (wc >> 1)][4 * (wc & 1) + (lane >> 4)]),
+                          __builtin_bit_cast(uint32_t, mx));
+      }
+    }
+  }
+#pragma unroll
+  for (int f = 0; f < kFormTasks && !row_form; ++f) {
     const int t = wc + 4 * f;
     fv[f][0] = fv[f][1] = 0.0f;
     if (t < kTasks) {
@@ -561,6 +610,33 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
       return ((step * 4 + gg) * kCols) * 8 + slot;
     };
     const uint32_t gact = vq::lds_address(act + grp * kActHalves);
+    if (row_form) {
+      // inputs 8 rl + 2 i, + 1 of a block: adjacent halves of group i of
+      // step rl / 4, at slot 4 ((rl & 3) >> 1) + 2 (rl & 1): one dword each
+      const int s0 = 4 * ((rl & 3) >> 1) + 2 * (rl & 1);
+#pragma unroll
+      for (int p = 0; p < kPasses; ++p) {
+        const int b = 2 * p + (wc >> 1);
+        const int r = 4 * (wc & 1) + (lane >> 4);
+        const int e = row_exponent(r);
+        const uint32_t base = gact + 2 * uint32_t(b * 4 * 4 * kCols * 8 + (2 * r) * 8);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float t0 = ldexpf(fr[p][2 * i], e);
+          const float t1 = ldexpf(fr[p][2 * i + 1], e);
+          const _Float16 hi0 = _Float16(t0), hi1 = _Float16(t1);
+          const _Float16 lo0 = _Float16(t0 - float(hi0)), lo1 = _Float16(t1 - float(hi1));
+          const uint32_t hw = uint32_t(__builtin_bit_cast(uint16_t, hi0)) |
+                              (uint32_t(__builtin_bit_cast(uint16_t, hi1)) << 16);
+          const uint32_t lw = uint32_t(__builtin_bit_cast(uint16_t, lo0)) |
+                              (uint32_t(__builtin_bit_cast(uint16_t, lo1)) << 16);
+          const uint32_t h = uint32_t(((rl >> 2) * 4 + i) * kCols * 8 + s0);
+          vq::lds_store_b32(base + 2 * h, hw);
+          vq::lds_store_b32(base + 2 * (h + 8), lw);
+        }
+      }
+      return;
+    }
     const int h0 = slot_of(lane);
     const int h1 = slot_of(lane + 64);
 #pragma unroll
