@@ -276,9 +276,10 @@ def test_linear_workgroup_shapes_match_oracle(ops, device, blocks, groups, bits_
 @pytest.mark.parametrize("blocks", [2, 4])
 def test_linear_row_form_equals_task_form(ops, device, rows, blocks):
     """The 8-row kernel forms its activations eight inputs a lane (16-byte
-    loads) when logical_in is a multiple of 8, and two inputs a lane per
-    (block, row) otherwise.  The same inputs through both (logical_in 2040,
-    and 2041 with a zero last input) give the same outputs, bitwise."""
+    loads) when logical_in is a multiple of 8 and x and suh are 16-byte
+    aligned, and two inputs a lane per (block, row) otherwise.  The same
+    inputs through both (logical_in 2040; 2041 with a zero last input; x at
+    a 2-byte offset) give the same outputs, bitwise."""
     from vllm_mi355x import _native
     rng = np.random.default_rng(40 + rows + blocks)
     trellis, suh, svh = random_matrix(rng, 2048, 384, 8, scales="test")
@@ -289,9 +290,20 @@ def test_linear_row_form_equals_task_form(ops, device, rows, blocks):
         _native.check(lib.exl3_set_gemv_blocks(blocks))
         a = _run_linear(ops, device, trellis, suh, svh, x, code, 8, 2, 380, torch.float32)
         b = _run_linear(ops, device, trellis, suh, svh, x_pad, code, 8, 2, 380, torch.float32)
+        flat = torch.zeros(rows * 2040 + 1, dtype=torch.float16, device=device)
+        x_odd = flat[1:].view(rows, 2040)
+        x_odd.copy_(_to_torch_act(x, code, device))
+        assert x_odd.data_ptr() % 16 == 2
+        c = torch.empty(rows, 380, dtype=torch.float32, device=device)
+        ws = torch.empty(ops.linear_workspace_size(rows, suh.size, svh.size), dtype=torch.float32,
+                         device=device)
+        ops.linear_out(x_odd, _dev(trellis, device), _dev(suh, device), _dev(svh, device), 8, 2, 2040, 380,
+                       c, ws)
+        torch.cuda.synchronize()
     finally:
         _native.check(lib.exl3_set_gemv_blocks(0))
     assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    assert torch.equal(a.view(torch.int32), c.view(torch.int32))
     want = O.linear_out(x, code, trellis, suh, svh, 8, 2, 380, O.FP32)
     _assert_fp32_close(_out_np(a), want, f"rows={rows} blocks={blocks}")
 

@@ -420,11 +420,13 @@ __global__ __launch_bounds__(kThreads * kGroups) void gemv_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t suh_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.suh), 0, int(2 * a.logical_in), 0x00020000);
   //    8-row kernels whose input rows are whole 16-byte chunks (logical_in
-  //    a multiple of 8) take the row form: a lane's eight inputs, all below
-  //    logical_in or all past it (zeros), in one 16-byte load each of x and
-  //    suh.  (Eight 2-byte loads a lane, each spread over four rows, were
-  //    slower than the per-task form, which the others keep.)
-  const bool row_form = kRowForm && (a.logical_in & 7) == 0;
+  //    a multiple of 8, x and suh 16-byte aligned) take the row form: a
+  //    lane's eight inputs, all below logical_in or all past it (zeros), in
+  //    one 16-byte load each of x and suh.  (Eight 2-byte loads a lane, each
+  //    spread over four rows, were slower than the per-task form, which the
+  //    others keep.)
+  const bool row_form = kRowForm && (a.logical_in & 7) == 0 &&
+                        ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.suh)) & 15) == 0;
   uint32_t xv[kFormTasks][2], sv[kFormTasks][2];
   u32x4_t xq[kPasses], sq[kPasses];  // row form: a lane's eight inputs of each pass
   const int rl = lane & 15;          // row form: the lane's place in its 16-lane row
