@@ -245,6 +245,30 @@ def test_moe_deterministic_and_workspace_independent(ops, device):
     assert torch.equal(first.view(torch.int16), third.view(torch.int16))
 
 
+def test_moe_input_at_two_byte_offset(ops, device):
+    """The forming reads x rows with 16-byte loads at any alignment: x at a
+    2-byte offset (a view into a larger buffer) gives the aligned call's
+    outputs bitwise, on the GEMV path and with the forming one wavefront a
+    row (8192 or more routed slots)."""
+    rng = np.random.default_rng(17)
+    hidden, intermediate, experts, topk = 512, 256, 8, 8
+    layer = Layer(rng, experts, hidden, intermediate, [(6, 2)], device, scales="sign")
+    for rows in (24, 1100):
+        ids = np.stack([rng.permutation(experts)[:topk] for _ in range(rows)])
+        weights = rng.random((rows, topk)).astype(np.float32)
+        _, _, x = _acts(rng, rows, hidden, "bf16", device)
+        flat = torch.zeros(rows * hidden + 1, dtype=x.dtype, device=device)
+        x_odd = flat[1:].view(rows, hidden)
+        x_odd.copy_(x)
+        assert x_odd.data_ptr() % 16 == 2
+        args = (_dev(ids, device), _dev(weights, device), layer,
+                torch.arange(experts, device=device), intermediate)
+        aligned = _run(ops, x, *args, bits_x2=6)
+        shifted = _run(ops, x_odd, *args, bits_x2=6)
+        assert torch.isfinite(aligned.float()).all()
+        assert torch.equal(aligned.view(torch.int16), shifted.view(torch.int16)), f"rows={rows}"
+
+
 def test_moe_fully_masked_and_empty(ops, device):
     rng = np.random.default_rng(3)
     hidden, intermediate, experts, topk, rows = 256, 128, 2, 2, 5
