@@ -1331,11 +1331,19 @@ __device__ __forceinline__ void align_block_onepass(
   __syncthreads();
   int run = 0;  // this thread's expert's padded size
   if (tid < experts) {
+    // a round's 16 counts read together, then written back as prefixes (a
+    // read after the previous entry's write would wait for it: one LDS round
+    // trip per entry)
     int acc = 0;
-    for (int k = 0; k < rounds * 16; ++k) {
-      const int t = wcnt[k * experts + tid];
-      wcnt[k * experts + tid] = acc;
-      acc += t;
+    for (int c = 0; c < rounds; ++c) {
+      int t[16];
+#pragma unroll
+      for (int w = 0; w < 16; ++w) t[w] = wcnt[(c * 16 + w) * experts + tid];
+#pragma unroll
+      for (int w = 0; w < 16; ++w) {
+        wcnt[(c * 16 + w) * experts + tid] = acc;
+        acc += t[w];
+      }
     }
     count[tid] = acc;
     run = (acc + bs - 1) / bs * bs;
@@ -1359,19 +1367,13 @@ __device__ __forceinline__ void align_block_onepass(
     for (int64_t p = int64_t(start[tid]) + count[tid]; p < p1; ++p) sorted[p] = int32_t(numel);
   }
   for (int64_t p = total + tid; p < sorted_size; p += kAlignThreads) sorted[p] = int32_t(numel);
-  for (int64_t b = tid; b < blocks; b += kAlignThreads) {
-    int owner = -1;
-    if (b < total / bs) {
-      // last expert whose first block is at or before b
-      int lo = 0, hi = experts;
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (start[mid] / bs <= b) lo = mid; else hi = mid;
-      }
-      owner = lo;
-    }
-    eids[b] = owner;
+  // each expert's blocks name it (an expert of no rows owns none); blocks
+  // past the padded total name -1
+  if (tid < experts) {
+    const int b1 = min(int64_t(start[tid] + run) / bs, blocks);
+    for (int b = start[tid] / bs; b < b1; ++b) eids[b] = tid;
   }
+  for (int64_t b = total / bs + tid; b < blocks; b += kAlignThreads) eids[b] = -1;
 }
 
 // One workgroup: counts, padded exclusive scan, expert per block, then the
@@ -2212,12 +2214,11 @@ int align_checks(int64_t numel, int64_t num_experts, int64_t block_size, int64_t
   const int64_t need = numel < num_experts ? std::min(numel * block_size, worst) : worst;
   if (sorted_numel < need) return fail("align: sorted_token_ids is smaller than numel + E (bs - 1)");
   if (expert_ids_numel * block_size < need) return fail("align: expert_ids too small");
-  // one pass (mode 2) over 2-8 rounds of rows when every row fits the
-  // registers and the per-round counts fit 64 KB of LDS (one round: the
-  // rounds below measured as fast); else per-wavefront counts when they
-  // fit, with the rest; else turns at the cursors
+  // one pass (mode 2) over 1-8 rounds of rows when every row fits the
+  // registers and the per-round counts fit 64 KB of LDS; else per-wavefront
+  // counts when they fit, with the rest; else turns at the cursors
   const int64_t rounds = (numel + kAlignThreads - 1) / kAlignThreads;
-  if (rounds >= 2 && rounds <= kAlignChunks && num_experts <= kAlignThreads &&
+  if (rounds >= 1 && rounds <= kAlignChunks && num_experts <= kAlignThreads &&
       (2 + 16 * rounds) * num_experts * int64_t(sizeof(int)) <= 65536) {
     wave_counts = 2;
     lds = size_t(2 + 16 * rounds) * size_t(num_experts) * sizeof(int);
