@@ -2,7 +2,8 @@
 bit-exact: the decoder's arithmetic is fully IEEE-specified (FP32 product,
 FP32 sum, FP16 and BF16 round-to-nearest, no contraction).  Cases follow the
 reference's decoder test (tests/models/qwen4_exp/test_exl3_ple_decode.py):
-three row layouts, owner shards, a NaN scale, and rows beyond one grid pass.
+three row layouts, owner shards, a NaN scale, and rows beyond one grid pass;
+and more layouts: every chunk width, a long row, many heads.
 """
 
 import numpy as np
@@ -40,6 +41,22 @@ def test_ple_decode_bit_exact(ops, device, bits, dim, sizes, owner):
     lo, hi = {"all": (0, rows), "lower": (0, middle), "upper": (middle, rows)}[owner]
     got = _decode(ops, device, packed, ids, bias, offsets, sizes, lo, hi, bits)
     assert np.array_equal(got, P.decode(packed, ids, bias, offsets, sizes, lo, hi, bits))
+
+
+# every chunk count: 1-bit (16 chunks, the first 15 channels wrapping), 2-,
+# 4-, 7-, 8-, 9-, 12- and 16-bit chunks, a 2560-channel row, 70 heads (two
+# ballots of 64) with an empty head among them
+MORE_LAYOUTS = [(1, 16, (7, 5)), (2, 64, (20, 11)), (4, 256, (33,)), (7, 32, (12, 3)),
+                (8, 96, (10, 10)), (9, 16, (4, 4)), (12, 4, (6,)), (16, 48, (9, 4, 6)),
+                (6, 2560, (40, 9)), (5, 16, tuple([2] * 40 + [0] + [1] * 29))]
+
+
+@pytest.mark.parametrize("bits,dim,sizes", MORE_LAYOUTS)
+def test_ple_decode_bit_exact_more_layouts(ops, device, bits, dim, sizes):
+    print(f"ple bits={bits} dim={dim} heads={len(sizes)}", flush=True)
+    packed, ids, bias, offsets, sizes, rows = synthetic(bits, dim, sizes, seed=100 + bits)
+    got = _decode(ops, device, packed, ids, bias, offsets, sizes, 0, rows, bits)
+    assert np.array_equal(got, P.decode(packed, ids, bias, offsets, sizes, 0, rows, bits))
 
 
 @pytest.mark.parametrize("bits,dim,sizes", LAYOUTS)

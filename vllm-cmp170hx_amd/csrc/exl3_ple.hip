@@ -7,16 +7,21 @@
 //
 // Channel c's 16-bit state takes bit m from ring bit ((c - m / bits) mod dim)
 // * bits + m % bits: the low `bits` state bits are channel c's own ring
-// chunk, the next `bits` the chunk of channel c - 1, and so on.  So the state
-// is the chunks of channels c, c - 1, c - 2, ... laid side by side from the
-// low bit, each chunk read from the ring with one 32-bit window.  The value
-// is the mul1 codebook in the PLE decoder's own arithmetic: FP32 product of
-// (1024 + byte sum) and the FP16 constant 0x1EEE, FP32 add of 0xC931,
-// rounded to FP16; then an FP32 product with the row scale and an FP32 add
-// of the head bias (each rounded, never contracted), rounded to BF16.
+// chunk, the next `bits` the chunk of channel c - 1, and so on.  The chunks
+// of channels c - chunks + 1 .. c lie side by side in the ring, at most 31
+// bits, so a lane reads them as one window (three halfword loads) and lays
+// them out in reverse chunk order; only the first chunks - 1 channels, whose
+// chunks wrap to the ring's end, read them one at a time.  The value is the
+// mul1 codebook in the PLE decoder's own arithmetic: the hash's byte sum in
+// one v_sad_u8, the FP32 product of (1024 + byte sum) and the FP16 constant
+// 0x1EEE, FP32 add of 0xC931, rounded to FP16; then an FP32 product with the
+// row scale and an FP32 add of the head bias (each rounded, never
+// contracted), rounded to BF16.
 //
-// One workgroup per row (a bounded grid strides over the rows); the row's
-// head and scale are found once, by the first thread.
+// One wavefront per row, four rows a workgroup (a bounded grid strides over
+// the rows), no LDS and no barrier: the wavefront finds the row's head by
+// counting, a ballot per 64 heads, the heads that start at or before the id.
+
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -30,37 +35,57 @@ namespace ple {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;  // rows a workgroup decodes at once
 
-// Last head starting at or before id, if id lies inside its vocabulary (gaps
-// and table-padding rows read nothing): reference ple.cu:51-75.
-__device__ int64_t head_of(int64_t id, const int64_t* offsets, const int64_t* sizes, int64_t heads) {
-  int64_t lo = 0, hi = heads;
-  while (lo < hi) {
-    const int64_t mid = lo + (hi - lo) / 2;
-    if (offsets[mid] <= id) lo = mid + 1; else hi = mid;
+// The head of row id: the last head starting at or before id (head offsets
+// ascend), when id lies inside its vocabulary (gaps and table-padding rows
+// read nothing); else -1.  The heads starting at or before id are counted
+// 64 at a time, one ballot each.
+__device__ int64_t head_of(int64_t id, const int64_t* offsets, const int64_t* sizes, int64_t heads,
+                           int lane) {
+  int64_t at_or_before = 0;
+  for (int64_t h0 = 0; h0 < heads; h0 += 64) {
+    const int64_t h = h0 + lane;
+    at_or_before += __builtin_popcountll(__ballot(h < heads && offsets[h] <= id));
   }
-  if (lo == 0) return -1;
-  const int64_t head = lo - 1;
+  if (at_or_before == 0) return -1;
+  const int64_t head = at_or_before - 1;
   const int64_t start = offsets[head];
   const int64_t size = sizes[head];
   return start >= 0 && size > 0 && id >= start && id - start < size ? head : -1;
 }
 
-// 32 ring bits starting at ring bit p, little-endian (ring bit p is bit 0):
-// words w = p / 16 and w + 1 of the ring (the second only when inside it).
-__device__ __forceinline__ uint32_t ring_window(const uint16_t* ring, int64_t words, int64_t p) {
+// Up to 32 ring bits from ring bit p on, little-endian (ring bit p lands in
+// bit 0): halfwords p / 16 .. p / 16 + 2 (those inside the ring).
+__device__ __forceinline__ uint32_t ring_bits(const uint16_t* ring, int64_t ring_words, int64_t p) {
   const int64_t w = p >> 4;
-  const uint32_t lo = ring[w];
-  const uint32_t hi = w + 1 < words ? ring[w + 1] : 0u;
-  return ((hi << 16) | lo) >> (p & 15);
+  uint64_t v = ring[w];
+  if (w + 1 < ring_words) v |= uint64_t(ring[w + 1]) << 16;
+  if (w + 2 < ring_words) v |= uint64_t(ring[w + 2]) << 32;
+  return uint32_t(v >> (p & 15));
+}
+
+// The state of channel c (see the file comment).
+__device__ __forceinline__ uint32_t channel_state(const uint16_t* ring, int64_t ring_words, int64_t dim,
+                                                  int bits, int chunks, int64_t c) {
+  const uint32_t mask = (1u << bits) - 1u;  // bits <= 16
+  uint32_t state = 0;
+  if (c >= chunks - 1) {
+    // chunk q (channel c - q) sits chunks - 1 - q chunks above the window's base
+    const uint32_t w = ring_bits(ring, ring_words, (c - chunks + 1) * bits);
+    for (int q = 0; q < chunks; ++q) state |= ((w >> ((chunks - 1 - q) * bits)) & mask) << (q * bits);
+  } else {
+    for (int q = 0; q < chunks; ++q) {
+      const int64_t from = c >= q ? c - q : dim - (q - c);
+      state |= (ring_bits(ring, ring_words, from * bits) & mask) << (q * bits);
+    }
+  }
+  return state & 0xffffu;
 }
 
 __device__ __forceinline__ float mul1_value(uint32_t state) {
-  const uint32_t p = state * 0x83DCD12Du;
-  const uint32_t t = (p & 255u) + ((p >> 8) & 255u) + ((p >> 16) & 255u) + (p >> 24);
-  const float k_inv = vq::f16_to_f32(0x1eee);
-  const float k_bias = vq::f16_to_f32(0xc931);
-  const float v = __fadd_rn(__fmul_rn(float(1024u + t), k_inv), k_bias);
+  const uint32_t t = __builtin_amdgcn_sad_u8(state * 0x83DCD12Du, 0u, 0u);  // byte sum of the hash
+  const float v = __fadd_rn(__fmul_rn(float(1024u + t), vq::f16_to_f32(0x1eee)), vq::f16_to_f32(0xc931));
   return float(_Float16(v));
 }
 
@@ -69,43 +94,25 @@ __global__ __launch_bounds__(kThreads) void ple_decode_kernel(
     const uint16_t* __restrict__ head_bias, const int64_t* __restrict__ offsets,
     const int64_t* __restrict__ sizes, int64_t rows, int64_t words, int64_t heads, int64_t dim,
     int64_t owner_lo, int64_t owner_hi, int bits, uint16_t* __restrict__ out) {
-  __shared__ int64_t row_head;
-  __shared__ float row_scale;
-  const int64_t ring_words = words - 1;
-  const uint32_t mask = (1u << bits) - 1u;  // bits <= 16
+  const int lane = threadIdx.x & 63;
   const int chunks = (16 + bits - 1) / bits;
-  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    if (threadIdx.x == 0) {
-      const int64_t id = ids[row];
-      int64_t head = -1;
-      float scale = 0.0f;
-      if (id >= 0 && id >= owner_lo && id < owner_hi) {
-        head = head_of(id, offsets, sizes, heads);
-        if (head >= 0) scale = vq::f16_to_f32(packed[row * words]);
-      }
-      row_head = head;
-      row_scale = scale;
+  const int64_t stride = int64_t(gridDim.x) * kWaves;
+  for (int64_t row = int64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
+    const int64_t id = ids[row];
+    const int64_t head =
+        id >= 0 && id >= owner_lo && id < owner_hi ? head_of(id, offsets, sizes, heads, lane) : -1;
+    uint16_t* dst = out + row * dim;
+    if (head < 0) {
+      for (int64_t c = lane; c < dim; c += 64) dst[c] = 0;  // BF16 zero: masked rows read nothing
+      continue;
     }
-    __syncthreads();
-    const int64_t head = row_head;
-    const float scale = row_scale;
+    const float scale = vq::f16_to_f32(packed[row * words]);
     const uint16_t* ring = packed + row * words + 1;
-    for (int64_t c = threadIdx.x; c < dim; c += kThreads) {
-      uint16_t v = 0;  // BF16 zero: masked rows read nothing
-      if (head >= 0) {
-        uint32_t state = 0;
-        for (int q = 0; q < chunks; ++q) {
-          const int64_t j = c >= q ? c - q : dim - (q - c);
-          state |= (ring_window(ring, ring_words, j * bits) & mask) << (q * bits);
-        }
-        const float scaled = __fmul_rn(mul1_value(state & 0xffffu), scale);
-        const float biased = __fadd_rn(scaled, vq::f16_to_f32(head_bias[head * dim + c]));
-        v = vq::f32_to_bf16(biased);
-      }
-      out[row * dim + c] = v;
+    const uint16_t* bias = head_bias + head * dim;
+    for (int64_t c = lane; c < dim; c += 64) {
+      const float scaled = __fmul_rn(mul1_value(channel_state(ring, words - 1, dim, bits, chunks, c)), scale);
+      dst[c] = vq::f32_to_bf16(__fadd_rn(scaled, vq::f16_to_f32(bias[c])));
     }
-    // the next row's head must not replace this one under a slower thread
-    __syncthreads();
   }
 }
 
@@ -152,7 +159,7 @@ extern "C" int exl3_ple_decode_out(const void* packed_rows, int64_t rows, int64_
     }
   }
   if (rows == 0) return kOk;
-  const unsigned blocks = unsigned(std::min<int64_t>(rows, 65535));
+  const unsigned blocks = unsigned(std::min<int64_t>((rows + ple::kWaves - 1) / ple::kWaves, 65535));
   hipLaunchKernelGGL(ple::ple_decode_kernel, dim3(blocks), dim3(ple::kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(packed_rows),
                      global_ids, static_cast<const uint16_t*>(head_bias), head_offsets,
