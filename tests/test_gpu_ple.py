@@ -44,11 +44,13 @@ def test_ple_decode_bit_exact(ops, device, bits, dim, sizes, owner):
 
 
 # every chunk count: 1-bit (16 chunks, the first 15 channels wrapping), 2-,
-# 4-, 7-, 8-, 9-, 12- and 16-bit chunks, a 2560-channel row, 70 heads (two
-# ballots of 64) with an empty head among them
+# 4-, 7-, 8-, 9-, 12- and 16-bit chunks, a 2560-channel row, 70 heads (one
+# search round, then a direct count) with an empty head among them, and 5000
+# heads (two rounds), a third of them empty
 MORE_LAYOUTS = [(1, 16, (7, 5)), (2, 64, (20, 11)), (4, 256, (33,)), (7, 32, (12, 3)),
                 (8, 96, (10, 10)), (9, 16, (4, 4)), (12, 4, (6,)), (16, 48, (9, 4, 6)),
-                (6, 2560, (40, 9)), (5, 16, tuple([2] * 40 + [0] + [1] * 29))]
+                (6, 2560, (40, 9)), (5, 16, tuple([2] * 40 + [0] + [1] * 29)),
+                (3, 16, tuple(([1, 2, 0] * 1700)[:5000]))]
 
 
 @pytest.mark.parametrize("bits,dim,sizes", MORE_LAYOUTS)

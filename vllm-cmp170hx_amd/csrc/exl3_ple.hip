@@ -19,8 +19,8 @@
 // contracted), rounded to BF16.
 //
 // One wavefront per row, four rows a workgroup (a bounded grid strides over
-// the rows), no LDS and no barrier: the wavefront finds the row's head by
-// counting, a ballot per 64 heads, the heads that start at or before the id.
+// the rows), no LDS and no barrier: the wavefront finds the row's head with
+// a 64-way search, one ballot a round.
 
 #include <hip/hip_runtime.h>
 
@@ -39,15 +39,27 @@ constexpr int kWaves = kThreads / 64;  // rows a workgroup decodes at once
 
 // The head of row id: the last head starting at or before id (head offsets
 // ascend), when id lies inside its vocabulary (gaps and table-padding rows
-// read nothing); else -1.  The heads starting at or before id are counted
-// 64 at a time, one ballot each.
+// read nothing); else -1.  The count of heads starting at or before id is
+// found by a 64-way search: each round the wavefront probes 64 evenly spaced
+// heads of the remaining range and one ballot keeps the stretch between the
+// last probe at or before id and the next; a range of at most 64 heads is
+// counted directly.
 __device__ int64_t head_of(int64_t id, const int64_t* offsets, const int64_t* sizes, int64_t heads,
                            int lane) {
-  int64_t at_or_before = 0;
-  for (int64_t h0 = 0; h0 < heads; h0 += 64) {
-    const int64_t h = h0 + lane;
-    at_or_before += __builtin_popcountll(__ballot(h < heads && offsets[h] <= id));
+  int64_t lo = 0, hi = heads;  // the count lies in [lo, hi]
+  while (hi - lo > 64) {
+    const int64_t step = (hi - lo + 63) / 64;
+    const int64_t probe = lo + lane * step;
+    const int k = __builtin_popcountll(__ballot(probe < hi && offsets[probe] <= id));
+    if (k == 0) {
+      hi = lo;
+    } else {
+      hi = std::min(lo + k * step, hi);
+      lo += (k - 1) * step + 1;
+    }
   }
+  const int64_t at_or_before =
+      lo + __builtin_popcountll(__ballot(lo + lane < hi && offsets[lo + lane] <= id));
   if (at_or_before == 0) return -1;
   const int64_t head = at_or_before - 1;
   const int64_t start = offsets[head];
