@@ -118,6 +118,22 @@ def _run_linear(ops, device, trellis, suh, svh, x, x_code, bits_x2, codebook, lo
     return out
 
 
+def test_linear_zero_rows(ops, device):
+    """An empty batch: linear_out returns with nothing to do, and the row
+    chunking (the reference's exl3_linear, ops.py:1455-1486) gives a
+    [0, logical_out] result."""
+    rng = np.random.default_rng(5)
+    trellis, suh, svh = random_matrix(rng, 256, 384, 8, scales="test")
+    t, u, v = _dev(trellis, device), _dev(suh, device), _dev(svh, device)
+    x = torch.empty(0, 250, dtype=torch.bfloat16, device=device)
+    out = torch.empty(0, 300, dtype=torch.bfloat16, device=device)
+    ws = torch.empty(ops.linear_workspace_size(1, 256, 384), dtype=torch.float32, device=device)
+    ops.linear_out(x, t, u, v, 8, 2, 250, 300, out, ws)
+    y = ops.exl3_linear(x, t, u, v, 8, 2, 300)
+    torch.cuda.synchronize()
+    assert y.shape == (0, 300) and y.dtype == torch.bfloat16
+
+
 @pytest.mark.parametrize("bits_x2,codebook", FORMATS)
 @pytest.mark.parametrize("rows", [1, 3, 8, 17])
 def test_linear_matches_oracle(ops, device, bits_x2, codebook, rows):
