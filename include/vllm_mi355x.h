@@ -267,8 +267,9 @@ int exl3_decode(const void* trellis, int64_t tiles_k, int64_t tiles_n, int64_t t
  * value is RN_bf16(RN32(RN16(RN32(RN32(1024 + bytesum(state * 0x83DCD12D)) *
  * fp16(0x1EEE)) + fp16(0xC931))) * scale) + head_bias[head][c]) for a row
  * whose global id lies in [owner_lo, owner_hi) and inside the vocabulary of
- * the last head starting at or before it (head_offsets / head_vocab_sizes
- * int64 [heads], head_bias fp16 [heads][dim]); every other row is zero.
+ * the last head starting at or before it (head_offsets ascending, as the
+ * reference's search also assumes; head_offsets / head_vocab_sizes int64
+ * [heads], head_bias fp16 [heads][dim]); every other row is zero.
  * Replaces _exl3_C::ple_decode_out (csrc/exl3/ple.cu:167-234; schema
  * csrc/exl3/module.cpp:30-32).
  */
